@@ -1,0 +1,153 @@
+/*
+ * pdscope_moe.h -- C-ABI of libpdscope_moe.so, the gfx950 MoE-layer path.
+ *
+ * Plain pointers and sizes only.  Every device pointer is a HIP device
+ * address (hipMalloc / torch CUDA tensor storage); `stream` is a hipStream_t
+ * (NULL = legacy default stream).  bf16 tensors are row-major arrays of
+ * 16-bit bfloat16 bit patterns.
+ *
+ * Return value: 0 on success, 1 for an invalid argument, 2 for a HIP runtime
+ * error; pdscope_last_error() then returns a thread-local message.  No entry
+ * point allocates device memory, synchronises the device or reads device
+ * memory on the host, so every launch sequence can be captured in a hipGraph.
+ * Work is stream-ordered on `stream`.
+ *
+ * Expert weights are addressed through a device table `slots[E]` of base
+ * pointers; expert e's block holds gate_proj [I,H], up_proj [I,H] and
+ * down_proj [H,I] back to back (bf16, row-major), the order of
+ * PROJECTIONS in expertbench/adapters/qwen.py:27 and of the per-expert
+ * copy in expertbench/executor.py:344-357.  Cache slots and demand staging
+ * slots are therefore addressed uniformly.
+ */
+#ifndef PDSCOPE_MOE_H
+#define PDSCOPE_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Message for the last failing call on this thread ("" if none). */
+const char *pdscope_last_error(void);
+
+/* Library version string. */
+const char *pdscope_version(void);
+
+/* Bytes of zero-initialised device workspace pdscope_route_topk needs
+ * (the caller zero-fills it once at allocation; the kernels leave it zeroed). */
+size_t pdscope_route_workspace_bytes(void);
+
+/*
+ * A1 router: replaces `route` (expertbench/adapters/qwen.py:140-152).
+ *   logits[t,e] = bf16(sum_h x[t,h] * gate[e,h])     (fp32 accumulation)
+ *   p = softmax(float(logits[t,:]) + bias)           (fp32; bias nullable)
+ *   ids[t,:]    = top-k experts by p, ties -> lower expert id, sorted
+ *   weights     = bf16(p_sel / sum(p_sel)) if normalize else bf16(p_sel)
+ * x [T,H] bf16, gate [E,H] bf16, bias [E] fp32 or NULL, logits [T,E] bf16,
+ * ids [T,k] int32, weights [T,k] bf16, probs [T,E] fp32 or NULL.
+ * Limits: E % 32 == 0, E <= 256, 1 <= k <= min(E, 16), H % 16 == 0.
+ * workspace: pdscope_route_workspace_bytes() zeroed bytes (used when T <= 8).
+ */
+int pdscope_route_topk(const void *x, const void *gate, const float *bias, int T, int H, int E,
+                       int k, int normalize, void *logits, int32_t *ids, void *weights,
+                       float *probs, void *workspace, void *stream);
+
+/*
+ * A2 gate-fallback predictor histogram: replaces the Counter over
+ * route(x, next_gate).selected (expertbench/pdscope_runtime.py:245-249).
+ * hist[e] = number of (t, slot) with ids[t,slot] == e; hist is overwritten.
+ */
+int pdscope_route_hist(const int32_t *ids, int n, int E, int32_t *hist, void *stream);
+
+/*
+ * A3 ragged grouping: replaces compact_expert_groups
+ * (expertbench/pdscope_runtime.py:16-39) and expert_groups
+ * (expertbench/adapters/qwen.py:155-174).
+ * Stable order over the slot-major flat index f = s*T + t, grouped by expert
+ * ascending.  Outputs: counts[E], offsets[E+1] (exclusive prefix sum),
+ * perm_token[T*k] (token of each grouped row), perm_pos[T*k] (= t*k + s) and
+ * row_of[T*k] (grouped row of position t*k+s).  Requires E <= 256.
+ */
+int pdscope_pack(const int32_t *ids, int T, int k, int E, int32_t *counts, int32_t *offsets,
+                 int32_t *perm_token, int32_t *perm_pos, int32_t *row_of, void *stream);
+
+/*
+ * Tile schedule for pdscope_swiglu_grouped over a subset of experts:
+ * tile_start[i] = sum_{j<i} ceil(counts[sel[j]] / block_m), i = 0..nsel.
+ * block_m is the row tile the grouped call will use (see
+ * pdscope_grouped_block_m).
+ */
+int pdscope_schedule(const int32_t *counts, const int32_t *sel, int nsel, int block_m,
+                     int32_t *tile_start, void *stream);
+
+/* Row tile (32, 64 or 128) pdscope_swiglu_grouped uses for `rows_hint`
+ * average rows per selected expert. */
+int pdscope_grouped_block_m(int rows_hint);
+
+/*
+ * A4 grouped SwiGLU for prefill: replaces expert_forward
+ * (expertbench/adapters/qwen.py:87-90) over every selected expert, as
+ * launched per expert by ExpertExecutor.gpu (expertbench/executor.py:454-488).
+ * For each selected expert e and each grouped row r in
+ * [offsets[e], offsets[e+1]):
+ *   g,u  = bf16(x[perm_token[r]] . gate_e^T), bf16(x[perm_token[r]] . up_e^T)
+ *   h[r] = bf16(bf16(silu(g)) * u)                    (h_ws [T*k, I] bf16)
+ *   y[r] = bf16(h[r] . down_e^T)                      (y [T*k, H] bf16)
+ * bf16 MFMA with fp32 accumulation.  max_tiles bounds sum ceil(m_e/block_m)
+ * (e.g. ceil(rows/block_m) + nsel); tiles beyond tile_start[nsel] exit.
+ * Limits: H % 64 == 0, I % 64 == 0.
+ */
+int pdscope_swiglu_grouped(const void *x, const int32_t *perm_token, const int32_t *offsets,
+                           const int32_t *sel, int nsel, const int32_t *tile_start,
+                           int max_tiles, int block_m, const void *const *slots, int H, int I,
+                           void *h_ws, void *y, void *stream);
+
+/*
+ * A8 fused weighted merge: replaces the index_add_ merge
+ * (expertbench/pdscope_runtime.py:450-469).
+ *   out[t,:] = bf16( add_in[t,:] + sum_s w[t,s] * y[row_of[t*k+s],:] )
+ * summed in fp32 in slot order s = 0..k-1 and rounded once; deterministic.
+ * add_in (nullable) is added unweighted (shared experts).
+ */
+int pdscope_merge(const void *y, const int32_t *row_of, const void *w, int T, int k, int H,
+                  const void *add_in, void *out, void *stream);
+
+/*
+ * A4+A8 for one decode token (T == 1): replaces the per-expert decode
+ * submissions (expertbench/pdscope_runtime.py:326-350, executor.py:454-488,
+ * including the resident-graph replay of executor.py:113-138) and the merge.
+ *   h_s  = bf16(bf16(silu(bf16(x.gate_s^T))) * bf16(x.up_s^T))  (h_ws [k,I])
+ *   out  = bf16( sum_s w[s] * bf16(h_s . down_s^T) )            (out [H])
+ * for the k experts ids[0..k). Streaming GEMV, weights read once.
+ * Limits: H % 512 == 0, I % 8 == 0, k <= 16.
+ */
+int pdscope_swiglu_decode(const void *x, const int32_t *ids, const void *w, int k,
+                          const void *const *slots, int H, int I, void *h_ws, void *out,
+                          void *stream);
+
+/*
+ * A7 demand staging: replaces the three per-projection non_blocking copies
+ * (expertbench/executor.py:341-363).  One hipMemcpyAsync of `bytes` from
+ * page-locked host memory into a cache or staging slot on `stream`, then
+ * hipEventRecord(event) when event != NULL.
+ */
+int pdscope_stage_expert(void *dst_slot, const void *pinned_src, size_t bytes, void *event,
+                         void *stream);
+
+/*
+ * A9 native CPU-group tail, GPU half: replaces the stage + index_add_ of
+ * finish_and_merge / submit_and_merge (native/native_layer_dispatch.cpp:83-88,
+ * 124-129).  Copies host block [rows, row_bytes] into device scratch, then
+ * for r = 0..rows-1 in order: out[tokens[r],:] += bf16(scratch[r,:]*weights[r])
+ * with bf16 accumulation (one valid order of the reference's index_add_).
+ * tokens int64 [rows], weights bf16 [rows], out bf16 [*, row_bytes/2].
+ */
+int pdscope_stage_merge(const void *host_block, int64_t rows, int64_t row_bytes, void *scratch,
+                        void *out, const int64_t *tokens, const void *weights, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PDSCOPE_MOE_H */

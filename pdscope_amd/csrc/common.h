@@ -1,0 +1,128 @@
+// Shared device helpers for the gfx950 MoE-layer kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#define PD_API extern "C" __attribute__((visibility("default")))
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+namespace pd {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- errors
+
+void set_error(const std::string &msg);
+int fail(int code, const std::string &msg);
+int check_launch(const char *what);
+
+enum : int { kOk = 0, kEInval = 1, kEHip = 2 };
+
+// ---------------------------------------------------------------- bf16
+
+__device__ __forceinline__ float bf2f(uint32_t h16) { return __uint_as_float(h16 << 16); }
+
+// round-to-nearest-even fp32 -> bf16 (same rule as torch's c10::BFloat16)
+__device__ __forceinline__ uint32_t f2bf(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+__device__ __forceinline__ float bf16_round(float f) { return bf2f(f2bf(f)); }
+
+// low / high bf16 of a packed 32-bit word, widened to fp32
+__device__ __forceinline__ float lo_bf(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi_bf(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// 16-byte streaming load that bypasses cache allocation (weights read once)
+__device__ __forceinline__ uint4 ld_nt(const void *p) {
+    u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// dot of 8 bf16 pairs packed in two uint4, accumulated in order into acc
+__device__ __forceinline__ float dot8(const uint4 a, const uint4 b, float acc) {
+    acc = __builtin_fmaf(lo_bf(a.x), lo_bf(b.x), acc);
+    acc = __builtin_fmaf(hi_bf(a.x), hi_bf(b.x), acc);
+    acc = __builtin_fmaf(lo_bf(a.y), lo_bf(b.y), acc);
+    acc = __builtin_fmaf(hi_bf(a.y), hi_bf(b.y), acc);
+    acc = __builtin_fmaf(lo_bf(a.z), lo_bf(b.z), acc);
+    acc = __builtin_fmaf(hi_bf(a.z), hi_bf(b.z), acc);
+    acc = __builtin_fmaf(lo_bf(a.w), lo_bf(b.w), acc);
+    acc = __builtin_fmaf(hi_bf(a.w), hi_bf(b.w), acc);
+    return acc;
+}
+
+// ---------------------------------------------------------------- wave ops
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+// sum inside each 32-lane half (offsets 16..1)
+__device__ __forceinline__ float half_sum(float v) {
+#pragma unroll
+    for (int off = 16; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+    return v;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        uint32_t lo = __shfl_xor((uint32_t)v, off, kWave);
+        uint32_t hi = __shfl_xor((uint32_t)(v >> 32), off, kWave);
+        uint64_t o = ((uint64_t)hi << 32) | lo;
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
+
+// exp(x) for x <= 0 with a fixed fp32 operation sequence: Cody-Waite
+// reduction x = n*ln2 + r with ln2 split into a 13-bit head and a tail, the
+// degree-7 Taylor polynomial of exp(r) in Horner form, and scaling by 2^n
+// built in the exponent field.  Results below 2^-125 flush to 0, so the value
+// never depends on the denormal mode.  The host-side checker evaluates the
+// same sequence, which makes routing probabilities reproducible bit for bit.
+__device__ __forceinline__ float route_expf(float x) {
+#pragma clang fp contract(off)
+    const float log2e = 0x1.715476p+0f;
+    const float ln2_hi = 0x1.62ep-1f;
+    const float ln2_lo = 0x1.0bfbe8p-15f;
+    float n = __builtin_rintf(x * log2e);
+    if (!(n >= -125.0f)) return 0.0f;
+    float r = __builtin_fmaf(-n, ln2_hi, x);
+    r = __builtin_fmaf(-n, ln2_lo, r);
+    float p = 0x1.a01a02p-13f;
+    p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
+    p = __builtin_fmaf(p, r, 0x1.111112p-7f);
+    p = __builtin_fmaf(p, r, 0x1.555556p-5f);
+    p = __builtin_fmaf(p, r, 0x1.555556p-3f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    float s = __uint_as_float((uint32_t)((int)n + 127) << 23);
+    return p * s;
+}
+
+__device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
+
+}  // namespace pd

@@ -1,0 +1,94 @@
+// K5: deterministic weighted merge back to token order, and the GPU half of
+// the native CPU-group tail.
+//   merge       restates the fused index_add_ merge of
+//               expertbench/pdscope_runtime.py:450-469 as a gather: each
+//               thread owns 8 output columns of one token and sums its k
+//               rows in fp32, slot order, rounding once (no atomics).
+//   stage_merge restates native/native_layer_dispatch.cpp:83-88 (copy the
+//               CPU block to device scratch, then index_add_ of
+//               scratch * weights into out) in bf16 arithmetic, rows in order.
+#include "common.h"
+
+namespace pd {
+
+__global__ __launch_bounds__(256) void merge_kernel(const uint16_t *__restrict__ y,
+                                                    const int32_t *__restrict__ row_of,
+                                                    const uint16_t *__restrict__ w, int T, int k, int H,
+                                                    const uint16_t *__restrict__ add_in,
+                                                    uint16_t *__restrict__ out) {
+    const int CH = H >> 3;
+    const int64_t total = (int64_t)T * CH;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        const int t = (int)(idx / CH), c = (int)(idx - (int64_t)t * CH);
+        float acc[8];
+        if (add_in) {
+            const uint4 v = reinterpret_cast<const uint4 *>(add_in + (size_t)t * H)[c];
+            acc[0] = lo_bf(v.x); acc[1] = hi_bf(v.x); acc[2] = lo_bf(v.y); acc[3] = hi_bf(v.y);
+            acc[4] = lo_bf(v.z); acc[5] = hi_bf(v.z); acc[6] = lo_bf(v.w); acc[7] = hi_bf(v.w);
+        } else {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) acc[q] = 0.0f;
+        }
+        for (int s = 0; s < k; ++s) {
+            const int r = row_of[(size_t)t * k + s];
+            const float ws = bf2f(w[(size_t)t * k + s]);
+            const uint4 v = reinterpret_cast<const uint4 *>(y + (size_t)r * H)[c];
+            acc[0] = __builtin_fmaf(ws, lo_bf(v.x), acc[0]);
+            acc[1] = __builtin_fmaf(ws, hi_bf(v.x), acc[1]);
+            acc[2] = __builtin_fmaf(ws, lo_bf(v.y), acc[2]);
+            acc[3] = __builtin_fmaf(ws, hi_bf(v.y), acc[3]);
+            acc[4] = __builtin_fmaf(ws, lo_bf(v.z), acc[4]);
+            acc[5] = __builtin_fmaf(ws, hi_bf(v.z), acc[5]);
+            acc[6] = __builtin_fmaf(ws, lo_bf(v.w), acc[6]);
+            acc[7] = __builtin_fmaf(ws, hi_bf(v.w), acc[7]);
+        }
+        uint4 o;
+        o.x = f2bf(acc[0]) | (f2bf(acc[1]) << 16);
+        o.y = f2bf(acc[2]) | (f2bf(acc[3]) << 16);
+        o.z = f2bf(acc[4]) | (f2bf(acc[5]) << 16);
+        o.w = f2bf(acc[6]) | (f2bf(acc[7]) << 16);
+        reinterpret_cast<uint4 *>(out + (size_t)t * H)[c] = o;
+    }
+}
+
+__global__ __launch_bounds__(256) void stage_merge_kernel(const uint16_t *__restrict__ scratch, int64_t rows,
+                                                          int H, const int64_t *__restrict__ tokens,
+                                                          const uint16_t *__restrict__ weights,
+                                                          uint16_t *__restrict__ out) {
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= H) return;
+    for (int64_t r = 0; r < rows; ++r) {
+        const size_t o = (size_t)tokens[r] * H + j;
+        const float prod = bf16_round(bf2f(scratch[(size_t)r * H + j]) * bf2f(weights[r]));
+        out[o] = (uint16_t)f2bf(bf2f(out[o]) + prod);
+    }
+}
+
+}  // namespace pd
+
+using namespace pd;
+
+PD_API int pdscope_merge(const void *y, const int32_t *row_of, const void *w, int T, int k, int H,
+                         const void *add_in, void *out, void *stream) {
+    if (!y || !row_of || !w || !out) return fail(kEInval, "merge: null pointer");
+    if (T < 1 || k < 1 || H < 8 || H % 8) return fail(kEInval, "merge: need T,k >= 1 and H % 8 == 0");
+    const int64_t total = (int64_t)T * (H / 8);
+    const int blocks = (int)std::min<int64_t>((total + 255) / 256, 65536);
+    merge_kernel<<<blocks, 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+        (const uint16_t *)y, row_of, (const uint16_t *)w, T, k, H, (const uint16_t *)add_in, (uint16_t *)out);
+    return check_launch("merge_kernel");
+}
+
+PD_API int pdscope_stage_merge(const void *host_block, int64_t rows, int64_t row_bytes, void *scratch,
+                               void *out, const int64_t *tokens, const void *weights, void *stream) {
+    if (!host_block || !scratch || !out || !tokens || !weights) return fail(kEInval, "stage_merge: null pointer");
+    if (rows < 1 || row_bytes < 2 || row_bytes % 2) return fail(kEInval, "invalid decode pack shape");
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    hipError_t err = hipMemcpyAsync(scratch, host_block, (size_t)rows * (size_t)row_bytes, hipMemcpyHostToDevice, s);
+    if (err != hipSuccess) return fail(kEHip, std::string("hipMemcpyAsync(stage): ") + hipGetErrorString(err));
+    const int H = (int)(row_bytes / 2);
+    stage_merge_kernel<<<(H + 255) / 256, 256, 0, s>>>((const uint16_t *)scratch, rows, H, tokens,
+                                                       (const uint16_t *)weights, (uint16_t *)out);
+    return check_launch("stage_merge_kernel");
+}

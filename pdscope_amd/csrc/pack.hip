@@ -1,0 +1,156 @@
+// K2: expert-sorted ragged packing.  Restates compact_expert_groups
+// (expertbench/pdscope_runtime.py:16-39): a stable sort of the slot-major
+// flat expert ids (f = s*T + t), i.e. a counting sort.
+//
+// One workgroup of 16 waves.  Each wave owns a contiguous segment of the
+// flat index space.  Pass 1 counts the segment per expert: a wave splits its
+// 64 ids into equal-id groups with 8 ballots (one per id bit); the lowest
+// lane of each group adds the group size to the wave's private LDS row.
+// A scan over (expert, wave) turns the counts into per-wave write bases.
+// Pass 2 repeats the ballots; a lane's grouped row is its wave base plus the
+// number of equal ids in lower lanes, so the order inside an expert stays
+// (slot, token) ascending.
+#include "common.h"
+
+namespace pd {
+
+constexpr int kPackWaves = 16;
+constexpr int kPackMaxE = 256;
+
+__device__ __forceinline__ uint64_t group_mask(int e, bool valid) {
+    uint64_t m = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+        uint64_t bb = __ballot((e >> b) & 1);
+        m &= ((e >> b) & 1) ? bb : ~bb;
+    }
+    return m;
+}
+
+// inclusive scan of one value per thread over the first 256 threads
+__device__ int block_scan256(int v, int *s_wsum) {
+    const int lane = lane_id(), wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        int o = __shfl_up(v, off, kWave);
+        if (lane >= off) v += o;
+    }
+    if (lane == 63 && wave < 4) s_wsum[wave] = v;
+    __syncthreads();
+    int add = 0;
+    for (int w = 0; w < wave && w < 4; ++w) add += s_wsum[w];
+    __syncthreads();
+    return v + add;
+}
+
+__global__ __launch_bounds__(1024) void pack_kernel(const int32_t *__restrict__ ids, int T, int k, int E,
+                                                    int32_t *__restrict__ counts, int32_t *__restrict__ offsets,
+                                                    int32_t *__restrict__ perm_token,
+                                                    int32_t *__restrict__ perm_pos,
+                                                    int32_t *__restrict__ row_of) {
+    __shared__ int32_t s_cnt[kPackWaves][kPackMaxE];
+    __shared__ int s_wsum[4];
+    const int n = T * k;
+    const int wave = threadIdx.x >> 6, lane = lane_id();
+    const int seg = ((n + kPackWaves * 64 - 1) / (kPackWaves * 64)) * 64;
+    const int beg = min(wave * seg, n), end = min(beg + seg, n);
+    const uint64_t below = (1ull << lane) - 1ull;
+
+    for (int e = lane; e < E; e += 64) s_cnt[wave][e] = 0;
+    __syncthreads();
+    for (int base = beg; base < end; base += 64) {
+        const int f = base + lane;
+        bool valid = f < end;
+        int e = 0;
+        if (valid) {
+            int s = f / T, t = f - s * T;
+            e = ids[(size_t)t * k + s];
+            valid = (e >= 0 && e < E);
+            if (!valid) e = 0;
+        }
+        const uint64_t m = group_mask(e, valid);
+        if (valid && !(m & below)) s_cnt[wave][e] += __popcll(m);
+    }
+    __syncthreads();
+    int tot = 0;
+    if (threadIdx.x < E)
+        for (int w = 0; w < kPackWaves; ++w) tot += s_cnt[w][threadIdx.x];
+    const int incl = block_scan256(threadIdx.x < 256 ? tot : 0, s_wsum);
+    if (threadIdx.x < E) {
+        const int e = threadIdx.x;
+        int run = incl - tot;
+        counts[e] = tot;
+        offsets[e] = run;
+        if (e == E - 1) offsets[E] = incl;
+        for (int w = 0; w < kPackWaves; ++w) {
+            int c = s_cnt[w][e];
+            s_cnt[w][e] = run;
+            run += c;
+        }
+    }
+    __syncthreads();
+    for (int base = beg; base < end; base += 64) {
+        const int f = base + lane;
+        bool valid = f < end;
+        int e = 0, s = 0, t = 0;
+        if (valid) {
+            s = f / T;
+            t = f - s * T;
+            e = ids[(size_t)t * k + s];
+            valid = (e >= 0 && e < E);
+            if (!valid) e = 0;
+        }
+        const uint64_t m = group_mask(e, valid);
+        if (valid) {
+            const int pos = s_cnt[wave][e] + __popcll(m & below);
+            perm_token[pos] = t;
+            perm_pos[pos] = t * k + s;
+            row_of[(size_t)t * k + s] = pos;
+            if (!(m & below)) s_cnt[wave][e] += __popcll(m);
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void schedule_kernel(const int32_t *__restrict__ counts,
+                                                       const int32_t *__restrict__ sel, int nsel, int bm,
+                                                       int32_t *__restrict__ tile_start) {
+    __shared__ int s_wsum[4];
+    __shared__ int s_carry;
+    if (threadIdx.x == 0) {
+        s_carry = 0;
+        tile_start[0] = 0;
+    }
+    __syncthreads();
+    for (int base = 0; base < nsel; base += 256) {
+        const int i = base + threadIdx.x;
+        const int tiles = i < nsel ? (counts[sel[i]] + bm - 1) / bm : 0;
+        const int incl = block_scan256(tiles, s_wsum);
+        if (i < nsel) tile_start[i + 1] = s_carry + incl;
+        __syncthreads();
+        if (threadIdx.x == 255) s_carry += incl;
+        __syncthreads();
+    }
+}
+
+}  // namespace pd
+
+using namespace pd;
+
+PD_API int pdscope_pack(const int32_t *ids, int T, int k, int E, int32_t *counts, int32_t *offsets,
+                        int32_t *perm_token, int32_t *perm_pos, int32_t *row_of, void *stream) {
+    if (!ids || !counts || !offsets || !perm_token || !perm_pos || !row_of)
+        return fail(kEInval, "pack: null pointer");
+    if (T < 1 || k < 1 || E < 1 || E > kPackMaxE) return fail(kEInval, "pack: need T,k >= 1 and 1 <= E <= 256");
+    if ((int64_t)T * k > (1ll << 30)) return fail(kEInval, "pack: T*k too large");
+    pack_kernel<<<1, 1024, 0, reinterpret_cast<hipStream_t>(stream)>>>(ids, T, k, E, counts, offsets,
+                                                                       perm_token, perm_pos, row_of);
+    return check_launch("pack_kernel");
+}
+
+PD_API int pdscope_schedule(const int32_t *counts, const int32_t *sel, int nsel, int block_m,
+                            int32_t *tile_start, void *stream) {
+    if (!counts || !sel || !tile_start || nsel < 0) return fail(kEInval, "schedule: bad arguments");
+    if (block_m != 32 && block_m != 64 && block_m != 128) return fail(kEInval, "schedule: block_m must be 32, 64 or 128");
+    schedule_kernel<<<1, 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(counts, sel, nsel, block_m, tile_start);
+    return check_launch("schedule_kernel");
+}

@@ -1,0 +1,203 @@
+"""torch-tensor front end of the gfx950 MoE-layer kernels.
+
+Each function checks shapes/dtypes/devices on the host, then calls the C-ABI
+(include/pdscope_moe.h) on the current HIP stream of the tensors' device.
+Tensors are borrowed; nothing here allocates unless an output is omitted.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+BF16 = torch.bfloat16
+
+
+def _p(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _need(t, name, dtype=None, ndim=None, device=None):
+    if not isinstance(t, torch.Tensor):
+        raise ValueError(f"{name} must be a tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must live on the GPU")
+    if device is not None and t.device != device:
+        raise ValueError(f"{name} is on {t.device}, expected {device}")
+    if dtype is not None and t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if ndim is not None and t.ndim != ndim:
+        raise ValueError(f"{name} must be {ndim}-D")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+_route_ws = {}
+
+
+def route_workspace(device) -> torch.Tensor:
+    """Zero-filled device scratch for the small-T router (kept zero by the kernel)."""
+    device = torch.device(device)
+    ws = _route_ws.get(device)
+    if ws is None:
+        n = int(_lib.load().pdscope_route_workspace_bytes())
+        ws = torch.zeros(n, dtype=torch.uint8, device=device)
+        _route_ws[device] = ws
+    return ws
+
+
+def slot_table(tensors, device) -> torch.Tensor:
+    """Device int64 table of expert base addresses (gate|up|down blocks)."""
+    return torch.tensor([t.data_ptr() for t in tensors], dtype=torch.int64, device=device)
+
+
+# --------------------------------------------------------------------- A1/A2
+
+def route_topk(x, gate, top_k, normalize, *, bias=None, capture_probabilities=False, out=None):
+    """K1 router.  Returns (logits bf16 [T,E], ids int32 [T,k], weights bf16 [T,k], probs|None)."""
+    _need(x, "inputs", BF16, 2)
+    _need(gate, "gate", BF16, 2, x.device)
+    T, H = x.shape
+    E = gate.shape[0]
+    if gate.shape[1] != H:
+        raise ValueError("router input shape/dtype mismatch")
+    if type(top_k) is not int or not 0 < top_k <= E:
+        raise ValueError("invalid routing parameters")
+    if bias is not None:
+        _need(bias, "bias", torch.float32, 1, x.device)
+        if bias.numel() != E:
+            raise ValueError("bias must have one entry per expert")
+    if out is None:
+        logits = torch.empty((T, E), dtype=BF16, device=x.device)
+        ids = torch.empty((T, top_k), dtype=torch.int32, device=x.device)
+        weights = torch.empty((T, top_k), dtype=BF16, device=x.device)
+    else:
+        logits, ids, weights = out
+    probs = torch.empty((T, E), dtype=torch.float32, device=x.device) if capture_probabilities else None
+    _lib.call("pdscope_route_topk", _p(x), _p(gate), _p(bias), T, H, E, top_k, int(bool(normalize)),
+              _p(logits), _p(ids), _p(weights), _p(probs), _p(route_workspace(x.device)), _stream(x.device))
+    return logits, ids, weights, probs
+
+
+def route_hist(ids, E, out=None):
+    _need(ids, "ids", torch.int32)
+    hist = out if out is not None else torch.empty(E, dtype=torch.int32, device=ids.device)
+    _lib.call("pdscope_route_hist", _p(ids), ids.numel(), E, _p(hist), _stream(ids.device))
+    return hist
+
+
+# --------------------------------------------------------------------- A3
+
+@dataclass
+class Packed:
+    counts: torch.Tensor      # int32 [E]
+    offsets: torch.Tensor     # int32 [E+1]
+    perm_token: torch.Tensor  # int32 [T*k]
+    perm_pos: torch.Tensor    # int32 [T*k]
+    row_of: torch.Tensor      # int32 [T*k]
+
+
+def pack(ids, E, out: Packed | None = None) -> Packed:
+    _need(ids, "ids", torch.int32, 2)
+    T, k = ids.shape
+    dev = ids.device
+    n = T * k
+    if out is None:
+        out = Packed(torch.empty(E, dtype=torch.int32, device=dev), torch.empty(E + 1, dtype=torch.int32, device=dev),
+                     torch.empty(n, dtype=torch.int32, device=dev), torch.empty(n, dtype=torch.int32, device=dev),
+                     torch.empty(n, dtype=torch.int32, device=dev))
+    _lib.call("pdscope_pack", _p(ids), T, k, E, _p(out.counts), _p(out.offsets), _p(out.perm_token),
+              _p(out.perm_pos), _p(out.row_of), _stream(dev))
+    return out
+
+
+def grouped_block_m(rows_hint: int) -> int:
+    return int(_lib.load().pdscope_grouped_block_m(int(rows_hint)))
+
+
+def schedule(counts, sel, block_m, out=None):
+    _need(counts, "counts", torch.int32, 1)
+    _need(sel, "sel", torch.int32, 1, counts.device)
+    tile_start = out if out is not None else torch.empty(sel.numel() + 1, dtype=torch.int32, device=counts.device)
+    _lib.call("pdscope_schedule", _p(counts), _p(sel), sel.numel(), block_m, _p(tile_start), _stream(counts.device))
+    return tile_start
+
+
+# --------------------------------------------------------------------- A4
+
+def swiglu_grouped(x, perm_token, offsets, sel, tile_start, max_tiles, block_m, slots, H, I, h_ws, y):
+    _need(x, "inputs", BF16, 2)
+    dev = x.device
+    for t, n in ((perm_token, "perm_token"), (offsets, "offsets"), (sel, "sel"), (tile_start, "tile_start")):
+        _need(t, n, torch.int32, 1, dev)
+    _need(slots, "slots", torch.int64, 1, dev)
+    _need(h_ws, "h_ws", BF16, None, dev)
+    _need(y, "y", BF16, None, dev)
+    if h_ws.numel() < perm_token.numel() * I or y.numel() < perm_token.numel() * H:
+        raise ValueError("h_ws / y workspaces are smaller than rows x I / rows x H")
+    _lib.call("pdscope_swiglu_grouped", _p(x), _p(perm_token), _p(offsets), _p(sel), sel.numel(), _p(tile_start),
+              int(max_tiles), int(block_m), _p(slots), H, I, _p(h_ws), _p(y), _stream(dev))
+    return y
+
+
+def swiglu_decode(x, ids, w, slots, H, I, h_ws, out):
+    _need(x, "inputs", BF16)
+    dev = x.device
+    _need(ids, "ids", torch.int32, None, dev)
+    _need(w, "weights", BF16, None, dev)
+    _need(slots, "slots", torch.int64, 1, dev)
+    _need(h_ws, "h_ws", BF16, None, dev)
+    _need(out, "out", BF16, None, dev)
+    k = ids.numel()
+    if x.numel() != H or out.numel() != H or w.numel() != k or h_ws.numel() < k * I:
+        raise ValueError("decode expects one token: x/out [H], ids/weights [k], h_ws >= k*I")
+    _lib.call("pdscope_swiglu_decode", _p(x), _p(ids), _p(w), k, _p(slots), H, I, _p(h_ws), _p(out), _stream(dev))
+    return out
+
+
+# --------------------------------------------------------------------- A8/A9
+
+def merge(y, row_of, w, out, add_in=None):
+    _need(w, "weights", BF16, 2)
+    dev = w.device
+    _need(y, "y", BF16, None, dev)
+    _need(row_of, "row_of", torch.int32, 1, dev)
+    _need(out, "out", BF16, 2, dev)
+    T, k = w.shape
+    H = out.shape[1]
+    if add_in is not None:
+        _need(add_in, "add_in", BF16, 2, dev)
+    _lib.call("pdscope_merge", _p(y), _p(row_of), _p(w), T, k, H, _p(add_in), _p(out), _stream(dev))
+    return out
+
+
+def stage_expert(dst, src, *, event=None, stream=None):
+    """One H2D copy of a pinned expert block into a device slot (+ event)."""
+    if src.device.type != "cpu" or not src.is_pinned():
+        raise ValueError("staging source must be page-locked host memory")
+    nbytes = src.numel() * src.element_size()
+    if dst.numel() * dst.element_size() < nbytes:
+        raise ValueError("staging slot is smaller than the expert block")
+    s = stream if stream is not None else torch.cuda.current_stream(dst.device)
+    ev = None if event is None else ctypes.c_void_p(event.cuda_event)
+    _lib.call("pdscope_stage_expert", _p(dst), _p(src), nbytes, ev, ctypes.c_void_p(s.cuda_stream))
+
+
+def stage_merge(host_block_ptr, rows, row_bytes, scratch, out, tokens, weights):
+    _need(scratch, "scratch", BF16, None)
+    dev = scratch.device
+    _need(out, "out", BF16, None, dev)
+    _need(tokens, "tokens", torch.int64, 1, dev)
+    _need(weights, "weights", BF16, None, dev)
+    if scratch.numel() * 2 != rows * row_bytes:
+        raise RuntimeError("scratch buffer must match the packed block")
+    _lib.call("pdscope_stage_merge", ctypes.c_void_p(int(host_block_ptr)), int(rows), int(row_bytes), _p(scratch),
+              _p(out), _p(tokens), _p(weights), _stream(dev))
+    return out

@@ -1,0 +1,48 @@
+"""Shared helpers for the GPU parity tests."""
+import numpy as np
+import torch
+
+
+def u16(t: torch.Tensor) -> np.ndarray:
+    """bf16 tensor -> numpy uint16 bit patterns (on the host)."""
+    return t.detach().contiguous().cpu().view(torch.int16).numpy().view(np.uint16).copy()
+
+
+def from_u16(a: np.ndarray, device="cuda") -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16).to(device)
+
+
+def ulp_diff_bf16(a, b):
+    a = a.astype(np.int32)
+    b = b.astype(np.int32)
+    fa = np.where(a & 0x8000, -(a & 0x7FFF), a & 0x7FFF)
+    fb = np.where(b & 0x8000, -(b & 0x7FFF), b & 0x7FFF)
+    return np.abs(fa - fb)
+
+
+def err_metrics(actual_f32: np.ndarray, ref_f32: np.ndarray):
+    """max rel err := max|d| / max|ref|; mean abs err; rel-L2 (benchmarks/harness.py:33-43)."""
+    d = actual_f32.astype(np.float64) - ref_f32.astype(np.float64)
+    ref = ref_f32.astype(np.float64)
+    return dict(max_rel=float(np.abs(d).max() / max(np.abs(ref).max(), 1e-30)),
+                mean_abs=float(np.abs(d).mean()),
+                rel_l2=float(np.linalg.norm(d) / max(np.linalg.norm(ref), 1e-30)))
+
+
+# tolerance of the layer path vs the reference expert path (bf16, fp32 accumulate)
+MAX_REL = 1e-2
+MEAN_ABS = 1e-3
+
+
+def logits_within_accumulation_error(kern, orc_exact, x_u16, gate_u16, bf16_to_f32):
+    """Kernel logits (fp32 accumulate, any order) vs exactly rounded logits:
+    every mismatch is one bf16 ulp, or within n*2^-24*sum|x*w| near zero."""
+    d = ulp_diff_bf16(kern, orc_exact)
+    if (d == 0).all():
+        return True, 0
+    xf = bf16_to_f32(x_u16).astype(np.float64)
+    gf = bf16_to_f32(gate_u16).astype(np.float64)
+    bound = xf.shape[1] * 2.0 ** -24 * (np.abs(xf) @ np.abs(gf).T)
+    diff = np.abs(bf16_to_f32(kern).astype(np.float64) - bf16_to_f32(orc_exact))
+    ok = bool(np.all((d <= 1) | (diff <= bound)))
+    return ok, int((d > 0).sum())

@@ -1,0 +1,288 @@
+"""GPU parity tests: every kernel through the C-ABI against the oracle.
+
+Routing ids, weights and probabilities must be bit-exact with the oracle
+applied to the kernel's own bf16 logits (the logits themselves are checked
+against the exactly rounded dot products within fp32 accumulation error).
+Grouping (counts, offsets, permutations, inverse map) must be bit-exact.
+Expert outputs and the merged layer must be within max rel err <= 1e-2 and
+mean abs err <= 1e-3 of the oracle's bf16 expert path.
+"""
+import numpy as np
+import pytest
+import torch
+
+from tests.gpu_helpers import (MAX_REL, MEAN_ABS, err_metrics, from_u16, logits_within_accumulation_error, u16,
+                               ulp_diff_bf16)
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module")
+def pd():
+    from pdscope_amd import ops, layer, synthetic
+    return ops, layer, synthetic
+
+
+@pytest.fixture(scope="module")
+def qwen(pd):
+    _, _, synthetic = pd
+    lay = synthetic.make_layer(**{k: v for k, v in synthetic.QWEN.items()}, device=DEV)
+    torch.cuda.synchronize()
+    return lay
+
+
+@pytest.fixture(scope="module")
+def qwen_host(qwen):
+    return dict(gate=u16(qwen.gate), experts=u16(qwen.experts))
+
+
+def _route_check(orc, ops, x, gate, k, normalize, bias=None):
+    logits, ids, w, probs = ops.route_topk(x, gate, k, normalize, bias=bias, capture_probabilities=True)
+    torch.cuda.synchronize()
+    lk, ik, wk, pk = u16(logits), ids.cpu().numpy(), u16(w), probs.cpu().numpy()
+    bias_np = None if bias is None else bias.cpu().numpy()
+    oi, ow, op = orc.route_from_logits(lk, k, normalize, bias_np, want_probs=True)
+    assert np.array_equal(ik, oi), "top-k ids differ from the oracle given identical logits"
+    assert np.array_equal(wk, ow), "routing weights differ from the oracle given identical logits"
+    assert np.array_equal(pk.view(np.uint32), op.view(np.uint32)), "softmax probabilities not bit-exact"
+    exact = orc.route_logits(u16(x), u16(gate))
+    ok, nmis = logits_within_accumulation_error(lk, exact, u16(x), u16(gate), orc.bf16_to_f32)
+    assert ok, "logit mismatch beyond fp32 accumulation error"
+    assert nmis <= max(2, 2e-3 * lk.size), f"{nmis} logit mismatches"
+    return lk, ik, wk
+
+
+@pytest.mark.parametrize("T", [1, 2, 5, 8])
+def test_route_small_T_qwen(orc, pd, qwen, T):
+    ops, _, synthetic = pd
+    x = synthetic.make_tokens(T, 2048, seed=100 + T)
+    _route_check(orc, ops, x, qwen.gate, 8, True)
+
+
+@pytest.mark.parametrize("T", [9, 33, 512, 4096])
+def test_route_mfma_qwen(orc, pd, qwen, T):
+    ops, _, synthetic = pd
+    x = synthetic.make_tokens(T, 2048, seed=200 + T)
+    _route_check(orc, ops, x, qwen.gate, 8, True)
+
+
+@pytest.mark.parametrize("T", [1, 4096])
+def test_route_zipf_bias(orc, pd, qwen, T):
+    ops, _, synthetic = pd
+    x = synthetic.make_tokens(T, 2048, seed=300 + T)
+    bias, _ = synthetic.zipf_bias(128, device=DEV)
+    _, ids, _ = _route_check(orc, ops, x, qwen.gate, 8, True, bias=bias)
+    if T > 1:
+        counts = np.bincount(ids.reshape(-1), minlength=128)
+        assert counts.max() > 4 * counts.mean()  # skew reached the routing
+
+
+@pytest.mark.parametrize("T", [1, 48, 1304])
+def test_route_deepseek_no_renorm(orc, pd, T):
+    ops, _, synthetic = pd
+    gen = torch.Generator(device=DEV).manual_seed(7)
+    gate = (torch.randn((64, 2048), generator=gen, device=DEV) * 0.02).to(torch.bfloat16)
+    x = synthetic.make_tokens(T, 2048, seed=400 + T)
+    _route_check(orc, ops, x, gate, 6, False)
+
+
+@pytest.mark.parametrize("T", [1, 64])
+def test_route_tie_heavy(orc, pd, T):
+    """Few distinct router rows and coarse activations: many exact logit ties."""
+    ops, _, _ = pd
+    gen = torch.Generator(device=DEV).manual_seed(11)
+    rows = (torch.randn((4, 256), generator=gen, device=DEV) * 0.02).to(torch.bfloat16)
+    gate = rows[torch.randint(0, 4, (128,), generator=gen, device=DEV)].contiguous()
+    x = (torch.randint(-2, 3, (T, 256), generator=gen, device=DEV).float() * 0.5).to(torch.bfloat16)
+    lk, ik, _ = _route_check(orc, ops, x, gate, 8, True)
+    # ties were really exercised: some token has equal logits across its 8/9 boundary
+    srt = np.sort(orc.bf16_to_f32(lk), axis=1)[:, ::-1]
+    assert (srt[:, 7] == srt[:, 8]).any()
+
+
+def test_route_hist(orc, pd):
+    ops, _, _ = pd
+    ids = torch.randint(0, 128, (4096, 8), device=DEV, dtype=torch.int32)
+    hist = ops.route_hist(ids, 128)
+    assert np.array_equal(hist.cpu().numpy(), orc.route_hist(ids.cpu().numpy(), 128))
+
+
+def test_route_rejects_bad_args(pd, qwen):
+    ops, _, synthetic = pd
+    x = synthetic.make_tokens(2, 2048)
+    with pytest.raises(ValueError):
+        ops.route_topk(x, qwen.gate, 0, True)
+    with pytest.raises(ValueError):
+        ops.route_topk(x.float(), qwen.gate, 8, True)
+
+
+# ------------------------------------------------------------------ pack
+
+def _pack_check(orc, ops, ids_np, E):
+    ids = torch.from_numpy(ids_np.astype(np.int32)).to(DEV)
+    p = ops.pack(ids, E)
+    torch.cuda.synchronize()
+    o = orc.pack(ids_np, E)
+    for name in ("counts", "offsets", "perm_token", "perm_pos", "row_of"):
+        assert np.array_equal(getattr(p, name).cpu().numpy(), o[name]), name
+
+
+@pytest.mark.parametrize("T,k,E", [(1, 8, 128), (7, 8, 128), (512, 8, 128), (4096, 8, 128), (1304, 6, 64),
+                                   (3, 1, 32), (1000, 16, 256)])
+def test_pack_uniform(orc, pd, T, k, E):
+    ops, _, _ = pd
+    rng = np.random.default_rng(T * 31 + k)
+    ids = np.stack([rng.choice(E, k, replace=False) for _ in range(T)])
+    _pack_check(orc, ops, ids, E)
+
+
+def test_pack_zipf_skew(orc, pd):
+    ops, _, _ = pd
+    rng = np.random.default_rng(5)
+    p = np.arange(1, 129, dtype=np.float64) ** -1.1
+    p /= p.sum()
+    ids = np.stack([rng.choice(128, 8, replace=False, p=p) for _ in range(4096)])
+    _pack_check(orc, ops, ids, 128)
+
+
+def test_pack_all_one_expert_column(orc, pd):
+    """Every token routes slot 0 to expert 0: one run of T rows, many empty experts."""
+    ops, _, _ = pd
+    T, k = 3000, 4
+    ids = np.stack([np.array([0, 1 + (t % 3), 10, 20 + (t % 7)]) for t in range(T)])
+    _pack_check(orc, ops, ids, 128)
+
+
+# ------------------------------------------------------------------ experts
+
+def _oracle_layer_given_routing(orc, x_u16, ids, w_u16, experts_u16, H, I):
+    """Oracle expert path + merge for a given routing (ids/weights)."""
+    E = experts_u16.shape[0]
+    p = orc.pack(ids, E)
+    xg = x_u16[p["perm_token"]]
+    y = np.empty((ids.size, H), np.uint16)
+    IH = I * H
+    for e in np.nonzero(p["counts"])[0]:
+        a, b = p["offsets"][e], p["offsets"][e + 1]
+        blk = experts_u16[e]
+        y[a:b] = orc.expert_forward(xg[a:b], blk[:IH].reshape(I, H), blk[IH:2 * IH].reshape(I, H),
+                                    blk[2 * IH:].reshape(H, I))
+    return orc.merge(y, p["row_of"], w_u16), y, p
+
+
+@pytest.mark.parametrize("T", [2, 16, 64])
+def test_layer_prefill_qwen(orc, pd, qwen, qwen_host, T):
+    ops, layer, synthetic = pd
+    x = synthetic.make_tokens(T, 2048, seed=500 + T)
+    ws = layer.MoEWorkspace(T, 2048, 768, 128, 8, DEV)
+    slots = ops.slot_table([qwen.experts[e] for e in range(128)], DEV)
+    out, logits, ids, w = layer.moe_forward(x, qwen.gate, slots, ws)
+    torch.cuda.synchronize()
+    xu, ik, wk = u16(x), ids.cpu().numpy(), u16(w)
+    oi, ow = orc.route_from_logits(u16(logits), 8, True)
+    assert np.array_equal(ik, oi) and np.array_equal(wk, ow)
+    ref, y_ref, p = _oracle_layer_given_routing(orc, xu, ik, wk, qwen_host["experts"], 2048, 768)
+    # per-row expert outputs (grouped order) before the merge
+    y_k = u16(ws.y[:T * 8 * 2048]).reshape(T * 8, 2048)
+    m_y = err_metrics(orc.bf16_to_f32(y_k), orc.bf16_to_f32(y_ref))
+    assert m_y["max_rel"] <= MAX_REL and m_y["mean_abs"] <= MEAN_ABS, m_y
+    m = err_metrics(orc.bf16_to_f32(u16(out)), orc.bf16_to_f32(ref))
+    assert m["max_rel"] <= MAX_REL and m["mean_abs"] <= MEAN_ABS, m
+
+
+@pytest.mark.parametrize("bm", [32, 64, 128])
+def test_grouped_block_m_variants(orc, pd, bm):
+    """All three row tiles on a small layer with ragged expert sizes (0..many rows)."""
+    ops, layer, synthetic = pd
+    H, I, E, k, T = 256, 128, 32, 4, 150
+    lay = synthetic.make_layer(H, I, E, k, True, seed=900 + bm, device=DEV)
+    x = synthetic.make_tokens(T, H, seed=901 + bm)
+    ws = layer.MoEWorkspace(T, H, I, E, k, DEV)
+    slots = ops.slot_table([lay.experts[e] for e in range(E)], DEV)
+    # skew: bias the router so a few experts get most rows
+    bias = torch.zeros(E, device=DEV)
+    bias[3] = 4.0
+    bias[7] = 2.0
+    out, logits, ids, w = layer.moe_forward(x, lay.gate, slots, ws, bias=bias, block_m=bm)
+    torch.cuda.synchronize()
+    ik, wk = ids.cpu().numpy(), u16(w)
+    ref, _, p = _oracle_layer_given_routing(orc, u16(x), ik, wk, u16(lay.experts), H, I)
+    assert p["counts"].max() >= 100  # one expert holds most tokens: many row tiles
+    m = err_metrics(orc.bf16_to_f32(u16(out)), orc.bf16_to_f32(ref))
+    assert m["max_rel"] <= MAX_REL and m["mean_abs"] <= MEAN_ABS, m
+
+
+def test_decode_qwen(orc, pd, qwen, qwen_host):
+    ops, layer, synthetic = pd
+    ws = layer.MoEWorkspace(1, 2048, 768, 128, 8, DEV)
+    slots = ops.slot_table([qwen.experts[e] for e in range(128)], DEV)
+    for seed in (600, 601, 602):
+        x = synthetic.make_tokens(1, 2048, seed=seed)
+        out, logits, ids, w = layer.moe_forward(x, qwen.gate, slots, ws)
+        torch.cuda.synchronize()
+        ik, wk = ids.cpu().numpy(), u16(w)
+        oi, ow = orc.route_from_logits(u16(logits), 8, True)
+        assert np.array_equal(ik, oi) and np.array_equal(wk, ow)
+        ref, _, _ = _oracle_layer_given_routing(orc, u16(x), ik, wk, qwen_host["experts"], 2048, 768)
+        m = err_metrics(orc.bf16_to_f32(u16(out)), orc.bf16_to_f32(ref))
+        assert m["max_rel"] <= MAX_REL and m["mean_abs"] <= MEAN_ABS, m
+
+
+def test_decode_equals_grouped_path(orc, pd, qwen):
+    """T=1 through K4 and through K2+K3+K5 (forced) agree within bf16 tolerance."""
+    ops, layer, synthetic = pd
+    x = synthetic.make_tokens(1, 2048, seed=700)
+    ws = layer.MoEWorkspace(2, 2048, 768, 128, 8, DEV)
+    slots = ops.slot_table([qwen.experts[e] for e in range(128)], DEV)
+    logits, ids, w = layer.route(x, qwen.gate, ws)
+    dec = layer.experts_resident(x, ids, w, slots, ws).clone()
+    # grouped path on the same routing: duplicate the token and keep row 0
+    x2 = torch.cat([x, x]).contiguous()
+    ids2 = torch.cat([ids, ids]).contiguous()
+    w2 = torch.cat([w, w]).contiguous()
+    grp = layer.experts_resident(x2, ids2, w2, slots, ws)[:1].clone()
+    torch.cuda.synchronize()
+    m = err_metrics(orc.bf16_to_f32(u16(dec)), orc.bf16_to_f32(u16(grp)))
+    assert m["max_rel"] <= MAX_REL and m["mean_abs"] <= MEAN_ABS, m
+
+
+def test_merge_matches_oracle(orc, pd):
+    ops, _, _ = pd
+    rng = np.random.default_rng(12)
+    T, k, H = 300, 8, 2048
+    y = orc.f32_to_bf16(rng.standard_normal((T * k, H)).astype(np.float32) * 0.3)
+    w = orc.f32_to_bf16(rng.random((T, k)).astype(np.float32) / k)
+    row_of = rng.permutation(T * k).astype(np.int32)
+    out = torch.empty((T, H), dtype=torch.bfloat16, device=DEV)
+    ops.merge(from_u16(y), torch.from_numpy(row_of).to(DEV), from_u16(w), out)
+    torch.cuda.synchronize()
+    ref = orc.merge(y, row_of, w)
+    d = ulp_diff_bf16(u16(out), ref)
+    assert (d <= 1).all() and (d > 0).mean() < 1e-3
+    add = orc.f32_to_bf16(rng.standard_normal((T, H)).astype(np.float32))
+    ops.merge(from_u16(y), torch.from_numpy(row_of).to(DEV), from_u16(w), out, add_in=from_u16(add))
+    torch.cuda.synchronize()
+    m = err_metrics(orc.bf16_to_f32(u16(out)), orc.bf16_to_f32(orc.merge(y, row_of, w, add_in=add)))
+    assert m["max_rel"] < 1e-2
+
+
+def test_stage_merge_matches_bf16_index_add(pd):
+    ops, _, _ = pd
+    rows, H = 8, 2048
+    g = torch.Generator().manual_seed(3)
+    block = torch.randn((rows, H), generator=g).to(torch.bfloat16).pin_memory()
+    weights = torch.rand(rows, generator=g).to(torch.bfloat16).to(DEV)
+    tokens = torch.zeros(rows, dtype=torch.int64, device=DEV)
+    scratch = torch.empty((rows, H), dtype=torch.bfloat16, device=DEV)
+    out = torch.zeros((1, H), dtype=torch.bfloat16, device=DEV)
+    ops.stage_merge(block.data_ptr(), rows, H * 2, scratch, out, tokens, weights)
+    torch.cuda.synchronize()
+    # sequential bf16 restatement of out.index_add_(0, tokens, scratch * weights[:, None])
+    ref = torch.zeros(H, dtype=torch.bfloat16)
+    prod = (block * weights.cpu()[:, None])
+    for r in range(rows):
+        ref = (ref.float() + prod[r].float()).to(torch.bfloat16)
+    assert torch.equal(out.cpu()[0], ref)
+    assert torch.equal(scratch.cpu(), block)
