@@ -1,0 +1,373 @@
+#!/usr/bin/env python3
+"""MoE-layer benchmark on one MI355X: Qwen3-30B-A3B-shaped layers, seeded random weights.
+
+    python bench.py [--steps K] [--warmup W] [--workload prefill512|decode|prefill4096]
+
+A step is one MoE layer forward over one batch of synthetic tokens whose
+inputs and weights are already resident in HBM: route (K1) -> pack (K2) ->
+tile schedule -> grouped SwiGLU gate/up + down (K3) -> merge (K5) for
+prefill, route (K1) -> decode GEMV gate/up + down/merge (K4) for T = 1
+(decode steps replay one hipGraph per layer).  Steps rotate over several
+independently seeded layer copies so the 256 MB Infinity Cache cannot hold
+the streamed weights between steps.
+
+The default workload is the T = 512 prefill (128 experts, top-8, all resident).
+The same JSON line also carries the T = 1 decode and T = 4096 prefill results
+("workloads"), each with its own roofline figure, and a CPU baseline: the
+AVX2 bf16 SwiGLU expert kernel under oracle/ (a stand-in for ktransformers'
+AVX2BF16_MOE, which is not available offline) timed on this host's cores on
+the same layer and routing.
+
+Roofline: ``achieved`` is algorithmic bytes (or useful flops) of the dominant
+kernel per launch divided by its mean duration, measured with HIP events on
+the launch stream during the timed steps.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+METRIC = "MoE layer tok/s at T=1 and T=4096; HBM GB/s and MFMA util vs peak"
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
+H, I, E, K_TOP = 2048, 768, 128, 8
+EXPERT_BYTES = 3 * I * H * 2   # 9 437 184
+ROUTER_BYTES = E * H * 2
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="prefill512", choices=["prefill512", "decode", "prefill4096"])
+    ap.add_argument("--no-extra", action="store_true", help="only the main workload")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, cpus) - 1")
+    return ap.parse_args()
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+# ----------------------------------------------------------------------------- GPU legs
+
+def build_layers(n, device, seed0):
+    from pdscope_amd import ops, synthetic
+    layers = []
+    for i in range(n):
+        lay = synthetic.make_layer(H, I, E, K_TOP, True, seed=seed0 + 1000 * i, device=device)
+        slots = ops.slot_table([lay.experts[e] for e in range(E)], device)
+        layers.append((lay, slots))
+    return layers
+
+
+def run_prefill(T, steps, warmup, n_layers, device, seed0):
+    """Eager launches; HIP events bracket the grouped gate/up kernel in every timed step."""
+    import torch
+    from pdscope_amd import layer, ops, synthetic
+    layers = build_layers(n_layers, device, seed0)
+    xs = [synthetic.make_tokens(T, H, seed=seed0 + 7 + 1000 * i, device=device) for i in range(n_layers)]
+    ws = layer.MoEWorkspace(T, H, I, E, K_TOP, device)
+    n = T * K_TOP
+    _, _, _, packed = ws.views(T)
+    stream = torch.cuda.current_stream(device)
+
+    def step(i, ev=None):
+        lay, slots = layers[i % n_layers]
+        x = xs[i % n_layers]
+        logits, ids, w = layer.route(x, lay.gate, ws)
+        ops.pack(ids, E, out=packed)
+        bm = ops.grouped_block_m(n // E)
+        ops.schedule(packed.counts, ws.sel_all, bm, out=ws.tile_start)
+        max_tiles = (n + bm - 1) // bm + E
+        if ev is not None:
+            ev[0].record(stream)
+        ops.swiglu_grouped_gateup(x, packed.perm_token, packed.offsets, ws.sel_all, ws.tile_start, max_tiles, bm,
+                                  slots, H, I, ws.h_ws)
+        if ev is not None:
+            ev[1].record(stream)
+        ops.swiglu_grouped_down(ws.h_ws, packed.offsets, ws.sel_all, ws.tile_start, max_tiles, bm, slots, H, I,
+                                ws.y)
+        ops.merge(ws.y, packed.row_of, w, ws.out[:T])
+
+    # experts touched per layer (for algorithmic bytes)
+    touched = []
+    for i in range(n_layers):
+        step(i)
+        torch.cuda.synchronize(device)
+        touched.append(int((ws.counts > 0).sum().item()))
+    for i in range(warmup):
+        step(i)
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize(device)
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(i, events[i])
+    torch.cuda.synchronize(device)
+    wall = time.perf_counter() - t0
+    gateup_ms = [a.elapsed_time(b) for a, b in events]
+    mean_touched = sum(touched[i % n_layers] for i in range(steps)) / steps
+    return dict(T=T, wall_s=wall, ms_per_step=wall / steps * 1e3, tok_s=T * steps / wall,
+                gateup_ms_mean=statistics.mean(gateup_ms), gateup_ms_median=statistics.median(gateup_ms),
+                touched=mean_touched, block_m=ops.grouped_block_m(n // E), layers=n_layers,
+                first_layer=layers[0], first_x=xs[0], ws=ws)
+
+
+def run_decode(steps, warmup, n_layers, device, seed0):
+    """One hipGraph per layer copy (route + gate/up + down/merge); events around each replay."""
+    import torch
+    from pdscope_amd import layer, synthetic
+    layers = build_layers(n_layers, device, seed0)
+    xs = [synthetic.make_tokens(1, H, seed=seed0 + 7 + 1000 * i, device=device) for i in range(n_layers)]
+    ws = layer.MoEWorkspace(1, H, I, E, K_TOP, device)
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        for i in range(n_layers):
+            layer.moe_forward(xs[i], layers[i][0].gate, layers[i][1], ws)
+    torch.cuda.current_stream(device).wait_stream(side)
+    torch.cuda.synchronize(device)
+    graphs = []
+    for i in range(n_layers):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            layer.moe_forward(xs[i], layers[i][0].gate, layers[i][1], ws)
+        graphs.append(g)
+    torch.cuda.synchronize(device)
+    # graph replay must equal eager execution
+    eager = []
+    for i in range(n_layers):
+        layer.moe_forward(xs[i], layers[i][0].gate, layers[i][1], ws)
+        eager.append(ws.out[:1].clone())
+    for i in range(n_layers):
+        graphs[i].replay()
+        if not torch.equal(ws.out[:1], eager[i]):
+            raise AssertionError("decode graph replay differs from eager execution")
+    for i in range(warmup):
+        graphs[i % n_layers].replay()
+    stream = torch.cuda.current_stream(device)
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    torch.cuda.synchronize(device)
+    t0 = time.perf_counter()
+    events[0].record(stream)
+    for i in range(steps):
+        graphs[i % n_layers].replay()
+        events[i + 1].record(stream)
+    torch.cuda.synchronize(device)
+    wall = time.perf_counter() - t0
+    layer_ms = [events[i].elapsed_time(events[i + 1]) for i in range(steps)]
+    return dict(T=1, wall_s=wall, ms_per_step=wall / steps * 1e3, tok_s=steps / wall,
+                layer_ms_mean=statistics.mean(layer_ms), layer_ms_median=statistics.median(layer_ms),
+                layers=n_layers, first_layer=layers[0], first_x=xs[0], ws=ws)
+
+
+# ----------------------------------------------------------------------------- CPU baseline
+
+def cpu_threads(requested):
+    if requested > 0:
+        return requested
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 2
+    return max(1, min(16, avail) - 1)
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def u16(t):
+    import numpy as np
+    import torch
+    return t.detach().contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def cpu_baseline_prefill(res, threads, reps=7, warm=2):
+    """Full expert work of the first layer's routing (all T*k rows) on the host cores."""
+    import numpy as np
+    from oracle import oracle as orc
+    lay, _ = res["first_layer"]
+    ws = res["ws"]
+    T = res["T"]
+    from pdscope_amd import layer
+    layer.route(res["first_x"], lay.gate, ws)
+    ids = ws.ids[:T].cpu().numpy()
+    w = ws.weights[:T].float().cpu().numpy()
+    x = u16(res["first_x"])
+    experts = np.ascontiguousarray(u16(lay.experts))
+    ptrs = [experts[e].ctypes.data for e in range(E)]
+    rows = np.ascontiguousarray(np.repeat(x, K_TOP, axis=0))
+    sel = ids.reshape(-1).astype(np.int64)
+    coeff = w.reshape(-1).astype(np.float32)
+    times = []
+    for r in range(warm + reps):
+        t0 = time.perf_counter()
+        orc.cpu_moe_rows(rows, sel, coeff, ptrs, H, I, threads)
+        if r >= warm:
+            times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return dict(value=T / med, unit="tok/s", cores=threads, kind="port",
+                sample=f"full T={T} layer expert work ({T * K_TOP} rows, routing of layer 0), median of {reps} "
+                       f"runs after {warm} warm-ups, {threads} threads, {cpu_model()}",
+                median_s=med)
+
+
+def cpu_baseline_decode(res, threads, reps=7, warm=2):
+    import numpy as np
+    from oracle import oracle as orc
+    from pdscope_amd import layer
+    lay, _ = res["first_layer"]
+    ws = res["ws"]
+    layer.route(res["first_x"], lay.gate, ws)
+    ids = ws.ids[:1].cpu().numpy()
+    w = u16(ws.weights[:1])
+    x = u16(res["first_x"])
+    experts = np.ascontiguousarray(u16(lay.experts))
+    ptrs = [experts[e].ctypes.data for e in range(E)]
+    # rotate the 8 selected experts through distinct host copies so DRAM, not the
+    # CPU caches, serves the weights (8 x 9 MiB per token)
+    copies = [np.ascontiguousarray(experts[ids[0]].copy()) for _ in range(4)]
+    times = []
+    for r in range(warm + reps):
+        c = copies[r % len(copies)]
+        local_ptrs = list(ptrs)
+        for s, e in enumerate(ids[0]):
+            local_ptrs[e] = c[s].ctypes.data
+        t0 = time.perf_counter()
+        orc.cpu_moe_decode(x, ids, w, local_ptrs, H, I, threads)
+        if r >= warm:
+            times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return dict(value=1.0 / med, unit="tok/s", cores=threads, kind="port",
+                sample=f"one T=1 token through its 8 routed experts, median of {reps} runs after {warm} warm-ups, "
+                       f"{threads} threads, {cpu_model()}",
+                dram_gbs=K_TOP * EXPERT_BYTES / med / 1e9)
+
+
+# ----------------------------------------------------------------------------- reporting
+
+def prefill_record(res):
+    T, touched = res["T"], res["touched"]
+    n = T * K_TOP
+    gateup_bytes = touched * 2 * I * H * 2 + T * H * 2 + n * I * 2
+    gateup_flops = 2.0 * n * H * 2 * I
+    t = res["gateup_ms_mean"] / 1e3
+    layer_bytes = touched * EXPERT_BYTES + ROUTER_BYTES + 2 * T * H * 2
+    layer_flops = 2.0 * n * 3 * I * H + 2.0 * T * E * H
+    hbm = dict(bound="hbm", achieved=gateup_bytes / t / 1e9, peak=HBM_PEAK_GBS, unit="GB/s")
+    hbm["frac"] = hbm["achieved"] / hbm["peak"]
+    mfma = dict(bound="mfma", achieved=gateup_flops / t / 1e12, peak=BF16_PEAK_TFLOPS, unit="TFLOP/s")
+    mfma["frac"] = mfma["achieved"] / mfma["peak"]
+    layer_s = res["ms_per_step"] / 1e3
+    return dict(tok_s=res["tok_s"], ms_per_step=res["ms_per_step"], kernel="grouped_kernel<gateup>",
+                kernel_ms_mean=res["gateup_ms_mean"], kernel_ms_median=res["gateup_ms_median"],
+                kernel_bytes=gateup_bytes, kernel_flops=gateup_flops, experts_touched=touched,
+                block_m=res["block_m"], layers_rotated=res["layers"], hbm=hbm, mfma=mfma,
+                layer_hbm_gbs=layer_bytes / layer_s / 1e9, layer_mfma_tflops=layer_flops / layer_s / 1e12)
+
+
+def decode_record(res):
+    layer_bytes = K_TOP * EXPERT_BYTES + ROUTER_BYTES + 2 * H * 2
+    t = res["layer_ms_mean"] / 1e3
+    hbm = dict(bound="hbm", achieved=layer_bytes / t / 1e9, peak=HBM_PEAK_GBS, unit="GB/s")
+    hbm["frac"] = hbm["achieved"] / hbm["peak"]
+    return dict(tok_s=res["tok_s"], ms_per_step=res["ms_per_step"], kernel="decode layer hipGraph (3 kernels)",
+                kernel_ms_mean=res["layer_ms_mean"], kernel_ms_median=res["layer_ms_median"],
+                kernel_bytes=layer_bytes, layers_rotated=res["layers"], hbm=hbm,
+                layer_hbm_gbs=layer_bytes / (res["ms_per_step"] / 1e3) / 1e9)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the MoE layer path here is "
+              "single-GPU and multi-GPU figures are not measured", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from pdscope_amd import _lib
+    _lib.load()
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    threads = cpu_threads(args.cpu_threads)
+
+    plan = {"prefill512": ("prefill", 512, 4), "decode": ("decode", 1, 16), "prefill4096": ("prefill", 4096, 2)}
+    order = [args.workload] + ([] if args.no_extra else [w for w in plan if w != args.workload])
+    records, raw = {}, {}
+    for wl in order:
+        kind, T, nl = plan[wl]
+        main_leg = wl == args.workload
+        steps = args.steps if main_leg else {"prefill512": 200, "decode": 2000, "prefill4096": 50}[wl]
+        warmup = args.warmup if main_leg else {"prefill512": 20, "decode": 200, "prefill4096": 5}[wl]
+        if kind == "decode":
+            steps = max(steps, 1)
+        log(f"[bench] {wl}: T={T} layers={nl} steps={steps} warmup={warmup}")
+        if kind == "prefill":
+            res = run_prefill(T, steps, warmup, nl, device, 20261011)
+            rec = prefill_record(res)
+        else:
+            res = run_decode(steps, warmup, nl, device, 20261011)
+            rec = decode_record(res)
+        rec["steps"], rec["warmup"] = steps, warmup
+        log(f"[bench] {wl}: {rec['tok_s']:.1f} tok/s, {rec['ms_per_step']:.4f} ms/step, kernel "
+            f"{rec['kernel_ms_mean']:.4f} ms, {rec['hbm']['achieved']:.0f} GB/s")
+        records[wl] = rec
+        raw[wl] = res
+        if not args.no_cpu_baseline and wl in ("prefill512", "decode"):
+            log(f"[bench] {wl}: CPU baseline on {threads} threads")
+            cb = cpu_baseline_prefill(res, threads) if kind == "prefill" else cpu_baseline_decode(res, threads)
+            rec["cpu_baseline"] = cb
+            log(f"[bench] {wl}: CPU baseline {cb['value']:.2f} tok/s")
+        for k in ("first_layer", "first_x", "ws"):
+            res.pop(k, None)
+        torch.cuda.empty_cache()
+
+    main = records[args.workload]
+    if args.workload == "prefill4096":
+        roof = dict(main["mfma"])
+    else:
+        roof = dict(main["hbm"])
+    roof["kernel"] = main["kernel"]
+    roof["traffic"] = None
+    cfg_name = {"prefill512": "Qwen3-30B-A3B-shaped MoE layer, prefill T=512 uniform routing, 128 experts resident",
+                "decode": "Qwen3-30B-A3B-shaped MoE layer, decode T=1, 128 experts resident (hipGraph per layer)",
+                "prefill4096": "Qwen3-30B-A3B-shaped MoE layer, prefill T=4096 uniform routing, 128 experts resident"}
+    kind, T, nl = plan[args.workload]
+    line = {
+        "metric": METRIC,
+        "value": round(main["tok_s"], 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": main["steps"],
+        "warmup": main["warmup"],
+        "ms_per_step": round(main["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded random bf16 weights ~N(0,0.02), activations ~N(0,1))",
+        "config": {"workload": cfg_name[args.workload], "tokens": T, "hidden": H, "experts": E,
+                   "intermediate": I, "top_k": K_TOP, "layers_rotated": nl, "parallelism": "single GPU"},
+        "roofline": roof,
+        "cpu_baseline": {k: v for k, v in main.get("cpu_baseline", {}).items() if k in
+                         ("value", "unit", "cores", "kind", "sample")} or None,
+        "workloads": records,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -104,6 +104,17 @@ int pdscope_swiglu_grouped(const void *x, const int32_t *perm_token, const int32
                            int max_tiles, int block_m, const void *const *slots, int H, int I,
                            void *h_ws, void *y, void *stream);
 
+/* The two launches of pdscope_swiglu_grouped, separately (same arguments):
+ * gate/up + SwiGLU into h_ws, then down into y.  Lets a caller overlap or
+ * time them individually. */
+int pdscope_swiglu_grouped_gateup(const void *x, const int32_t *perm_token, const int32_t *offsets,
+                                  const int32_t *sel, int nsel, const int32_t *tile_start, int max_tiles,
+                                  int block_m, const void *const *slots, int H, int I, void *h_ws,
+                                  void *stream);
+int pdscope_swiglu_grouped_down(const void *h_ws, const int32_t *offsets, const int32_t *sel, int nsel,
+                                const int32_t *tile_start, int max_tiles, int block_m,
+                                const void *const *slots, int H, int I, void *y, void *stream);
+
 /*
  * A8 fused weighted merge: replaces the index_add_ merge
  * (expertbench/pdscope_runtime.py:450-469).

@@ -26,6 +26,8 @@ SIGNATURES = {
     "pdscope_schedule": ([_vp, _vp, _i32, _i32, _vp, _vp], _i32),
     "pdscope_grouped_block_m": ([_i32], _i32),
     "pdscope_swiglu_grouped": ([_vp, _vp, _vp, _vp, _i32, _vp, _i32, _i32, _vp, _i32, _i32, _vp, _vp, _vp], _i32),
+    "pdscope_swiglu_grouped_gateup": ([_vp, _vp, _vp, _vp, _i32, _vp, _i32, _i32, _vp, _i32, _i32, _vp, _vp], _i32),
+    "pdscope_swiglu_grouped_down": ([_vp, _vp, _vp, _i32, _vp, _i32, _i32, _vp, _i32, _i32, _vp, _vp], _i32),
     "pdscope_merge": ([_vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp], _i32),
     "pdscope_swiglu_decode": ([_vp, _vp, _vp, _i32, _vp, _i32, _i32, _vp, _vp, _vp], _i32),
     "pdscope_stage_expert": ([_vp, _vp, _sz, _vp, _vp], _i32),

@@ -173,20 +173,53 @@ __global__ __launch_bounds__(256, 2) void grouped_kernel(
     }
 }
 
+// phase: 1 = gate/up only, 2 = down only, 3 = both
 template <int BM, int BN, int WM, int WN>
-int launch_grouped(const uint16_t *x, const int32_t *perm_token, const int32_t *offsets, const int32_t *sel,
-                   int nsel, const int32_t *tile_start, int max_tiles, const uint16_t *const *slots, int H,
-                   int I, uint16_t *h_ws, uint16_t *y, hipStream_t s) {
+int launch_grouped(int phase, const uint16_t *x, const int32_t *perm_token, const int32_t *offsets,
+                   const int32_t *sel, int nsel, const int32_t *tile_start, int max_tiles,
+                   const uint16_t *const *slots, int H, int I, uint16_t *h_ws, uint16_t *y, hipStream_t s) {
     if (I % (BN / 2) || H % BN) return fail(kEInval, "grouped: I must divide by BN/2 and H by BN");
-    dim3 g1(max_tiles, I / (BN / 2));
-    grouped_kernel<BM, BN, WM, WN, true><<<g1, 256, 0, s>>>(x, perm_token, offsets, sel, nsel, tile_start,
-                                                             slots, H, I, h_ws);
-    int rc = check_launch("grouped_kernel<gateup>");
-    if (rc) return rc;
-    dim3 g2(max_tiles, H / BN);
-    grouped_kernel<BM, BN, WM, WN, false><<<g2, 256, 0, s>>>(h_ws, nullptr, offsets, sel, nsel, tile_start,
-                                                              slots, H, I, y);
-    return check_launch("grouped_kernel<down>");
+    if (phase & 1) {
+        dim3 g1(max_tiles, I / (BN / 2));
+        grouped_kernel<BM, BN, WM, WN, true><<<g1, 256, 0, s>>>(x, perm_token, offsets, sel, nsel, tile_start,
+                                                                 slots, H, I, h_ws);
+        int rc = check_launch("grouped_kernel<gateup>");
+        if (rc) return rc;
+    }
+    if (phase & 2) {
+        dim3 g2(max_tiles, H / BN);
+        grouped_kernel<BM, BN, WM, WN, false><<<g2, 256, 0, s>>>(h_ws, nullptr, offsets, sel, nsel, tile_start,
+                                                                  slots, H, I, y);
+        return check_launch("grouped_kernel<down>");
+    }
+    return kOk;
+}
+
+int grouped_entry(int phase, const void *x, const int32_t *perm_token, const int32_t *offsets, const int32_t *sel,
+                  int nsel, const int32_t *tile_start, int max_tiles, int block_m, const void *const *slots, int H,
+                  int I, void *h_ws, void *y, void *stream) {
+    if (((phase & 1) && (!x || !perm_token)) || !offsets || !sel || !tile_start || !slots || !h_ws ||
+        ((phase & 2) && !y))
+        return fail(kEInval, "grouped: null pointer");
+    if (nsel < 1 || max_tiles < 1) return fail(kEInval, "grouped: need nsel >= 1 and max_tiles >= 1");
+    if (H % 64 || I % 64 || H < 64 || I < 64) return fail(kEInval, "grouped: need H % 64 == 0 and I % 64 == 0");
+    if (max_tiles > (1 << 30)) return fail(kEInval, "grouped: max_tiles too large");
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const uint16_t *xp = (const uint16_t *)x;
+    const uint16_t *const *sp = (const uint16_t *const *)slots;
+    switch (block_m) {
+    case 32:
+        return launch_grouped<32, 256, 1, 4>(phase, xp, perm_token, offsets, sel, nsel, tile_start, max_tiles, sp, H,
+                                             I, (uint16_t *)h_ws, (uint16_t *)y, s);
+    case 64:
+        return launch_grouped<64, 128, 2, 2>(phase, xp, perm_token, offsets, sel, nsel, tile_start, max_tiles, sp, H,
+                                             I, (uint16_t *)h_ws, (uint16_t *)y, s);
+    case 128:
+        return launch_grouped<128, 128, 2, 2>(phase, xp, perm_token, offsets, sel, nsel, tile_start, max_tiles, sp,
+                                              H, I, (uint16_t *)h_ws, (uint16_t *)y, s);
+    default:
+        return fail(kEInval, "grouped: block_m must be 32, 64 or 128");
+    }
 }
 
 }  // namespace pd
@@ -203,25 +236,21 @@ PD_API int pdscope_swiglu_grouped(const void *x, const int32_t *perm_token, cons
                                   const int32_t *sel, int nsel, const int32_t *tile_start, int max_tiles,
                                   int block_m, const void *const *slots, int H, int I, void *h_ws, void *y,
                                   void *stream) {
-    if (!x || !perm_token || !offsets || !sel || !tile_start || !slots || !h_ws || !y)
-        return fail(kEInval, "grouped: null pointer");
-    if (nsel < 1 || max_tiles < 1) return fail(kEInval, "grouped: need nsel >= 1 and max_tiles >= 1");
-    if (H % 64 || I % 64 || H < 64 || I < 64) return fail(kEInval, "grouped: need H % 64 == 0 and I % 64 == 0");
-    if (max_tiles > (1 << 30)) return fail(kEInval, "grouped: max_tiles too large");
-    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    const uint16_t *xp = (const uint16_t *)x;
-    const uint16_t *const *sp = (const uint16_t *const *)slots;
-    switch (block_m) {
-    case 32:
-        return launch_grouped<32, 256, 1, 4>(xp, perm_token, offsets, sel, nsel, tile_start, max_tiles, sp, H, I,
-                                             (uint16_t *)h_ws, (uint16_t *)y, s);
-    case 64:
-        return launch_grouped<64, 128, 2, 2>(xp, perm_token, offsets, sel, nsel, tile_start, max_tiles, sp, H, I,
-                                             (uint16_t *)h_ws, (uint16_t *)y, s);
-    case 128:
-        return launch_grouped<128, 128, 2, 2>(xp, perm_token, offsets, sel, nsel, tile_start, max_tiles, sp, H,
-                                              I, (uint16_t *)h_ws, (uint16_t *)y, s);
-    default:
-        return fail(kEInval, "grouped: block_m must be 32, 64 or 128");
-    }
+    return grouped_entry(3, x, perm_token, offsets, sel, nsel, tile_start, max_tiles, block_m, slots, H, I, h_ws, y,
+                         stream);
+}
+
+PD_API int pdscope_swiglu_grouped_gateup(const void *x, const int32_t *perm_token, const int32_t *offsets,
+                                         const int32_t *sel, int nsel, const int32_t *tile_start, int max_tiles,
+                                         int block_m, const void *const *slots, int H, int I, void *h_ws,
+                                         void *stream) {
+    return grouped_entry(1, x, perm_token, offsets, sel, nsel, tile_start, max_tiles, block_m, slots, H, I, h_ws,
+                         nullptr, stream);
+}
+
+PD_API int pdscope_swiglu_grouped_down(const void *h_ws, const int32_t *offsets, const int32_t *sel, int nsel,
+                                       const int32_t *tile_start, int max_tiles, int block_m,
+                                       const void *const *slots, int H, int I, void *y, void *stream) {
+    return grouped_entry(2, nullptr, nullptr, offsets, sel, nsel, tile_start, max_tiles, block_m, slots, H, I,
+                         const_cast<void *>(h_ws), y, stream);
 }

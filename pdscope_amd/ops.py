@@ -147,6 +147,25 @@ def swiglu_grouped(x, perm_token, offsets, sel, tile_start, max_tiles, block_m, 
     return y
 
 
+def swiglu_grouped_gateup(x, perm_token, offsets, sel, tile_start, max_tiles, block_m, slots, H, I, h_ws):
+    """Only the gate/up + SwiGLU launch of swiglu_grouped (K3, first half)."""
+    dev = x.device
+    _need(x, "inputs", BF16, 2)
+    _need(h_ws, "h_ws", BF16, None, dev)
+    if h_ws.numel() < perm_token.numel() * I:
+        raise ValueError("h_ws is smaller than rows x I")
+    _lib.call("pdscope_swiglu_grouped_gateup", _p(x), _p(perm_token), _p(offsets), _p(sel), sel.numel(),
+              _p(tile_start), int(max_tiles), int(block_m), _p(slots), H, I, _p(h_ws), _stream(dev))
+
+
+def swiglu_grouped_down(h_ws, offsets, sel, tile_start, max_tiles, block_m, slots, H, I, y):
+    """Only the down-projection launch of swiglu_grouped (K3, second half)."""
+    dev = h_ws.device
+    _need(y, "y", BF16, None, dev)
+    _lib.call("pdscope_swiglu_grouped_down", _p(h_ws), _p(offsets), _p(sel), sel.numel(), _p(tile_start),
+              int(max_tiles), int(block_m), _p(slots), H, I, _p(y), _stream(dev))
+
+
 def swiglu_decode(x, ids, w, slots, H, I, h_ws, out):
     _need(x, "inputs", BF16)
     dev = x.device
