@@ -86,10 +86,7 @@ __global__ __launch_bounds__(256) void decode_down_kernel(const uint16_t *__rest
             const uint4 *row = reinterpret_cast<const uint4 *>(slots[ids[s]] + IH2 + (size_t)j * I);
             uint4 wv[CPL];
 #pragma unroll
-            for (int c = 0; c < CPL; ++c) {
-                const int ch = hl + 32 * c;
-                if (ch < CI) wv[c] = ld_nt(row + ch);
-            }
+            for (int c = 0; c < CPL; ++c) wv[c] = ld_nt(row + min(hl + 32 * c, CI - 1));
 #pragma unroll
             for (int c = 0; c < CPL; ++c) {
                 const int ch = hl + 32 * c;

@@ -38,9 +38,16 @@ __global__ __launch_bounds__(256, 2) void grouped_kernel(
     __shared__ __attribute__((aligned(16))) uint16_t s_a[2][BM * kBK];
     __shared__ __attribute__((aligned(16))) uint16_t s_b[2][BN * kBK];
 
-    // ---- locate (expert, m-tile): binary search over the tile prefix
-    const int bx = blockIdx.x;
+    // ---- XCD-aware tile order: blocks are dispatched round-robin over the 8
+    // XCDs (block b -> XCD b % 8).  m-tile mt is pinned to XCD mt % 8 and its
+    // n-tiles are consecutive blocks of that XCD, so the gathered activation
+    // rows of an m-tile are fetched into one L2 and reused by every n-tile.
+    const int ntn = GATEUP ? I / (BN / 2) : H / BN;
+    const int xcd = blockIdx.x & 7, pos = blockIdx.x >> 3;
+    const int jm = pos / ntn, nt = pos - jm * ntn;
+    const int bx = jm * 8 + xcd;
     if (bx >= tile_start[nsel]) return;
+    // ---- locate (expert, m-tile): binary search over the tile prefix
     int lo = 0, hi = nsel - 1;
     while (lo < hi) {
         int mid = (lo + hi + 1) >> 1;
@@ -51,7 +58,7 @@ __global__ __launch_bounds__(256, 2) void grouped_kernel(
     const int row_end = offsets[e + 1];
     const int m0 = offsets[e] + (bx - tile_start[lo]) * BM;
     const int K = GATEUP ? H : I;
-    const int n0 = blockIdx.y * (GATEUP ? BN / 2 : BN);  // first intermediate (gate/up) or output column
+    const int n0 = nt * (GATEUP ? BN / 2 : BN);  // first intermediate (gate/up) or output column
     const uint16_t *base = slots[e];
     const size_t IH = (size_t)I * H;
 
@@ -180,14 +187,14 @@ int launch_grouped(int phase, const uint16_t *x, const int32_t *perm_token, cons
                    const uint16_t *const *slots, int H, int I, uint16_t *h_ws, uint16_t *y, hipStream_t s) {
     if (I % (BN / 2) || H % BN) return fail(kEInval, "grouped: I must divide by BN/2 and H by BN");
     if (phase & 1) {
-        dim3 g1(max_tiles, I / (BN / 2));
+        const unsigned g1 = (unsigned)((max_tiles + 7) / 8 * 8) * (unsigned)(I / (BN / 2));
         grouped_kernel<BM, BN, WM, WN, true><<<g1, 256, 0, s>>>(x, perm_token, offsets, sel, nsel, tile_start,
                                                                  slots, H, I, h_ws);
         int rc = check_launch("grouped_kernel<gateup>");
         if (rc) return rc;
     }
     if (phase & 2) {
-        dim3 g2(max_tiles, H / BN);
+        const unsigned g2 = (unsigned)((max_tiles + 7) / 8 * 8) * (unsigned)(H / BN);
         grouped_kernel<BM, BN, WM, WN, false><<<g2, 256, 0, s>>>(h_ws, nullptr, offsets, sel, nsel, tile_start,
                                                                   slots, H, I, y);
         return check_launch("grouped_kernel<down>");
@@ -203,7 +210,7 @@ int grouped_entry(int phase, const void *x, const int32_t *perm_token, const int
         return fail(kEInval, "grouped: null pointer");
     if (nsel < 1 || max_tiles < 1) return fail(kEInval, "grouped: need nsel >= 1 and max_tiles >= 1");
     if (H % 64 || I % 64 || H < 64 || I < 64) return fail(kEInval, "grouped: need H % 64 == 0 and I % 64 == 0");
-    if (max_tiles > (1 << 30)) return fail(kEInval, "grouped: max_tiles too large");
+    if (max_tiles > (1 << 22)) return fail(kEInval, "grouped: max_tiles too large");
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const uint16_t *xp = (const uint16_t *)x;
     const uint16_t *const *sp = (const uint16_t *const *)slots;
@@ -226,9 +233,11 @@ int grouped_entry(int phase, const void *x, const int32_t *perm_token, const int
 
 using namespace pd;
 
+// Weights are re-read once per m-tile of an expert, so the row tile should
+// cover a typical expert in one tile; 32 only for very thin experts.
 PD_API int pdscope_grouped_block_m(int rows_hint) {
-    if (rows_hint <= 32) return 32;
-    if (rows_hint <= 96) return 64;
+    if (rows_hint <= 16) return 32;
+    if (rows_hint <= 80) return 64;
     return 128;
 }
 

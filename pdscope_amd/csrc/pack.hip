@@ -43,6 +43,31 @@ __device__ int block_scan256(int v, int *s_wsum) {
     return v + add;
 }
 
+constexpr int kPackRC = 32;  // 64-id chunks per wave held in registers
+
+// Load up to kPackRC chunks of the wave's segment (expert id, or -1 outside
+// the segment / outside [0, E)) with every load in flight at once.
+__device__ __forceinline__ void pack_load(const int32_t *__restrict__ ids, int T, int k, int E, int sc, int end,
+                                          int lane, int (&idv)[kPackRC]) {
+    // Addresses are clamped into the segment so every load is unconditional
+    // and all kPackRC loads are in flight together; out-of-segment lanes are
+    // masked afterwards.
+    const int last = max(end - 1, 0);
+    int raw[kPackRC];
+#pragma unroll
+    for (int c = 0; c < kPackRC; ++c) {
+        const int f = min(sc + c * 64 + lane, last);
+        const int s = f / T, t = f - s * T;
+        raw[c] = ids[(size_t)t * k + s];
+    }
+#pragma unroll
+    for (int c = 0; c < kPackRC; ++c) {
+        const int f = sc + c * 64 + lane;
+        const int e = raw[c];
+        idv[c] = (f < end && e >= 0 && e < E) ? e : -1;
+    }
+}
+
 __global__ __launch_bounds__(1024) void pack_kernel(const int32_t *__restrict__ ids, int T, int k, int E,
                                                     int32_t *__restrict__ counts, int32_t *__restrict__ offsets,
                                                     int32_t *__restrict__ perm_token,
@@ -55,21 +80,21 @@ __global__ __launch_bounds__(1024) void pack_kernel(const int32_t *__restrict__ 
     const int seg = ((n + kPackWaves * 64 - 1) / (kPackWaves * 64)) * 64;
     const int beg = min(wave * seg, n), end = min(beg + seg, n);
     const uint64_t below = (1ull << lane) - 1ull;
+    const bool one_pass = (end - beg) <= kPackRC * 64;
+    int idv[kPackRC];
 
     for (int e = lane; e < E; e += 64) s_cnt[wave][e] = 0;
     __syncthreads();
-    for (int base = beg; base < end; base += 64) {
-        const int f = base + lane;
-        bool valid = f < end;
-        int e = 0;
-        if (valid) {
-            int s = f / T, t = f - s * T;
-            e = ids[(size_t)t * k + s];
-            valid = (e >= 0 && e < E);
-            if (!valid) e = 0;
+    // pass 1: per-wave counts
+    for (int sc = beg; sc < end; sc += kPackRC * 64) {
+        pack_load(ids, T, k, E, sc, end, lane, idv);
+#pragma unroll
+        for (int c = 0; c < kPackRC; ++c) {
+            if (sc + c * 64 >= end) break;
+            const int e = idv[c];
+            const uint64_t m = group_mask(e < 0 ? 0 : e, e >= 0);
+            if (e >= 0 && !(m & below)) s_cnt[wave][e] += __popcll(m);
         }
-        const uint64_t m = group_mask(e, valid);
-        if (valid && !(m & below)) s_cnt[wave][e] += __popcll(m);
     }
     __syncthreads();
     int tot = 0;
@@ -89,24 +114,23 @@ __global__ __launch_bounds__(1024) void pack_kernel(const int32_t *__restrict__ 
         }
     }
     __syncthreads();
-    for (int base = beg; base < end; base += 64) {
-        const int f = base + lane;
-        bool valid = f < end;
-        int e = 0, s = 0, t = 0;
-        if (valid) {
-            s = f / T;
-            t = f - s * T;
-            e = ids[(size_t)t * k + s];
-            valid = (e >= 0 && e < E);
-            if (!valid) e = 0;
-        }
-        const uint64_t m = group_mask(e, valid);
-        if (valid) {
-            const int pos = s_cnt[wave][e] + __popcll(m & below);
-            perm_token[pos] = t;
-            perm_pos[pos] = t * k + s;
-            row_of[(size_t)t * k + s] = pos;
-            if (!(m & below)) s_cnt[wave][e] += __popcll(m);
+    // pass 2: stable scatter
+    for (int sc = beg; sc < end; sc += kPackRC * 64) {
+        if (!one_pass) pack_load(ids, T, k, E, sc, end, lane, idv);
+#pragma unroll
+        for (int c = 0; c < kPackRC; ++c) {
+            if (sc + c * 64 >= end) break;
+            const int e = idv[c];
+            const uint64_t m = group_mask(e < 0 ? 0 : e, e >= 0);
+            if (e >= 0) {
+                const int f = sc + c * 64 + lane;
+                const int s = f / T, t = f - s * T;
+                const int pos = s_cnt[wave][e] + __popcll(m & below);
+                perm_token[pos] = t;
+                perm_pos[pos] = t * k + s;
+                row_of[(size_t)t * k + s] = pos;
+                if (!(m & below)) s_cnt[wave][e] += __popcll(m);
+            }
         }
     }
 }

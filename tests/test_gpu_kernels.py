@@ -88,6 +88,15 @@ def test_route_deepseek_no_renorm(orc, pd, T):
     _route_check(orc, ops, x, gate, 6, False)
 
 
+@pytest.mark.parametrize("T", [3, 100])
+def test_route_256_experts_top16(orc, pd, T):
+    ops, _, synthetic = pd
+    gen = torch.Generator(device=DEV).manual_seed(9)
+    gate = (torch.randn((256, 1024), generator=gen, device=DEV) * 0.02).to(torch.bfloat16)
+    x = synthetic.make_tokens(T, 1024, seed=450 + T)
+    _route_check(orc, ops, x, gate, 16, True)
+
+
 @pytest.mark.parametrize("T", [1, 64])
 def test_route_tie_heavy(orc, pd, T):
     """Few distinct router rows and coarse activations: many exact logit ties."""
