@@ -132,7 +132,7 @@ int pdscope_merge(const void *y, const int32_t *row_of, const void *w, int T, in
  *   h_s  = bf16(bf16(silu(bf16(x.gate_s^T))) * bf16(x.up_s^T))  (h_ws [k,I])
  *   out  = bf16( sum_s w[s] * bf16(h_s . down_s^T) )            (out [H])
  * for the k experts ids[0..k). Streaming GEMV, weights read once.
- * Limits: H % 512 == 0, I % 8 == 0, k <= 16.
+ * Limits: H % 8 == 0, H <= 4096, I % 8 == 0, k <= 16, k*I*2 <= 64 KiB.
  */
 int pdscope_swiglu_decode(const void *x, const int32_t *ids, const void *w, int k,
                           const void *const *slots, int H, int I, void *h_ws, void *out,
@@ -157,6 +157,15 @@ int pdscope_stage_expert(void *dst_slot, const void *pinned_src, size_t bytes, v
  */
 int pdscope_stage_merge(const void *host_block, int64_t rows, int64_t row_bytes, void *scratch,
                         void *out, const int64_t *tokens, const void *weights, void *stream);
+
+/*
+ * A9 native CPU-group tail, host half: replaces fill_packed and the id /
+ * coefficient / count setup of submit_group (native/native_layer_dispatch.cpp:
+ * 34-40, 59-67).  Copies `row` (row_bytes) into packed[r] for r < rows, sets
+ * selected[r] = ids[r], coeff[r] = 1.0f and *count = rows.  Host memory only.
+ */
+int pdscope_dispatch_pack(const void *row, int64_t rows, int64_t row_bytes, void *packed, int32_t *count,
+                          int64_t *selected, float *coeff, const int64_t *ids);
 
 #ifdef __cplusplus
 }

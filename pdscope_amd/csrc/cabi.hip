@@ -2,6 +2,8 @@
 // demand-staging copy (A7, expertbench/executor.py:341-363).
 #include "common.h"
 
+#include <cstring>
+
 namespace pd {
 
 static thread_local std::string g_error;
@@ -37,5 +39,23 @@ PD_API int pdscope_stage_expert(void *dst_slot, const void *pinned_src, size_t b
         err = hipEventRecord(reinterpret_cast<hipEvent_t>(event), s);
         if (err != hipSuccess) return fail(kEHip, std::string("hipEventRecord: ") + hipGetErrorString(err));
     }
+    return kOk;
+}
+
+// Host half of the native decode dispatch (native/native_layer_dispatch.cpp:34-40,
+// 59-67): `rows` copies of one activation row into the packed block, expert ids
+// into `selected`, unit coefficients and the row count, ready for the CPU
+// expert queue's forward_task.
+PD_API int pdscope_dispatch_pack(const void *row, int64_t rows, int64_t row_bytes, void *packed, int32_t *count,
+                                 int64_t *selected, float *coeff, const int64_t *ids) {
+    if (rows < 1 || row_bytes < 2 || row_bytes % 2 != 0) return fail(kEInval, "invalid decode pack shape");
+    if (!row || !packed || !count || !selected || !coeff || !ids) return fail(kEInval, "dispatch_pack: null pointer");
+    char *dst = static_cast<char *>(packed);
+    for (int64_t r = 0; r < rows; ++r) {
+        selected[r] = ids[r];
+        coeff[r] = 1.0f;
+        std::memcpy(dst + r * row_bytes, row, static_cast<size_t>(row_bytes));
+    }
+    *count = static_cast<int32_t>(rows);
     return kOk;
 }

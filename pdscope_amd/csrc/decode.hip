@@ -27,21 +27,30 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(const uint16_t *__re
     const int q0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 2;
     const int items = k * I;
     if (q0 >= items) return;
+    // lane owns 16-byte chunks lane + 64*j (j < NJ) of each H-row; when H is
+    // not a multiple of 512 the tail chunks are clamped and masked out
+    const int C = H >> 3;
     uint4 xv[NJ];
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) xv[j] = reinterpret_cast<const uint4 *>(x)[lane + 64 * j];
+    for (int j = 0; j < NJ; ++j) xv[j] = reinterpret_cast<const uint4 *>(x)[min(lane + 64 * j, C - 1)];
     uint4 gv[2][NJ], uv[2][NJ];
+    bool ok[2];
 #pragma unroll
     for (int it = 0; it < 2; ++it) {
         const int q = min(q0 + it, items - 1);
         const int s = q / I, i = q - s * I;
         const uint16_t *base = slots[ids[s]];
-        const uint4 *grow = reinterpret_cast<const uint4 *>(base + (size_t)i * H);
-        const uint4 *urow = reinterpret_cast<const uint4 *>(base + (size_t)(I + i) * H);
+        // an expert without a ready copy reads the activation row instead
+        // (H elements, in bounds) and contributes h = 0
+        ok[it] = base != nullptr;
+        const uint4 *grow = ok[it] ? reinterpret_cast<const uint4 *>(base + (size_t)i * H)
+                                   : reinterpret_cast<const uint4 *>(x);
+        const uint4 *urow = ok[it] ? reinterpret_cast<const uint4 *>(base + (size_t)(I + i) * H)
+                                   : reinterpret_cast<const uint4 *>(x);
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
-            gv[it][j] = ld_nt(grow + lane + 64 * j);
-            uv[it][j] = ld_nt(urow + lane + 64 * j);
+            gv[it][j] = ld_nt(grow + min(lane + 64 * j, C - 1));
+            uv[it][j] = ld_nt(urow + min(lane + 64 * j, C - 1));
         }
     }
 #pragma unroll
@@ -49,15 +58,17 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(const uint16_t *__re
         float g = 0.0f, u = 0.0f;
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
-            g = dot8(gv[it][j], xv[j], g);
-            u = dot8(uv[it][j], xv[j], u);
+            if (lane + 64 * j < C) {
+                g = dot8(gv[it][j], xv[j], g);
+                u = dot8(uv[it][j], xv[j], u);
+            }
         }
         g = wave_sum(g);
         u = wave_sum(u);
         const int q = q0 + it;
         if (lane == 0 && q < items) {
             const float a = bf16_round(silu_f32(bf16_round(g)));
-            h_ws[q] = (uint16_t)f2bf(a * bf16_round(u));
+            h_ws[q] = ok[it] ? (uint16_t)f2bf(a * bf16_round(u)) : (uint16_t)0;
         }
     }
 }
@@ -83,7 +94,10 @@ __global__ __launch_bounds__(256) void decode_down_kernel(const uint16_t *__rest
         const int s = p + half;
         float acc = 0.0f;
         if (s < k) {
-            const uint4 *row = reinterpret_cast<const uint4 *>(slots[ids[s]] + IH2 + (size_t)j * I);
+            const uint16_t *base = slots[ids[s]];
+            // no ready copy: read h itself (k*I elements, in bounds) and add 0
+            const uint4 *row = base ? reinterpret_cast<const uint4 *>(base + IH2 + (size_t)j * I)
+                                    : reinterpret_cast<const uint4 *>(h_ws);
             uint4 wv[CPL];
 #pragma unroll
             for (int c = 0; c < CPL; ++c) wv[c] = ld_nt(row + min(hl + 32 * c, CI - 1));
@@ -92,6 +106,7 @@ __global__ __launch_bounds__(256) void decode_down_kernel(const uint16_t *__rest
                 const int ch = hl + 32 * c;
                 if (ch < CI) acc = dot8(wv[c], s_h[s * CI + ch], acc);
             }
+            if (!base) acc = 0.0f;
         }
         acc = half_sum(acc);
         const float odd = __shfl(acc, 32, kWave);
@@ -112,7 +127,7 @@ PD_API int pdscope_swiglu_decode(const void *x, const int32_t *ids, const void *
                                  void *stream) {
     if (!x || !ids || !w || !slots || !h_ws || !out) return fail(kEInval, "decode: null pointer");
     if (k < 1 || k > 16) return fail(kEInval, "decode: need 1 <= k <= 16");
-    if (H < 512 || H % 512 || H > 8192) return fail(kEInval, "decode: need H % 512 == 0 and H <= 8192");
+    if (H < 8 || H % 8 || H > 4096) return fail(kEInval, "decode: need H % 8 == 0 and H <= 4096");
     if (I < 8 || I % 8 || I > 8192) return fail(kEInval, "decode: need I % 8 == 0 and I <= 8192");
     if ((size_t)k * I * 2 > 64 * 1024) return fail(kEInval, "decode: k*I*2 must fit 64 KiB of LDS");
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
@@ -120,7 +135,7 @@ PD_API int pdscope_swiglu_decode(const void *x, const int32_t *ids, const void *
     const uint16_t *const *sp = (const uint16_t *const *)slots;
     const int waves = (k * I + 1) / 2;
     const int blocks = (waves + 3) / 4;
-    switch (H / 512) {
+    switch ((H / 8 + 63) / 64) {
 #define PD_GU(NJ)                                                                                          \
     case NJ:                                                                                               \
         decode_gateup_kernel<NJ><<<blocks, 256, 0, s>>>(xp, ids, sp, H, I, k, (uint16_t *)h_ws);           \

@@ -60,6 +60,7 @@ __global__ __launch_bounds__(256, 2) void grouped_kernel(
     const int K = GATEUP ? H : I;
     const int n0 = nt * (GATEUP ? BN / 2 : BN);  // first intermediate (gate/up) or output column
     const uint16_t *base = slots[e];
+    if (base == nullptr) return;  // no ready copy of this expert: never dereference
     const size_t IH = (size_t)I * H;
 
     // ---- per-thread global row pointers (fixed over the K loop)

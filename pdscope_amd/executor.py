@@ -1,0 +1,432 @@
+"""Device executor: pinned-source staging into HBM slots and grouped expert launches.
+
+Mirrors ExpertExecutor (expertbench/executor.py:165-680) for the GPU path:
+
+* ``load`` reserves a copy in the ledger and stages the expert's whole
+  gate|up|down block (one pinned host block, one ``hipMemcpyAsync``) into a
+  cache-pool slot or a demand staging slot on the load stream, recording one
+  event (executor.py:333-372);
+* ``finish_load`` reports completion to the ledger only after that event
+  completed (executor.py:374-390);
+* ``gpu_group`` acquires every expert of a launch, runs ONE grouped launch on
+  the compute stream and records one event; ``finish_gpu`` releases them after
+  the event completed (executor.py:430-511 keep one event per expert; here a
+  layer's experts share one launch and one event);
+* ``gpu(key, inputs)`` keeps the per-expert operator hook of executor.py:454-488
+  (rows of one expert through the same grouped kernel);
+* each layer has a device slot table (int64 base address per expert, 0 when
+  no ready copy), so kernels address cache and staging slots uniformly.
+
+Single control thread; streams keep the default priority.
+"""
+from __future__ import annotations
+
+import contextlib
+import ctypes
+from dataclasses import dataclass, field
+
+import torch
+
+from . import ops
+from .cache import ExpertKey
+
+PROJECTIONS = ("gate_proj", "up_proj", "down_proj")
+
+
+@dataclass
+class ExpertWeights:
+    """One expert's three projections; ``flat`` is the gate|up|down block when contiguous."""
+    key: ExpertKey
+    tensors: dict
+    provenance: dict = field(default_factory=dict)
+    flat: torch.Tensor | None = None
+
+    @property
+    def nbytes(self):
+        return sum(t.numel() * t.element_size() for t in self.tensors.values())
+
+
+def masters_from_block(layer, block, E, H, I, *, pin=True):
+    """ExpertWeights for one layer whose experts are rows of a [E, 3*I*H] bf16 tensor.
+
+    The host copy is page-locked (pinned) so staging is one DMA per expert.
+    """
+    host = block.detach().to("cpu")
+    if pin:
+        host = host.pin_memory()
+    IH = I * H
+    out = {}
+    for e in range(E):
+        row = host[e]
+        tensors = {"gate_proj": row[:IH].view(I, H), "up_proj": row[IH:2 * IH].view(I, H),
+                   "down_proj": row[2 * IH:].view(H, I)}
+        key = ExpertKey(layer, e, "bf16")
+        out[key] = ExpertWeights(key, tensors, {"source": "synthetic seeded layer"}, flat=row)
+    return out
+
+
+@dataclass
+class PendingCompute:
+    handles: tuple
+    output: object
+    event: object
+    input_ref: object
+    keys: tuple = ()
+
+
+class _PinnedRing:
+    """Small page-locked upload buffers reused after their last copy completed."""
+
+    def __init__(self, nbytes, depth=16):
+        self.bufs = [torch.empty(nbytes, dtype=torch.uint8, pin_memory=True) for _ in range(depth)]
+        self.events = [None] * depth
+        self.i = 0
+
+    def take(self):
+        i = self.i
+        self.i = (i + 1) % len(self.bufs)
+        if self.events[i] is not None:
+            self.events[i].synchronize()
+        return i, self.bufs[i]
+
+    def mark(self, i, stream):
+        ev = torch.cuda.Event()
+        ev.record(stream)
+        self.events[i] = ev
+
+
+class ExpertExecutor:
+    def __init__(self, cache, masters, device=0, *, pinned_source_mode="all_masters", capture_events=True,
+                 streams=None, cpu_backend=None, cache_storage=None, staging_storage=None, profile_stages=False):
+        if pinned_source_mode not in ("all_masters", "lazy_pinned"):
+            raise ValueError("unknown pinned source mode")
+        if cpu_backend is not None and not callable(cpu_backend):
+            raise ValueError("CPU backend must be an explicit callable")
+        self.cache, self.masters = cache, dict(masters)
+        if set(cache.expert_bytes) != set(self.masters):
+            raise ValueError("cache and master weight registries differ")
+        for key, w in self.masters.items():
+            if w.nbytes != cache.expert_bytes[key] or any(
+                    t.device.type != "cpu" or t.dtype != torch.bfloat16 for t in w.tensors.values()):
+                raise ValueError("master bytes/device/dtype do not match the cache contract")
+        sizes = set(cache.expert_bytes.values())
+        if len(sizes) != 1:
+            raise ValueError("equal-size bf16 experts required")
+        self.expert_bytes = next(iter(sizes))
+        self.device = torch.device("cuda", device) if isinstance(device, int) else torch.device(device)
+        self.cpu_backend = cpu_backend
+        self.gpu_backend = None
+        self.capture_events = capture_events
+        self.profile_stages = profile_stages
+        self.pinned_source_mode = pinned_source_mode
+        self.events: list = []
+        if streams is None:
+            self.load_stream = torch.cuda.Stream(device=self.device)
+            self.compute_stream = torch.cuda.Stream(device=self.device)
+        else:
+            if (not isinstance(streams, tuple) or len(streams) != 2 or streams[0] == streams[1]
+                    or any(s.device != self.device for s in streams)):
+                raise ValueError("shared executor streams must be a distinct pair on the same device")
+            self.load_stream, self.compute_stream = streams
+        # ---- device storage: one contiguous cache pool of equal slots, plus staging slots
+        nslots = cache.cache_bytes // self.expert_bytes
+        if cache_storage is None:
+            cache_storage = torch.empty(nslots * self.expert_bytes, dtype=torch.uint8, device=self.device)
+        if (cache_storage.device != self.device or cache_storage.dtype != torch.uint8 or cache_storage.ndim != 1
+                or not cache_storage.is_contiguous() or cache_storage.numel() < nslots * self.expert_bytes):
+            raise ValueError("cache storage must be a contiguous uint8 device tensor covering every cache slot")
+        self.cache_storage = cache_storage
+        self._free_cache_slots = list(reversed(range(nslots)))
+        if staging_storage is None:
+            staging_storage = tuple(torch.empty(n, dtype=torch.uint8, device=self.device)
+                                    for n in cache.staging_slot_bytes)
+        if (len(staging_storage) != len(cache.staging_slot_bytes)
+                or any(t.device != self.device or t.dtype != torch.uint8 or not t.is_contiguous() or t.numel() < n
+                       for t, n in zip(staging_storage, cache.staging_slot_bytes))):
+            raise ValueError("staging storage must match every declared staging slot")
+        spans = sorted((t.data_ptr(), t.data_ptr() + t.numel()) for t in staging_storage)
+        spans.append((cache_storage.data_ptr(), cache_storage.data_ptr() + cache_storage.numel()))
+        spans.sort()
+        if any(a[1] > b[0] for a, b in zip(spans, spans[1:])):
+            raise ValueError("cache and staging buffers must not overlap")
+        self.staging = list(staging_storage)
+        # ---- pinned sources (one flat block per expert)
+        self.pinned = {}
+        if pinned_source_mode == "all_masters":
+            for key in self.masters:
+                self.pinned[key] = self._pinned_block(key)
+        # ---- bookkeeping
+        self.copies = {}     # ticket -> flat device uint8 view
+        self._cache_slot_of = {}
+        self.loads = {}      # ticket -> event
+        self.computes = {}   # id(pending) -> pending
+        self._free_events = []
+        self.closed = False
+        self._host_tables = {}  # layer -> host list of base addresses (0 = no ready copy)
+        self._dev_tables = {}   # layer -> device int64 [E]
+        self._ring = _PinnedRing(8 * 256)
+        self._group_stream_ctx = None
+
+    # ------------------------------------------------------------ sources
+
+    def _pinned_block(self, key):
+        w = self.masters[key]
+        flat = w.flat
+        if flat is not None and flat.is_pinned() and flat.is_contiguous():
+            return flat.view(torch.uint8) if flat.dtype != torch.uint8 else flat
+        block = torch.empty(self.expert_bytes, dtype=torch.uint8, pin_memory=True)
+        off = 0
+        for name in PROJECTIONS:
+            t = w.tensors[name].contiguous()
+            n = t.numel() * t.element_size()
+            block[off:off + n].copy_(t.view(torch.uint8).reshape(-1))
+            off += n
+        return block
+
+    def prepare_source(self, key):
+        self._open()
+        if key not in self.pinned:
+            self.pinned[key] = self._pinned_block(key)
+        return self.pinned[key]
+
+    # ------------------------------------------------------------ helpers
+
+    def _open(self):
+        if self.closed:
+            raise RuntimeError("executor has been shut down; its ledger cannot be reused")
+
+    def _event(self):
+        return self._free_events.pop() if self._free_events else torch.cuda.Event()
+
+    def _log(self, **kw):
+        if self.capture_events:
+            self.events.append(kw)
+
+    def _host_table(self, layer, E):
+        """Host mirror of a layer's slot table, seeded from the ready copies in the ledger."""
+        host = self._host_tables.get(layer)
+        if host is None:
+            host = [0] * E
+            for e in range(E):
+                key = ExpertKey(layer, e, "bf16")
+                if key not in self.masters:
+                    continue
+                view = self.cache.lookup(key)
+                if view is not None and view.state != "loading" and view.ticket in self.copies:
+                    host[e] = self.copies[view.ticket].data_ptr()
+            self._host_tables[layer] = host
+        return host
+
+    def table(self, layer, E):
+        """Device slot table of `layer` (int64 [E]) and its host mirror; 0 = no ready copy."""
+        host = self._host_table(layer, E)
+        dev = self._dev_tables.get(layer)
+        if dev is None:
+            dev = torch.zeros(E, dtype=torch.int64, device=self.device)
+            self._dev_tables[layer] = dev
+        return dev, host
+
+    def _set_entry(self, key, addr):
+        host = self._host_tables.get(key.layer)
+        if host is not None and key.expert < len(host):
+            host[key.expert] = addr
+
+    def table_entry(self, layer, e):
+        host = self._host_tables.get(layer)
+        return 0 if host is None or e >= len(host) else host[e]
+
+    def upload_table(self, layer, E, stream):
+        """Copy the host mirror of a layer's slot table to the device on `stream`."""
+        dev, host = self.table(layer, E)
+        i, buf = self._ring.take()
+        view = buf[:8 * E].view(torch.int64)
+        view.copy_(torch.tensor(host, dtype=torch.int64))
+        with torch.cuda.stream(stream):
+            dev.copy_(view, non_blocking=True)
+        self._ring.mark(i, stream)
+        return dev
+
+    def upload_ints(self, values, stream):
+        """A fresh int32 device tensor holding `values`, copied on `stream` via the pinned ring."""
+        n = len(values)
+        if 4 * n > self._ring.bufs[0].numel():
+            raise ValueError("too many values for one upload")
+        i, buf = self._ring.take()
+        view = buf[:4 * n].view(torch.int32)
+        view.copy_(torch.tensor(values, dtype=torch.int32))
+        dev = torch.empty(n, dtype=torch.int32, device=self.device)
+        with torch.cuda.stream(stream):
+            dev.copy_(view, non_blocking=True)
+        self._ring.mark(i, stream)
+        return dev
+
+    def base_address(self, key):
+        view = self.cache.lookup(key)
+        if view is None:
+            return 0
+        flat = self.copies.get(view.ticket)
+        return 0 if flat is None else flat.data_ptr()
+
+    def reclaim(self):
+        self._open()
+        for ticket in self.cache.take_retired():
+            if ticket in self.loads:
+                raise RuntimeError("the ledger retired a copy with a transfer in flight")
+            flat = self.copies.pop(ticket, None)
+            slot = self._cache_slot_of.pop(ticket, None)
+            if slot is not None:
+                self._free_cache_slots.append(slot)
+            self._set_entry(ticket.key, 0)
+            self._log(event="retired", generation=ticket.generation, pool=ticket.pool)
+
+    # ------------------------------------------------------------ loads
+
+    def load(self, key, *, origin="demand", admit=True):
+        self._open()
+        ticket = self.cache.begin_load(key, origin=origin, admit=admit)
+        self.reclaim()
+        if ticket in self.copies:
+            return ticket
+        src = self.prepare_source(key)
+        if ticket.pool == "demand_staging":
+            flat = self.staging[ticket.slot][:self.expert_bytes]
+        else:
+            if not self._free_cache_slots:
+                raise RuntimeError("cache pool slot accounting differs from the ledger")
+            slot = self._free_cache_slots.pop()
+            self._cache_slot_of[ticket] = slot
+            flat = self.cache_storage[slot * self.expert_bytes:(slot + 1) * self.expert_bytes]
+        self.copies[ticket] = flat
+        self.cache.submit(ticket)
+        ev = self._event()
+        ops.stage_expert(flat, src, event=ev, stream=self.load_stream)
+        self.loads[ticket] = ev
+        self._log(event="load_submitted", generation=ticket.generation, pool=ticket.pool,
+                  expert_bytes=self.expert_bytes, source_pinned=bool(src.is_pinned()))
+        return ticket
+
+    def finish_load(self, ticket, *, wait=False):
+        self._open()
+        ev = self.loads[ticket]
+        if wait:
+            ev.synchronize()
+        if not ev.query():
+            return False
+        self.cache.complete_load(ticket)
+        del self.loads[ticket]
+        self._free_events.append(ev)
+        self._set_entry(ticket.key, self.copies[ticket].data_ptr())
+        self._log(event="load_completed", generation=ticket.generation)
+        return True
+
+    # ------------------------------------------------------------ compute
+
+    def begin_gpu_group(self):
+        """Join the current stream once for a span of already materialised inputs."""
+        self._open()
+        self.compute_stream.wait_stream(torch.cuda.current_stream(self.device))
+        self._group_stream_ctx = torch.cuda.stream(self.compute_stream)
+        self._group_stream_ctx.__enter__()
+
+    def end_gpu_group(self):
+        if self._group_stream_ctx is not None:
+            self._group_stream_ctx.__exit__(None, None, None)
+            self._group_stream_ctx = None
+
+    def gpu_group(self, keys, launch, *, input_ref=None, wait_for=None):
+        """Acquire `keys`, run `launch()` (one grouped launch) on the compute stream, record one event."""
+        self._open()
+        handles = tuple(self.cache.acquire(k) for k in keys)
+        for h in handles:
+            if h.ticket not in self.copies or h.ticket in self.loads:
+                raise RuntimeError("acquired a copy whose transfer has not been confirmed")
+        span = self._group_stream_ctx is not None
+        ctx = contextlib.nullcontext() if span else torch.cuda.stream(self.compute_stream)
+        with ctx:
+            if not span:
+                self.compute_stream.wait_stream(torch.cuda.current_stream(self.device)
+                                                if wait_for is None else wait_for)
+            output = launch()
+            ev = self._event()
+            ev.record(self.compute_stream)
+        p = PendingCompute(handles, output, ev, input_ref, tuple(keys))
+        self.computes[id(p)] = p
+        self._log(event="compute_submitted", experts=len(keys))
+        return p
+
+    def finish_gpu(self, pending, *, wait=False):
+        self._open()
+        if self.computes.get(id(pending)) is not pending:
+            raise ValueError("unknown or already completed GPU computation")
+        if wait:
+            pending.event.synchronize()
+        if not pending.event.query():
+            return None
+        for h in pending.handles:
+            self.cache.release(h)
+        del self.computes[id(pending)]
+        self._free_events.append(pending.event)
+        pending.event, pending.input_ref = None, None
+        self.reclaim()
+        self._log(event="compute_completed", experts=len(pending.handles))
+        return pending.output
+
+    def gpu(self, key, inputs):
+        """Per-expert operator hook: rows of one expert -> unweighted bf16 outputs."""
+        self._open()
+        if inputs.device != self.device or inputs.dtype != torch.bfloat16:
+            raise ValueError("GPU input must already be bf16 on the configured device")
+        w = self.masters[key]
+        I, H = w.tensors["gate_proj"].shape
+        if inputs.ndim != 2 or inputs.shape[1] != H:
+            raise ValueError("invalid expert input shape")
+        view = self.cache.lookup(key)
+        if view is None or view.ticket not in self.copies:
+            raise ValueError("expert has no device copy")
+        flat = self.copies[view.ticket]
+
+        def launch():
+            if self.gpu_backend is not None:
+                return self.gpu_backend(key, inputs, flat)
+            return expert_rows(inputs, flat, H, I)
+
+        return self.gpu_group([key], launch, input_ref=inputs)
+
+    def shutdown(self):
+        if not self.closed:
+            self.load_stream.synchronize()
+            self.compute_stream.synchronize()
+            self.copies.clear()
+            self.loads.clear()
+            self.computes.clear()
+            self.staging.clear()
+            self.pinned.clear()
+            self._host_tables.clear()
+            self._dev_tables.clear()
+            self.cache_storage = None
+            self.closed = True
+
+    def storage(self):
+        return dict(cache_tensor_bytes=sum(f.numel() for t, f in self.copies.items() if t.pool == "cache"),
+                    cache_reserved_tensor_bytes=self.cache_storage.numel() if self.cache_storage is not None else 0,
+                    staging_tensor_bytes=sum(t.numel() for t in self.staging),
+                    pinned_source_bytes=sum(t.numel() * t.element_size() for t in self.pinned.values()))
+
+
+def expert_rows(x, base, H, I, *, h_ws=None, y=None):
+    """y = expert(x) for rows x [m, H] of one expert whose gate|up|down block starts
+    at `base` (a device tensor or an integer device address)."""
+    m = x.shape[0]
+    dev = x.device
+    addr = base if isinstance(base, int) else base.data_ptr()
+    slots = torch.tensor([addr], dtype=torch.int64, device=dev)
+    i32 = dict(dtype=torch.int32, device=dev)
+    perm = torch.arange(m, **i32)
+    offsets = torch.tensor([0, m], **i32)
+    sel = torch.zeros(1, **i32)
+    bm = ops.grouped_block_m(m)
+    tile_start = torch.tensor([0, (m + bm - 1) // bm], **i32)
+    h_ws = torch.empty(m * I, dtype=torch.bfloat16, device=dev) if h_ws is None else h_ws
+    y = torch.empty((m, H), dtype=torch.bfloat16, device=dev) if y is None else y
+    ops.swiglu_grouped(x.contiguous(), perm, offsets, sel, tile_start, (m + bm - 1) // bm, bm, slots, H, I, h_ws, y)
+    return y

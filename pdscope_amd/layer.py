@@ -18,7 +18,7 @@ BF16 = torch.bfloat16
 class MoEWorkspace:
     """Device buffers for up to ``max_tokens`` tokens of one layer shape."""
 
-    def __init__(self, max_tokens: int, H: int, I: int, E: int, k: int, device):
+    def __init__(self, max_tokens: int, H: int, I: int, E: int, k: int, device, *, route_only: bool = False):
         device = torch.device(device)
         n = max_tokens * k
         i32 = dict(dtype=torch.int32, device=device)
@@ -33,9 +33,10 @@ class MoEWorkspace:
         self.row_of = torch.empty(n, **i32)
         self.tile_start = torch.empty(E + 1, **i32)
         self.sel_all = torch.arange(E, **i32)
-        self.h_ws = torch.empty(max(n, 1) * I, dtype=BF16, device=device)
-        self.y = torch.empty(max(n, 1) * H, dtype=BF16, device=device)
-        self.out = torch.empty((max_tokens, H), dtype=BF16, device=device)
+        rows = 1 if route_only else max(n, 1)
+        self.h_ws = torch.empty(rows * I, dtype=BF16, device=device)
+        self.y = torch.empty(rows * H, dtype=BF16, device=device)
+        self.out = torch.empty((1 if route_only else max_tokens, H), dtype=BF16, device=device)
         self.hist = torch.empty(E, **i32)
         ops.route_workspace(device)
 

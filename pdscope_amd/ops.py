@@ -198,15 +198,21 @@ def merge(y, row_of, w, out, add_in=None):
 
 
 def stage_expert(dst, src, *, event=None, stream=None):
-    """One H2D copy of a pinned expert block into a device slot (+ event)."""
+    """One H2D copy of a pinned expert block into a device slot, then `event` on the same stream.
+
+    The torch event is recorded by torch after the copy is enqueued (its HIP
+    event only exists once recorded), so completion of that event implies the
+    copy landed.
+    """
     if src.device.type != "cpu" or not src.is_pinned():
         raise ValueError("staging source must be page-locked host memory")
     nbytes = src.numel() * src.element_size()
     if dst.numel() * dst.element_size() < nbytes:
         raise ValueError("staging slot is smaller than the expert block")
     s = stream if stream is not None else torch.cuda.current_stream(dst.device)
-    ev = None if event is None else ctypes.c_void_p(event.cuda_event)
-    _lib.call("pdscope_stage_expert", _p(dst), _p(src), nbytes, ev, ctypes.c_void_p(s.cuda_stream))
+    _lib.call("pdscope_stage_expert", _p(dst), _p(src), nbytes, None, ctypes.c_void_p(s.cuda_stream))
+    if event is not None:
+        event.record(s)
 
 
 def stage_merge(host_block_ptr, rows, row_bytes, scratch, out, tokens, weights):

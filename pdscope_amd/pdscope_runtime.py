@@ -1,0 +1,404 @@
+"""Per-layer MoE runtime on the gfx950 kernels (drop-in for expertbench/pdscope_runtime.py).
+
+``PDScopeCudaRuntime(masters, *, hot_keys, speculative_slots, ...)`` and
+``.forward(inputs, gate, *, layer, step, request, next_gate, top_k, normalize,
+attention_ms, prefetch) -> (out, Routing, trace_row)`` keep the reference
+signature (pdscope_runtime.py:76-82, :208-209) and return triple
+(:492-512); invalid arguments raise ValueError, broken invariants
+AssertionError.
+
+One layer call:
+ 1. route on the GPU (K1); the gate-fallback predictor routes the same
+    activation with the next layer's gate and histograms it (K1 + hist);
+ 2. grouping (K2) on the GPU; one device->host copy of the per-expert counts
+    (and the predictor histogram) reveals the true demand to the ledger;
+ 3. every routed expert with a cache copy runs in ONE grouped launch (K3; K4
+    for a fully resident decode token) on the compute stream;
+ 4. experts without a copy stream through the demand staging slots: copy on
+    the load stream, grouped launch over that slot when its event completed,
+    slot released after the compute event (ping-pong depth slots-1 for
+    prefill, 1 for decode, as pdscope_runtime.py:361);
+ 5. predicted next-layer experts are prefetched into the cache pool
+    (speculative_slots bound, LRU eviction, never evicting the static hot set);
+ 6. the merge (K5) writes the layer output in token order.
+With ``resident_graphs=True`` a decode layer whose experts are all resident
+replays a captured hipGraph of route + decode (K1 + K4); its ledger accounting
+follows the replay (nothing can evict while the control thread waits).
+
+This runtime places every expert on the GPU: the CPU/GPU split of
+``plan_pdscope`` (expertbench/pdscope_policy.py:72-223) is not part of this
+path, so ``costs`` and ``cpu_backend`` are accepted and recorded but unused.
+"""
+from __future__ import annotations
+
+import hashlib
+from pathlib import Path
+
+import torch
+
+from . import layer as L
+from . import ops
+from .adapters.qwen import Routing
+from .cache import DemandID, ExpertCache, ExpertKey
+from .executor import ExpertExecutor
+
+
+def load_hot_profile(path, masters, slots):
+    """Static hot-expert table, one ``layer,expert`` per line (hot/qwen.txt format;
+    pdscope_runtime.py:62-72)."""
+    raw = Path(path).read_bytes()
+    rows = [tuple(map(int, line.split(","))) for line in raw.decode().splitlines() if line.strip()]
+    if (type(slots) is not int or slots < 0 or len(set(rows)) != len(rows)
+            or any(len(r) != 2 or r[0] < 0 or r[1] < 0 for r in rows)):
+        raise ValueError("invalid static hot profile or capacity")
+    keys = [ExpertKey(l, e, "bf16") for l, e in rows if ExpertKey(l, e, "bf16") in masters]
+    if len(keys) < slots:
+        raise ValueError("hot table cannot fill the declared static capacity")
+    return keys[:slots], dict(path=str(Path(path).resolve()), sha256=hashlib.sha256(raw).hexdigest(),
+                              entries=len(rows), eligible_entries=len(keys), selected=slots)
+
+
+class PDScopeCudaRuntime:
+    def __init__(self, masters, *, hot_keys, speculative_slots, costs=None, cpu_backend=None, device=0,
+                 streams=None, capture_events=False, diagnostics=True, cache_storage=None, staging_storage=None,
+                 source_mode="all_masters", resident_graphs=False, graph_cost_mode="eager_bound", cpu_batch="off",
+                 balance_profile=False, dispatch="reference", decode_cpu_target=None, merge="reference",
+                 input_pregather=False, graph_output_pool=False, demand_slots=2, native_dispatch=None):
+        if (type(speculative_slots) is not int or speculative_slots < 0
+                or len(set(hot_keys)) != len(hot_keys) or not set(hot_keys) <= masters.keys()):
+            raise ValueError("invalid PDScope cache contract")
+        sizes = {k: w.nbytes for k, w in masters.items()}
+        if len(set(sizes.values())) != 1:
+            raise ValueError("equal-size original BF16 experts required")
+        if cpu_batch not in ("off", "decode", "both") or dispatch not in ("reference", "compact"):
+            raise ValueError("invalid CPU packing or dispatch mode")
+        if merge not in ("reference", "fused") or type(input_pregather) is not bool:
+            raise ValueError("invalid merge mode or pre-gather switch")
+        if type(graph_output_pool) is not bool or type(resident_graphs) is not bool:
+            raise ValueError("graph switches must be boolean")
+        # the reference allows 2..4 staging slots (pdscope_runtime.py:108-109); this
+        # path also serves configurations with 8
+        if type(demand_slots) is not int or not 2 <= demand_slots <= 8:
+            raise ValueError("invalid demand staging depth")
+        if decode_cpu_target is not None and (type(decode_cpu_target) is not int or not 0 <= decode_cpu_target <= 8):
+            raise ValueError("invalid decode CPU balance target")
+        self.size = next(iter(sizes.values()))
+        self.hot = set(hot_keys)
+        self.layers = {k.layer for k in masters}
+        any_w = next(iter(masters.values()))
+        self.I, self.H = any_w.tensors["gate_proj"].shape
+        self.E = 1 + max(k.expert for k in masters)
+        self.speculative_slots = speculative_slots
+        self.costs, self.cpu_backend, self.native_dispatch = costs, cpu_backend, native_dispatch
+        self.demand_slots, self.diagnostics = demand_slots, diagnostics
+        self.merge, self.dispatch = merge, dispatch
+        self.resident_graphs = resident_graphs
+        self.cache = ExpertCache(sizes, (len(hot_keys) + speculative_slots) * self.size, [self.size] * demand_slots,
+                                 policy="LRU", initial_hotset=hot_keys)
+        self.executor = ExpertExecutor(self.cache, masters, device, pinned_source_mode=source_mode,
+                                       cpu_backend=cpu_backend, streams=streams, capture_events=capture_events,
+                                       cache_storage=cache_storage, staging_storage=staging_storage)
+        self.device = self.executor.device
+        self.pending = {}
+        self.transient = set()
+        self.forecasts = {}
+        self.prediction_counts = {p: dict(hits=0, total=0) for p in ("prefill", "decode")}
+        self._ws = {}
+        self._pws = {}
+        self._graphs = {}
+        self._pinned_counts = torch.empty(2 * self.E + 64, dtype=torch.int32, pin_memory=True)
+        self._copy_done = torch.cuda.Event()
+        try:
+            for key in hot_keys:
+                self.executor.finish_load(self.executor.load(key, origin="initial"), wait=True)
+            self.initial_stats = self.cache.stats()
+        except BaseException:
+            self.close()
+            raise
+
+    # ------------------------------------------------------------ helpers
+
+    def _workspace(self, T, k):
+        ws = self._ws.get(k)
+        if ws is None or ws.max_tokens < T:
+            cap = max(T, 1 if ws is None else 2 * ws.max_tokens)
+            ws = L.MoEWorkspace(cap, self.H, self.I, self.E, k, self.device)
+            self._ws[k] = ws
+        return ws
+
+    def _pred_workspace(self, T, k):
+        ws = self._pws.get(k)
+        if ws is None or ws.max_tokens < T:
+            cap = max(T, 1 if ws is None else 2 * ws.max_tokens)
+            ws = L.MoEWorkspace(cap, self.H, self.I, self.E, k, self.device, route_only=True)
+            self._pws[k] = ws
+        return ws
+
+    def _key(self, layer, e):
+        return ExpertKey(layer, e, "bf16")
+
+    def poll(self, wait=False):
+        for key, ticket in list(self.pending.items()):
+            if self.executor.finish_load(ticket, wait=wait):
+                del self.pending[key]
+
+    def _retire_current(self, layer, *, wait):
+        unfinished = set(self.cache.unfinished_demand_keys)
+        for key in list(self.transient):
+            if key.layer != layer or key in unfinished:
+                continue
+            if key in self.pending:
+                if not self.executor.finish_load(self.pending[key], wait=wait):
+                    continue
+                del self.pending[key]
+            view = self.cache.lookup(key)
+            if view is not None and view.state == "ready" and view.pool == "cache":
+                self.cache.evict(key)
+            self.transient.discard(key)
+        self.executor.reclaim()
+
+    def _layer_fully_resident(self, layer):
+        for e in range(self.E):
+            v = self.cache.lookup(self._key(layer, e))
+            if v is None or v.state != "ready" or v.pool != "cache":
+                return False
+        return True
+
+    # ------------------------------------------------------------ forward
+
+    def forward(self, inputs, gate, *, layer, step, request="pdscope", next_gate=None, top_k=8, normalize=True,
+                attention_ms=0., prefetch=True, bias=None):
+        if (inputs.ndim != 2 or (step > 0 and inputs.shape[0] != 1) or (step == 0 and inputs.shape[0] < 2)
+                or layer not in self.layers):
+            raise ValueError("invalid prefill/decode activation or layer")
+        if inputs.device != self.device or inputs.dtype != torch.bfloat16:
+            raise ValueError("inputs must be bf16 on the runtime device")
+        phase = "prefill" if step == 0 else "decode"
+        T, H = inputs.shape
+        E, k = self.E, top_k
+        x = inputs.contiguous()
+        ws = self._workspace(T, k)
+        cur = torch.cuda.current_stream(self.device)
+        key = lambda e: self._key(layer, e)  # noqa: E731
+        nkey = lambda e: self._key(layer + 1, e)  # noqa: E731
+        self.poll()
+        before = self.cache.stats()
+        graph_path = (self.resident_graphs and phase == "decode" and next_gate is None and bias is None
+                      and self._layer_fully_resident(layer))
+
+        # ---- 1-2: route (+ predictor), grouping, one D2H of the demand
+        out = torch.empty((T, H), dtype=torch.bfloat16, device=self.device)
+        if graph_path:
+            logits, ids, weights = self._replay_decode_graph(layer, x, gate, normalize, k, out)
+        else:
+            logits, ids, weights = L.route(x, gate, ws, normalize=normalize, bias=bias)
+        predict = prefetch and next_gate is not None
+        nws = None
+        if predict:
+            nws = self._pred_workspace(T, k)
+            _, nids, _ = L.route(x, next_gate, nws, normalize=normalize)
+            ops.route_hist(nids, E, out=nws.hist)
+        _, _, _, packed = ws.views(T)
+        if T > 1:
+            ops.pack(ids, E, out=packed)
+            counts_dev = packed.counts
+        else:
+            counts_dev = ids.reshape(-1)
+        host = self._pinned_counts
+        n0 = counts_dev.numel()
+        host[:n0].copy_(counts_dev, non_blocking=True)
+        if predict:
+            host[n0:n0 + E].copy_(nws.hist, non_blocking=True)
+        self._copy_done.record(cur)
+        self._copy_done.synchronize()
+        if T > 1:
+            counts = {e: int(c) for e, c in enumerate(host[:E].tolist()) if c}
+        else:
+            sel = host[:k].tolist()
+            if len(set(sel)) != k:
+                raise AssertionError("decode routing selected duplicate experts")
+            counts = {e: 1 for e in sel}
+        next_counts = ({e: int(c) for e, c in enumerate(host[n0:n0 + E].tolist()) if c} if predict else {})
+        if sum(counts.values()) != T * k:
+            raise AssertionError("lost or duplicated routed assignment")
+
+        identity = DemandID(request, step, layer)
+        observations = self.cache.on_demand(identity, {key(e): n for e, n in counts.items()})
+        prior = self.forecasts.pop((request, step, layer), None)
+        if prior:
+            self.prediction_counts[phase]["hits"] += len(set(prior) & set(counts))
+            self.prediction_counts[phase]["total"] += len(prior)
+        observed = dict(self.prediction_counts[phase])
+
+        # ---- plan: every expert on the GPU; resident first, misses through staging
+        resident = sorted((e for e in counts if self.cache.lookup(key(e)) is not None),
+                          key=lambda e: (-counts[e], e))
+        demand = sorted((e for e in counts if e not in set(resident)), key=lambda e: (-counts[e], e))
+        for e in resident:
+            view = self.cache.lookup(key(e))
+            if view.state == "loading":
+                self.executor.finish_load(view.ticket, wait=True)
+                self.pending.pop(key(e), None)
+
+        ex = self.executor
+        slots_dev = None
+        tasks = []
+
+        def require_copies(experts):
+            missing = [e for e in experts if ex.table_entry(layer, e) == 0]
+            if missing:
+                raise AssertionError(f"experts {missing} of layer {layer} have no ready device copy")
+        decode_fast = (T == 1 and not demand and not graph_path)
+        if T == 1 and demand:
+            ops.pack(ids, E, out=packed)  # decode misses take the grouped path
+        if graph_path:
+            # the replay already produced `out`; account the uses it made
+            tasks.append(ex.gpu_group([key(e) for e in resident], lambda: None, wait_for=cur))
+        elif resident:
+            ex.table(layer, E)
+            require_copies(resident if not decode_fast else sorted(counts))
+            slots_dev = ex.upload_table(layer, E, ex.compute_stream)
+            if decode_fast:
+                def launch():
+                    ops.swiglu_decode(x, ids, weights, slots_dev, H, self.I, ws.h_ws, out)
+            else:
+                sel_dev = ex.upload_ints(resident, ex.compute_stream)
+
+                def launch():
+                    self._grouped(x, packed, sel_dev, T, k, slots_dev, ws)
+            tasks.append(ex.gpu_group([key(e) for e in resident], launch, input_ref=x, wait_for=cur))
+
+        # ---- demand misses through the staging slots
+        ping_pong = []
+        if demand:
+            depth = max(1, min(self.demand_slots - 1 if phase == "prefill" else 1, len(demand)))
+            inflight = []
+            nxt = 0
+            while nxt < depth:
+                inflight.append(ex.load(key(demand[nxt]), admit=False))
+                nxt += 1
+            for e in demand:
+                ticket = inflight.pop(0)
+                ex.finish_load(ticket, wait=True)
+                ex.table(layer, E)
+                require_copies([e])
+                tab = ex.upload_table(layer, E, ex.compute_stream)
+                sel_dev = ex.upload_ints([e], ex.compute_stream)
+
+                def launch(sel_dev=sel_dev, tab=tab):
+                    self._grouped(x, packed, sel_dev, T, k, tab, ws)
+                comp = ex.gpu_group([key(e)], launch, input_ref=x, wait_for=cur)
+                ping_pong.append(dict(expert=e, slot=ticket.slot, generation=ticket.generation))
+                if nxt < len(demand):
+                    inflight.append(ex.load(key(demand[nxt]), admit=False))
+                    nxt += 1
+                if len({t.slot for t in inflight}) != len(inflight):
+                    raise AssertionError("an in-flight copy reuses a live consumer slot")
+                ex.finish_gpu(comp, wait=True)
+
+        # ---- retire this layer's speculation, prefetch the next layer's forecast
+        self._retire_current(layer, wait=True)
+        issued, skipped = [], []
+        if predict and (layer + 1) in self.layers:
+            forecast = sorted(next_counts, key=lambda e: (-next_counts[e], e))
+            for e in forecast:
+                target = nkey(e)
+                if self.cache.lookup(target) is not None:
+                    continue
+                if len(self.transient) >= self.speculative_slots:
+                    skipped.append(e)
+                    continue
+                try:
+                    ticket = ex.load(target, origin="prefetch")
+                except Exception as err:  # CapacityBlocked: no evictable bytes
+                    if type(err).__name__ != "CapacityBlocked":
+                        raise
+                    skipped.append(e)
+                    continue
+                self.pending[target] = ticket
+                self.transient.add(target)
+                issued.append(e)
+            if issued:
+                self.forecasts[(request, step, layer + 1)] = tuple(issued)
+
+        # ---- finish GPU work, merge in token order
+        for task in tasks:
+            ex.finish_gpu(task, wait=True)
+        if not (decode_fast or graph_path):
+            with torch.cuda.stream(ex.compute_stream):
+                ops.merge(ws.y, packed.row_of, weights, out)
+        done = torch.cuda.Event()
+        done.record(ex.compute_stream)
+        cur.wait_event(done)
+        self.cache.end_demand(identity)
+        self._retire_current(layer, wait=True)
+        self.poll()
+        if self.diagnostics and any(self.cache.lookup(h) is None for h in self.hot):
+            raise AssertionError("speculation evicted a charged static hot copy")
+        after = self.cache.stats()
+        delta = {kk: v - before.get(kk, 0) for kk, v in after.items()}
+        if delta.get("cpu_completed_experts", 0) + delta.get("gpu_completed_experts", 0) != len(counts):
+            raise AssertionError("lost or duplicated routed expert")
+        routing = Routing(logits.clone(), ids.long(), weights.clone())
+        placements = {e: "gpu" for e in sorted(counts)}
+        decision = dict(phase=phase, mode="gpu_all", cpu_queue=[], gpu_resident_queue=resident,
+                        on_demand_queue=demand, prefetch_queue=issued, unload_queue=[], placements=placements)
+        row = dict(phase=phase, step=step, layer=layer, token_counts=counts, decision=decision,
+                   prefetch_issued=issued, prefetch_capacity_skipped=skipped, next_prediction_counts=next_counts,
+                   causal_hit_counts=observed, predictor="next_layer_gate_on_current_activation",
+                   ready_at_reveal=sum(o.ready_hit for o in observations),
+                   loading_at_reveal=sum(o.state_at_reveal == "loading" for o in observations),
+                   counters=delta, ping_pong_slots=ping_pong, demand_slots=self.demand_slots,
+                   decode_path=("graph" if graph_path else "fused_gemv" if decode_fast else "grouped")
+                   if phase == "decode" else "grouped",
+                   measured_performance=False)
+        return out, routing, row
+
+    def _grouped(self, x, packed, sel_dev, T, k, slots_dev, ws):
+        bm = ops.grouped_block_m((T * k) // max(1, self.E))
+        nsel = sel_dev.numel()
+        tile_start = ws.tile_start[:nsel + 1]
+        ops.schedule(packed.counts, sel_dev, bm, out=tile_start)
+        max_tiles = (T * k + bm - 1) // bm + nsel
+        ops.swiglu_grouped(x, packed.perm_token, packed.offsets, sel_dev, tile_start, max_tiles, bm, slots_dev, self.H,
+                           self.I, ws.h_ws, ws.y)
+
+    # ------------------------------------------------------------ resident decode graph
+
+    def _replay_decode_graph(self, layer, x, gate, normalize, k, out):
+        gkey = (layer, k, normalize, gate.data_ptr())
+        g = self._graphs.get(gkey)
+        ex = self.executor
+        ex.table(layer, self.E)
+        if any(ex.table_entry(layer, e) == 0 for e in range(self.E)):
+            raise AssertionError("decode graph replay needs every expert of the layer resident")
+        # the table tensor is captured by address; refresh its contents (copies
+        # may have moved between calls) on the replay stream
+        slots_dev = ex.upload_table(layer, self.E, torch.cuda.current_stream(self.device))
+        if g is None:
+            gws = L.MoEWorkspace(1, self.H, self.I, self.E, k, self.device)
+            xin = torch.empty_like(x)
+            gout = torch.empty_like(out)
+            xin.copy_(x)
+            torch.cuda.synchronize(self.device)
+            side = torch.cuda.Stream(self.device)
+            side.wait_stream(torch.cuda.current_stream(self.device))
+            with torch.cuda.stream(side):
+                L.route(xin, gate, gws, normalize=normalize)
+                ops.swiglu_decode(xin, gws.ids[:1], gws.weights[:1], slots_dev, self.H, self.I, gws.h_ws, gout)
+            torch.cuda.current_stream(self.device).wait_stream(side)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                L.route(xin, gate, gws, normalize=normalize)
+                ops.swiglu_decode(xin, gws.ids[:1], gws.weights[:1], slots_dev, self.H, self.I, gws.h_ws, gout)
+            g = (graph, xin, gout, gws, slots_dev)
+            self._graphs[gkey] = g
+        graph, xin, gout, gws, _ = g
+        xin.copy_(x)
+        graph.replay()
+        out.copy_(gout)
+        return gws.logits[:1], gws.ids[:1], gws.weights[:1]
+
+    def close(self):
+        self._graphs.clear()
+        self.executor.shutdown()

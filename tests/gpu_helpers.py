@@ -46,3 +46,24 @@ def logits_within_accumulation_error(kern, orc_exact, x_u16, gate_u16, bf16_to_f
     diff = np.abs(bf16_to_f32(kern).astype(np.float64) - bf16_to_f32(orc_exact))
     ok = bool(np.all((d <= 1) | (diff <= bound)))
     return ok, int((d > 0).sum())
+
+
+def oracle_layer_given_routing(orc, x_u16, ids, w_u16, experts_u16, H, I):
+    """Oracle expert path + merge for a given routing (ids int [T,k], weights bf16 bits)."""
+    E = experts_u16.shape[0]
+    p = orc.pack(np.ascontiguousarray(ids, dtype=np.int32), E)
+    xg = x_u16[p["perm_token"]]
+    y = np.empty((ids.size, H), np.uint16)
+    IH = I * H
+    for e in np.nonzero(p["counts"])[0]:
+        a, b = p["offsets"][e], p["offsets"][e + 1]
+        blk = experts_u16[e]
+        y[a:b] = orc.expert_forward(xg[a:b], blk[:IH].reshape(I, H), blk[IH:2 * IH].reshape(I, H),
+                                    blk[2 * IH:].reshape(H, I))
+    return orc.merge(y, p["row_of"], w_u16), y, p
+
+
+def assert_layer_close(orc, out, ref_u16):
+    m = err_metrics(orc.bf16_to_f32(u16(out)), orc.bf16_to_f32(ref_u16))
+    assert m["max_rel"] <= MAX_REL and m["mean_abs"] <= MEAN_ABS, m
+    return m

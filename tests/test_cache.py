@@ -1,0 +1,196 @@
+"""Residency ledger (pdscope_amd.cache) lifecycle rules, on the CPU.
+
+The rules follow expertbench/cache.py:136-662: staging fallback to the
+smallest free fitting slot (:531-537), CapacityBlocked without side effects,
+release-frees-staging (:621-624), LRU/LFU eviction, and CacheError on every
+illegal transition.
+"""
+import random
+
+import pytest
+
+from pdscope_amd.cache import CacheError, CapacityBlocked, DemandID, ExpertCache, ExpertKey
+
+K = lambda l, e: ExpertKey(l, e, "bf16")  # noqa: E731
+
+
+def make(n_layers=2, E=8, size=10, cache_slots=3, staging=(10, 10), hot=(), policy="LRU"):
+    sizes = {K(l, e): size for l in range(n_layers) for e in range(E)}
+    return ExpertCache(sizes, cache_slots * size, list(staging), policy=policy, initial_hotset=hot)
+
+
+def load_ready(c, key, **kw):
+    t = c.begin_load(key, **kw)
+    c.submit(t)
+    c.complete_load(t)
+    return t
+
+
+def test_initial_hotset_then_demand_hits():
+    c = make(hot=(K(0, 0), K(0, 1)))
+    with pytest.raises(CacheError):  # hotset must be loaded first
+        c.on_demand(DemandID("r", 0, 0), {K(0, 0): 3})
+    for k in (K(0, 0), K(0, 1)):
+        load_ready(c, k, origin="initial")
+    obs = c.on_demand(DemandID("r", 0, 0), {K(0, 0): 3, K(0, 5): 1})
+    assert [o.ready_hit for o in obs] == [True, False]
+    h = c.acquire(K(0, 0))
+    c.release(h)
+    assert c.unfinished_demand_keys == (K(0, 5),)
+    with pytest.raises(CacheError):
+        c.end_demand(DemandID("r", 0, 0))
+    c.finish_cpu(K(0, 5))
+    c.end_demand(DemandID("r", 0, 0))
+    st = c.stats()
+    assert st["gpu_completed_experts"] == 1 and st["cpu_completed_experts"] == 1
+
+
+def test_staging_fallback_picks_smallest_free_slot_and_frees_on_release():
+    c = make(cache_slots=0, staging=(30, 10, 10))
+    c.on_demand(DemandID("r", 0, 0), {K(0, 1): 1, K(0, 2): 1, K(0, 3): 1, K(0, 4): 1})
+    t1 = c.begin_load(K(0, 1))
+    t2 = c.begin_load(K(0, 2))
+    t3 = c.begin_load(K(0, 3))
+    assert (t1.pool, t1.slot) == ("demand_staging", 1)   # min((capacity, index))
+    assert (t2.slot, t3.slot) == (2, 0)
+    with pytest.raises(CapacityBlocked):
+        c.begin_load(K(0, 4))
+    assert c.lookup(K(0, 4)) is None                       # no side effect
+    c.submit(t1)
+    c.complete_load(t1)
+    h = c.acquire(K(0, 1))
+    c.release(h)
+    assert c.lookup(K(0, 1)) is None                       # staged misses never stay
+    assert t1 in c.take_retired()
+    t4 = c.begin_load(K(0, 4))
+    assert t4.slot == 1
+
+
+def test_lru_eviction_order_and_protection():
+    c = make(cache_slots=2, staging=(10,))
+    c.on_demand(DemandID("r", 0, 0), {K(0, 0): 1})
+    load_ready(c, K(0, 0))
+    c.release(c.acquire(K(0, 0)))
+    c.end_demand(DemandID("r", 0, 0))
+    c.on_demand(DemandID("r", 0, 1), {K(1, 0): 1})
+    load_ready(c, K(1, 0))
+    c.release(c.acquire(K(1, 0)))
+    c.end_demand(DemandID("r", 0, 1))
+    # cache full (2 slots): a prefetch evicts the least recently demanded copy
+    load_ready(c, K(1, 5), origin="prefetch")
+    assert c.lookup(K(0, 0)) is None and c.lookup(K(1, 0)) is not None
+    assert c.stats()["evictions"] == 1
+    # protected copies go last
+    c.set_protected([K(1, 0)])
+    load_ready(c, K(1, 6), origin="prefetch")
+    assert c.lookup(K(1, 0)) is not None and c.lookup(K(1, 5)) is None
+
+
+def test_lfu_prefers_rarely_used():
+    c = make(cache_slots=2, staging=(10,), policy="LFU")
+    for step, key in enumerate([K(0, 0), K(0, 0), K(0, 1)]):
+        c.on_demand(DemandID("r", step, 0), {key: 1})
+        if c.lookup(key) is None:
+            load_ready(c, key)
+        c.release(c.acquire(key))
+        c.end_demand(DemandID("r", step, 0))
+    # K(0,0) was demanded twice, K(0,1) once but more recently: LFU evicts K(0,1)
+    c.on_demand(DemandID("r", 3, 0), {K(0, 7): 1})
+    t = c.begin_load(K(0, 7))
+    assert t.pool == "cache" and c.lookup(K(0, 1)) is None and c.lookup(K(0, 0)) is not None
+
+
+def test_static_policy_never_evicts_and_misses_use_staging():
+    c = make(cache_slots=1, staging=(10,), hot=(K(0, 0),), policy="static")
+    load_ready(c, K(0, 0), origin="initial")
+    c.on_demand(DemandID("r", 0, 0), {K(0, 3): 1})
+    t = c.begin_load(K(0, 3))
+    assert t.pool == "demand_staging"
+    with pytest.raises(CacheError):
+        c.begin_load(K(1, 2), origin="prefetch")
+
+
+@pytest.mark.parametrize("bad", ["acquire_loading", "complete_unsubmitted", "double_submit", "foreign_ticket",
+                                 "prefetch_revealed", "late_initial", "out_of_order", "conflicting_demand",
+                                 "release_twice", "evict_in_use"])
+def test_illegal_transitions_raise(bad):
+    c = make()
+    c.on_demand(DemandID("r", 1, 0), {K(0, 1): 1, K(0, 2): 2})
+    t = c.begin_load(K(0, 1))
+    with pytest.raises(CacheError):
+        if bad == "acquire_loading":
+            c.acquire(K(0, 1))
+        elif bad == "complete_unsubmitted":
+            c.complete_load(t)
+        elif bad == "double_submit":
+            c.submit(t)
+            c.submit(t)
+        elif bad == "foreign_ticket":
+            other = make()
+            other.on_demand(DemandID("r", 1, 0), {K(0, 1): 1})
+            c.submit(other.begin_load(K(0, 1)))
+        elif bad == "prefetch_revealed":
+            c.begin_load(K(0, 2), origin="prefetch")
+        elif bad == "late_initial":
+            c.begin_load(K(1, 1), origin="initial")
+        elif bad == "out_of_order":
+            c.submit(t)
+            c.complete_load(t)
+            c.release(c.acquire(K(0, 1)))
+            c.finish_cpu(K(0, 2))
+            c.end_demand(DemandID("r", 1, 0))
+            c.on_demand(DemandID("r", 0, 1), {K(1, 1): 1})
+        elif bad == "conflicting_demand":
+            c.on_demand(DemandID("r", 1, 0), {K(0, 1): 5})
+        elif bad == "release_twice":
+            c.submit(t)
+            c.complete_load(t)
+            h = c.acquire(K(0, 1))
+            c.release(h)
+            c.release(h)
+        elif bad == "evict_in_use":
+            c.submit(t)
+            c.complete_load(t)
+            c.acquire(K(0, 1))
+            c.evict(K(0, 1))
+
+
+def test_random_lifecycles_keep_invariants():
+    rng = random.Random(5)
+    for trial in range(30):
+        E, size, slots = 12, 10, rng.randint(1, 5)
+        c = make(E=E, cache_slots=slots, staging=(10,) * rng.randint(1, 4), policy=rng.choice(["LRU", "LFU"]))
+        for step in range(12):
+            layer = step % 2
+            demand = {K(layer, e): rng.randint(1, 4) for e in rng.sample(range(E), rng.randint(1, 5))}
+            c.on_demand(DemandID("q", step, layer), demand)
+            for key in sorted(demand):
+                view = c.lookup(key)
+                if view is None:
+                    try:
+                        t = c.begin_load(key, admit=rng.random() < 0.7)
+                    except CapacityBlocked:
+                        c.finish_cpu(key)
+                        continue
+                    c.submit(t)
+                    c.complete_load(t)
+                elif view.state == "loading":
+                    c.complete_load(view.ticket)
+                c.release(c.acquire(key))
+            c.end_demand(DemandID("q", step, layer))
+            mem = c.memory()
+            assert mem["cache_payload_bytes"] <= mem["cache_capacity_bytes"]
+            assert mem["staging_occupied_slots"] == 0
+            if rng.random() < 0.5:
+                nxt = K(1 - layer, rng.randrange(E))
+                if c.lookup(nxt) is None:
+                    try:
+                        t = c.begin_load(nxt, origin="prefetch")
+                        c.submit(t)
+                        c.complete_load(t)
+                    except CapacityBlocked:
+                        pass
+        st = c.stats()
+        assert st["h2d_bytes_submitted"] == st["h2d_bytes_completed"]
+        assert (st.get("gpu_completed_experts", 0) + st.get("cpu_completed_experts", 0)
+                == st["physical_expert_demands"])

@@ -1,0 +1,227 @@
+"""GPU tests of the drop-in runtime (PDScopeCudaRuntime), executor staging and native dispatch.
+
+Every layer output is compared with the oracle applied to the runtime's own
+routing (ids/weights, themselves checked bit-exact against the oracle on
+the returned logits).  Ledger closure (transfers completed, no demand left
+open, every routed expert completed once) is asserted after each sequence.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from tests.gpu_helpers import assert_layer_close, oracle_layer_given_routing, u16
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def build(n_layers, H, I, E, k, seed=77):
+    from pdscope_amd import synthetic
+    from pdscope_amd.executor import masters_from_block
+    layers = [synthetic.make_layer(H, I, E, k, True, seed=seed + 100 * l, device=DEV) for l in range(n_layers)]
+    masters = {}
+    for l, lay in enumerate(layers):
+        masters.update(masters_from_block(l, lay.experts, E, H, I))
+    return layers, masters
+
+
+def check_output(orc, out, routing, x, layer_obj, H, I, k, normalize=True):
+    ids = routing.selected.cpu().numpy()
+    oi, ow = orc.route_from_logits(u16(routing.logits), k, normalize)
+    assert np.array_equal(ids, oi) and np.array_equal(u16(routing.weights), ow)
+    ref, _, _ = oracle_layer_given_routing(orc, u16(x), ids, u16(routing.weights), u16(layer_obj.experts), H, I)
+    assert_layer_close(orc, out, ref)
+
+
+def closure(rt):
+    st = rt.cache.stats()
+    assert st.get("h2d_bytes_submitted", 0) == st.get("h2d_bytes_completed", 0)
+    assert rt.cache.active_demand is None
+    assert not rt.executor.loads and not rt.executor.computes
+
+
+def test_runtime_prefill_then_decode_with_staging_and_prefetch(orc):
+    from pdscope_amd import synthetic
+    from pdscope_amd.cache import ExpertKey
+    from pdscope_amd.pdscope_runtime import PDScopeCudaRuntime
+    H, I, E, k = 256, 128, 32, 4
+    layers, masters = build(2, H, I, E, k)
+    hot = [ExpertKey(l, e, "bf16") for l in range(2) for e in range(6)]
+    rt = PDScopeCudaRuntime(masters, hot_keys=hot, speculative_slots=4, demand_slots=2)
+    gen = torch.Generator(device=DEV).manual_seed(3)
+    try:
+        for step, T in enumerate((16, 1, 1, 1)):
+            x = (torch.randn((T, H), generator=gen, device=DEV)).to(torch.bfloat16)
+            for l in range(2):
+                out, routing, row = rt.forward(x, layers[l].gate, layer=l, step=step, next_gate=
+                                               layers[l + 1].gate if l + 1 < 2 else None, top_k=k)
+                torch.cuda.synchronize()
+                check_output(orc, out, routing, x, layers[l], H, I, k)
+                assert set(row["decision"]["gpu_resident_queue"]) | set(row["decision"]["on_demand_queue"]) == \
+                    set(row["token_counts"])
+                x = torch.nn.functional.layer_norm((out.float() + x.float()), (H,)).to(torch.bfloat16)
+        closure(rt)
+        st = rt.cache.stats()
+        assert st.get("demand_loads_submitted", 0) > 0          # misses went through staging
+        assert st.get("prefetch_loads_submitted", 0) > 0        # the predictor prefetched
+        assert all(rt.cache.lookup(h) is not None for h in hot)  # hot set intact
+    finally:
+        rt.close()
+
+
+def test_runtime_qwen_demand_staging_eight_slots(orc):
+    from pdscope_amd import synthetic
+    from pdscope_amd.cache import ExpertKey
+    from pdscope_amd.pdscope_runtime import PDScopeCudaRuntime
+    q = synthetic.QWEN
+    layers, masters = build(1, q["H"], q["I"], q["E"], q["k"], seed=91)
+    hot = [ExpertKey(0, e, "bf16") for e in range(32)]
+    rt = PDScopeCudaRuntime(masters, hot_keys=hot, speculative_slots=0, demand_slots=8)
+    try:
+        x = synthetic.make_tokens(64, q["H"], seed=92)
+        out, routing, row = rt.forward(x, layers[0].gate, layer=0, step=0, top_k=8)
+        torch.cuda.synchronize()
+        check_output(orc, out, routing, x, layers[0], q["H"], q["I"], 8)
+        assert len(row["decision"]["on_demand_queue"]) > 50
+        assert {p["slot"] for p in row["ping_pong_slots"]} <= set(range(8))
+        closure(rt)
+    finally:
+        rt.close()
+
+
+def test_runtime_decode_graph_matches_eager(orc):
+    from pdscope_amd import layer, ops, synthetic
+    from pdscope_amd.cache import ExpertKey
+    from pdscope_amd.pdscope_runtime import PDScopeCudaRuntime
+    q = synthetic.QWEN
+    layers, masters = build(1, q["H"], q["I"], q["E"], q["k"], seed=93)
+    hot = [ExpertKey(0, e, "bf16") for e in range(q["E"])]
+    rt = PDScopeCudaRuntime(masters, hot_keys=hot, speculative_slots=0, resident_graphs=True)
+    slots = ops.slot_table([layers[0].experts[e] for e in range(q["E"])], DEV)
+    ws = layer.MoEWorkspace(1, q["H"], q["I"], q["E"], 8, DEV)
+    try:
+        # step 0 is a prefill (T >= 2); decode steps replay the captured graph
+        x0 = synthetic.make_tokens(4, q["H"], seed=94)
+        rt.forward(x0, layers[0].gate, layer=0, step=0)
+        for step in range(1, 5):
+            x = synthetic.make_tokens(1, q["H"], seed=94 + step)
+            out, routing, row = rt.forward(x, layers[0].gate, layer=0, step=step)
+            assert row["decode_path"] == "graph"
+            ref_out, _, ids, w = layer.moe_forward(x, layers[0].gate, slots, ws)
+            torch.cuda.synchronize()
+            assert torch.equal(out, ref_out) and torch.equal(routing.selected, ids.long())
+            check_output(orc, out, routing, x, layers[0], q["H"], q["I"], 8)
+        closure(rt)
+    finally:
+        rt.close()
+
+
+def test_runtime_rejects_bad_phase_shapes():
+    from pdscope_amd.cache import ExpertKey
+    from pdscope_amd.pdscope_runtime import PDScopeCudaRuntime
+    layers, masters = build(1, 256, 128, 32, 4)
+    rt = PDScopeCudaRuntime(masters, hot_keys=[ExpertKey(0, 0, "bf16")], speculative_slots=0)
+    try:
+        x1 = torch.zeros((1, 256), dtype=torch.bfloat16, device=DEV)
+        x2 = torch.zeros((2, 256), dtype=torch.bfloat16, device=DEV)
+        with pytest.raises(ValueError):
+            rt.forward(x1, layers[0].gate, layer=0, step=0)
+        with pytest.raises(ValueError):
+            rt.forward(x2, layers[0].gate, layer=0, step=1)
+        with pytest.raises(ValueError):
+            rt.forward(x2, layers[0].gate, layer=5, step=0)
+    finally:
+        rt.close()
+    with pytest.raises(ValueError):
+        PDScopeCudaRuntime(masters, hot_keys=[], speculative_slots=0, demand_slots=1)
+
+
+def test_executor_per_expert_hook_matches_oracle(orc):
+    from pdscope_amd.cache import DemandID, ExpertCache, ExpertKey
+    from pdscope_amd.executor import ExpertExecutor
+    H, I, E, k = 256, 128, 32, 4
+    layers, masters = build(1, H, I, E, k, seed=5)
+    sizes = {key: w.nbytes for key, w in masters.items()}
+    size = next(iter(sizes.values()))
+    cache = ExpertCache(sizes, 4 * size, [size, size])
+    ex = ExpertExecutor(cache, masters, 0)
+    try:
+        key = ExpertKey(0, 3, "bf16")
+        cache.on_demand(DemandID("r", 0, 0), {key: 7})
+        t = ex.load(key)
+        assert ex.finish_load(t, wait=True)
+        x = torch.randn((7, H), device=DEV).to(torch.bfloat16)
+        pend = ex.gpu(key, x)
+        y = ex.finish_gpu(pend, wait=True)
+        blk = u16(layers[0].experts[3])
+        ref = orc.expert_forward(u16(x), blk[:I * H].reshape(I, H), blk[I * H:2 * I * H].reshape(I, H),
+                                 blk[2 * I * H:].reshape(H, I))
+        assert_layer_close(orc, y, ref)
+        cache.end_demand(DemandID("r", 0, 0))
+        # the staged bytes equal the pinned master bytes
+        flat = ex.copies[t]
+        assert torch.equal(flat.cpu(), masters[key].flat.view(torch.uint8))
+    finally:
+        ex.shutdown()
+
+
+class _Pool:
+    def __init__(self):
+        self.q = []
+
+    def submit(self, task):
+        self.q.append(task)
+
+    def sync(self):
+        for t in self.q:
+            t()
+        self.q.clear()
+
+
+class _OracleLayer:
+    """CPU expert queue layer: forward_task runs the oracle expert per packed row."""
+
+    def __init__(self, orc, experts_u16, H, I):
+        self.orc, self.experts, self.H, self.I = orc, experts_u16, H, I
+
+    def forward_task(self, count_ptr, k, selected_ptr, coeff_ptr, in_ptr, out_ptr, flag):
+        def run():
+            n = ctypes.c_int32.from_address(count_ptr).value
+            sel = np.ctypeslib.as_array((ctypes.c_int64 * n).from_address(selected_ptr))
+            x = np.ctypeslib.as_array((ctypes.c_uint16 * (n * self.H)).from_address(in_ptr)).reshape(n, self.H)
+            out = np.ctypeslib.as_array((ctypes.c_uint16 * (n * self.H)).from_address(out_ptr)).reshape(n, self.H)
+            IH = self.I * self.H
+            for r in range(n):
+                blk = self.experts[sel[r]]
+                out[r] = self.orc.expert_forward(x[r:r + 1].copy(), blk[:IH].reshape(self.I, self.H),
+                                                 blk[IH:2 * IH].reshape(self.I, self.H),
+                                                 blk[2 * IH:].reshape(self.H, self.I))[0]
+        return run
+
+
+def test_native_dispatch_submit_and_merge(orc):
+    from pdscope_amd import pdscope_layer_dispatch as nd
+    H, I, E, k = 256, 128, 32, 4
+    layers, _ = build(1, H, I, E, k, seed=8)
+    experts = u16(layers[0].experts)
+    rows = 3
+    ids = [5, 17, 2]
+    row = torch.randn(H).to(torch.bfloat16)
+    packed = torch.empty((rows, H), dtype=torch.bfloat16)
+    block = torch.empty((rows, H), dtype=torch.bfloat16)
+    count, sel, coeff = ctypes.c_int32(0), (ctypes.c_int64 * rows)(), (ctypes.c_float * rows)()
+    scratch = torch.empty((rows, H), dtype=torch.bfloat16, device=DEV)
+    out = torch.zeros((1, H), dtype=torch.bfloat16, device=DEV)
+    tokens = torch.zeros(rows, dtype=torch.long, device=DEV)
+    weights = torch.tensor([0.5, 0.25, 0.125], dtype=torch.bfloat16, device=DEV)
+    res = nd.submit_and_merge(_Pool(), _OracleLayer(orc, experts, H, I), row.data_ptr(), rows, H * 2,
+                              packed.data_ptr(), block.data_ptr(), scratch, ctypes.addressof(count),
+                              ctypes.addressof(sel), ctypes.addressof(coeff), ids, out, tokens, weights)
+    torch.cuda.synchronize()
+    assert res is out
+    ref = torch.zeros(H, dtype=torch.bfloat16)
+    for r in range(rows):
+        ref = (ref.float() + (block[r] * weights.cpu()[r]).float()).to(torch.bfloat16)
+    assert torch.equal(out.cpu()[0], ref)
