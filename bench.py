@@ -120,51 +120,72 @@ def run_prefill(T, steps, warmup, n_layers, device, seed0):
 
 
 def run_decode(steps, warmup, n_layers, device, seed0):
-    """One hipGraph per layer copy (route + gate/up + down/merge); events around each replay."""
+    """All layer copies captured in ONE hipGraph (as a decode step over a stack
+    of resident layers replays them); HIP events bracket every replay and the
+    per-layer time is the replay time over the layer count.  The same is done
+    for the three-launch path (route + decode GEMV + down/merge) for reference."""
     import torch
-    from pdscope_amd import layer, synthetic
+    from pdscope_amd import layer, ops, synthetic
     layers = build_layers(n_layers, device, seed0)
     xs = [synthetic.make_tokens(1, H, seed=seed0 + 7 + 1000 * i, device=device) for i in range(n_layers)]
-    ws = layer.MoEWorkspace(1, H, I, E, K_TOP, device)
-    side = torch.cuda.Stream(device)
-    side.wait_stream(torch.cuda.current_stream(device))
-    with torch.cuda.stream(side):
-        for i in range(n_layers):
-            layer.moe_forward(xs[i], layers[i][0].gate, layers[i][1], ws)
-    torch.cuda.current_stream(device).wait_stream(side)
-    torch.cuda.synchronize(device)
-    graphs = []
-    for i in range(n_layers):
+    wss = [layer.MoEWorkspace(1, H, I, E, K_TOP, device) for _ in range(n_layers)]
+    stream = torch.cuda.current_stream(device)
+
+    def capture(fused):
+        side = torch.cuda.Stream(device)
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            for i in range(n_layers):
+                layer.moe_forward(xs[i], layers[i][0].gate, layers[i][1], wss[i], fused_decode=fused)
+        stream.wait_stream(side)
+        torch.cuda.synchronize(device)
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            layer.moe_forward(xs[i], layers[i][0].gate, layers[i][1], ws)
-        graphs.append(g)
-    torch.cuda.synchronize(device)
-    # graph replay must equal eager execution
-    eager = []
-    for i in range(n_layers):
-        layer.moe_forward(xs[i], layers[i][0].gate, layers[i][1], ws)
-        eager.append(ws.out[:1].clone())
-    for i in range(n_layers):
-        graphs[i].replay()
-        if not torch.equal(ws.out[:1], eager[i]):
-            raise AssertionError("decode graph replay differs from eager execution")
-    for i in range(warmup):
-        graphs[i % n_layers].replay()
-    stream = torch.cuda.current_stream(device)
-    events = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
-    torch.cuda.synchronize(device)
-    t0 = time.perf_counter()
-    events[0].record(stream)
-    for i in range(steps):
-        graphs[i % n_layers].replay()
-        events[i + 1].record(stream)
-    torch.cuda.synchronize(device)
-    wall = time.perf_counter() - t0
-    layer_ms = [events[i].elapsed_time(events[i + 1]) for i in range(steps)]
-    return dict(T=1, wall_s=wall, ms_per_step=wall / steps * 1e3, tok_s=steps / wall,
+            for i in range(n_layers):
+                layer.moe_forward(xs[i], layers[i][0].gate, layers[i][1], wss[i], fused_decode=fused)
+        torch.cuda.synchronize(device)
+        return g
+
+    def timed(g, nsteps, nwarm):
+        # graph replay must equal eager execution, layer by layer
+        eager = []
+        for i in range(n_layers):
+            layer.moe_forward(xs[i], layers[i][0].gate, layers[i][1], wss[i])
+            eager.append(wss[i].out[:1].clone())
+        g.replay()
+        torch.cuda.synchronize(device)
+        for i in range(n_layers):
+            if not torch.equal(wss[i].out[:1], eager[i]):
+                raise AssertionError("decode graph replay differs from eager execution")
+        reps = max(1, nsteps // n_layers)
+        for _ in range(max(1, nwarm // n_layers)):
+            g.replay()
+        events = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+        torch.cuda.synchronize(device)
+        t0 = time.perf_counter()
+        events[0].record(stream)
+        for r in range(reps):
+            g.replay()
+            events[r + 1].record(stream)
+        torch.cuda.synchronize(device)
+        wall = time.perf_counter() - t0
+        layer_ms = [events[r].elapsed_time(events[r + 1]) / n_layers for r in range(reps)]
+        return reps * n_layers, wall, layer_ms
+
+    fused = ops.decode_layer_supported(H, I, E, K_TOP, device)
+    g = capture(True)
+    n_steps, wall, layer_ms = timed(g, steps, warmup)
+    if fused and ops.decode_workspace_error(device, H):
+        raise AssertionError("a bounded wait of the fused decode kernel gave up")
+    g3 = capture(False)
+    _, _, layer_ms3 = timed(g3, steps, warmup)
+    kernel = ("decode_layer_kernel (route + top-k + gate/up + down/merge in one launch), "
+              f"{n_layers} layers per hipGraph" if fused else
+              f"route_gemv + decode_gateup + decode_down, {n_layers} layers per hipGraph")
+    return dict(T=1, wall_s=wall, ms_per_step=wall / n_steps * 1e3, tok_s=n_steps / wall, kernel=kernel,
                 layer_ms_mean=statistics.mean(layer_ms), layer_ms_median=statistics.median(layer_ms),
-                layers=n_layers, first_layer=layers[0], first_x=xs[0], ws=ws)
+                three_launch_layer_ms=statistics.median(layer_ms3), steps_run=n_steps,
+                layers=n_layers, first_layer=layers[0], first_x=xs[0], ws=wss[0])
 
 
 # ----------------------------------------------------------------------------- CPU baseline
@@ -284,8 +305,9 @@ def decode_record(res):
     t = res["layer_ms_mean"] / 1e3
     hbm = dict(bound="hbm", achieved=layer_bytes / t / 1e9, peak=HBM_PEAK_GBS, unit="GB/s")
     hbm["frac"] = hbm["achieved"] / hbm["peak"]
-    return dict(tok_s=res["tok_s"], ms_per_step=res["ms_per_step"], kernel="decode layer hipGraph (3 kernels)",
+    return dict(tok_s=res["tok_s"], ms_per_step=res["ms_per_step"], kernel=res["kernel"],
                 kernel_ms_mean=res["layer_ms_mean"], kernel_ms_median=res["layer_ms_median"],
+                three_launch_layer_ms=res["three_launch_layer_ms"],
                 kernel_bytes=layer_bytes, layers_rotated=res["layers"], hbm=hbm,
                 layer_hbm_gbs=layer_bytes / (res["ms_per_step"] / 1e3) / 1e9)
 
@@ -321,7 +343,7 @@ def main():
         else:
             res = run_decode(steps, warmup, nl, device, 20261011)
             rec = decode_record(res)
-        rec["steps"], rec["warmup"] = steps, warmup
+        rec["steps"], rec["warmup"] = res.get("steps_run", steps), warmup
         log(f"[bench] {wl}: {rec['tok_s']:.1f} tok/s, {rec['ms_per_step']:.4f} ms/step, kernel "
             f"{rec['kernel_ms_mean']:.4f} ms, {rec['hbm']['achieved']:.0f} GB/s")
         records[wl] = rec

@@ -139,6 +139,32 @@ int pdscope_swiglu_decode(const void *x, const int32_t *ids, const void *w, int 
                           void *stream);
 
 /*
+ * A1+A4+A8 for one decode token in ONE launch: replaces route
+ * (expertbench/adapters/qwen.py:140-152), the per-expert decode submissions
+ * (expertbench/pdscope_runtime.py:326-350, executor.py:454-488, including the
+ * resident-graph replay of executor.py:113-138) and the merge
+ * (pdscope_runtime.py:450-469).  Results are bitwise those of
+ * pdscope_route_topk followed by pdscope_swiglu_decode (same arguments).
+ * x [H], gate [E,H], bias [E] fp32 or NULL, logits [E] bf16, ids [k] int32,
+ * weights [k] bf16, probs [E] fp32 or NULL, h_ws [k*I] bf16, out [H] bf16.
+ * workspace: pdscope_decode_workspace_bytes() bytes, zero-filled once by the
+ * caller and then owned by the kernel (per-block epochs and the words that
+ * carry logits and h between blocks; nothing to reset between launches).
+ * One workspace serves every launch of one hidden size H on one stream;
+ * launches that overlap in time, or of another H, need their own.
+ * 32-bit word 1024 of the workspace is a sticky error flag: non-zero if a
+ * bounded internal wait gave up (the output is then invalid).
+ * Returns 1 (EINVAL) for shapes outside the kernel (see
+ * pdscope_decode_layer_supported; E must be even, k <= 8) and when its grid
+ * of H/4 blocks cannot be resident at once on the current device.
+ */
+size_t pdscope_decode_workspace_bytes(void);
+int pdscope_decode_layer_supported(int H, int I, int E, int k);
+int pdscope_decode_layer(const void *x, const void *gate, const float *bias, int H, int E, int k,
+                         int normalize, const void *const *slots, int I, void *logits, int32_t *ids,
+                         void *weights, float *probs, void *h_ws, void *out, void *workspace, void *stream);
+
+/*
  * A7 demand staging: replaces the three per-projection non_blocking copies
  * (expertbench/executor.py:341-363).  One hipMemcpyAsync of `bytes` from
  * page-locked host memory into a cache or staging slot on `stream`, then

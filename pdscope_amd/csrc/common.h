@@ -43,9 +43,25 @@ __device__ __forceinline__ float bf16_round(float f) { return bf2f(f2bf(f)); }
 __device__ __forceinline__ float lo_bf(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi_bf(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
+// Global-address-space views.  Pointers read from memory (slot tables) are
+// generic to the compiler, which then emits flat loads; flat loads also
+// count against the LDS wait counter, so every LDS wait would drain them.
+// Casting to address space 1 keeps them global loads.
+typedef __attribute__((address_space(1))) const u32x4_t g_u32x4_t;
+
+__device__ __forceinline__ const g_u32x4_t *gptr(const void *p) {
+    return (const g_u32x4_t *)(reinterpret_cast<uintptr_t>(p));
+}
+
 // 16-byte streaming load that bypasses cache allocation (weights read once)
 __device__ __forceinline__ uint4 ld_nt(const void *p) {
-    u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
+    u32x4_t v = __builtin_nontemporal_load(gptr(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// plain 16-byte global load
+__device__ __forceinline__ uint4 ld_g(const void *p) {
+    u32x4_t v = *gptr(p);
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 

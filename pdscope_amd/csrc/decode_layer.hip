@@ -1,0 +1,428 @@
+// K4f: the whole T == 1 MoE layer in one persistent launch: router logits,
+// softmax / top-k / renorm, the SwiGLU gate/up GEMV of the k routed experts
+// and their down projection with the weighted merge.
+// Restates, for one decode token, route (expertbench/adapters/qwen.py:140-152),
+// the per-expert decode submissions of PDScopeCudaRuntime.forward
+// (expertbench/pdscope_runtime.py:326-350; expert_forward, qwen.py:87-90) and
+// the merge (pdscope_runtime.py:450-469).
+//
+// Grid: one wave per output column (H / 4 blocks of 4 waves), sized so that
+// every block is resident at once (checked against the occupancy of this
+// kernel on the current device).  Phases:
+//   1. blocks 0 .. E/4-1: one wave per router row -> bf16 logit;
+//   2. every block collects the E logits and runs softmax / top-k itself
+//      (block-wide ranking), so no further hop publishes the routing;
+//   3. every wave issues the loads of its P (gate, up) row pairs of the
+//      routed experts (16-byte non-temporal loads);
+//   4. gate/up dot products -> h; then the wave issues its down-projection
+//      rows (two slots x four output columns), which land while h is
+//      handed between blocks;
+//   5. every block collects all of h, finishes its down rows and merges in
+//      slot order: out[j] = bf16(sum_s w_s * bf16(h_s . down_s[j])).
+//
+// Cross-block hand-off without read-modify-write atomics.  Same-address
+// atomics from hundreds of blocks serialise at the memory side (~14 ns
+// each), and a release fence per block writes back the whole XCD L2, so a
+// counter barrier costs several microseconds.  Instead every published
+// value is one 32-bit word (epoch << 16 | bf16 bits) written with
+// device-scope relaxed stores (write-through) and read with device-scope
+// relaxed loads until its epoch is the current one.  A value and its
+// validity travel in one word, so no ordering between locations is needed.
+// Each block publishes its words with one thread, in 8-byte stores
+// (logits: 4 per block in a line of their own; h: 4P consecutive words).
+// The epoch is a per-block counter kept in the workspace (all blocks of a
+// launch see the same value because every launch runs every block once);
+// it cycles through 1..65535, never 0, so a zero-filled workspace holds no
+// valid word.  Polling is bounded: each thread has kSpinBudget polls for the
+// whole launch; when they are spent it sets the sticky error word and uses
+// what it read, so the launch always drains.  Because the epochs advance
+// per block, one workspace serves one grid size (one H) on one stream.
+//
+// Per-lane arithmetic order equals route_gemv_kernel, decode_gateup_kernel
+// and decode_down_kernel, so the result is bitwise the result of the
+// three-launch path (pdscope_route_topk + pdscope_swiglu_decode).
+#include <mutex>
+#include <unordered_map>
+
+#include "common.h"
+#include "topk.h"
+
+namespace pd {
+
+// Polls one thread may spend over the whole launch (a normal launch needs a
+// few hundred at most); once spent, the thread stops waiting.
+constexpr uint32_t kSpinBudget = 1u << 16;
+
+constexpr int kDecodeMaxK = 8;
+constexpr int kDecodeMaxE = 256;
+constexpr int kDecodeMaxBlocks = 1024;
+constexpr int kDecodeMaxKI = 16384;  // k * I words of h
+
+// Workspace layout in 32-bit words (zero-filled once by the caller).
+constexpr int kWsEpoch = 0;                          // [kDecodeMaxBlocks] per-block epoch
+constexpr int kWsError = kDecodeMaxBlocks;           // sticky error word
+constexpr int kWsLogit = kWsError + 32;              // [kDecodeMaxE / 4] lines of 4 published logits
+constexpr int kWsH = kWsLogit + kDecodeMaxE * 8;     // [kDecodeMaxKI] published h
+constexpr int kWsWords = kWsH + kDecodeMaxKI;
+
+__device__ __forceinline__ uint64_t load_pair(const uint32_t *w) {
+    return __hip_atomic_load(reinterpret_cast<const uint64_t *>(w), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ bool pair_ready(uint64_t v, uint32_t epoch) {
+    return ((uint32_t)v >> 16) == epoch && (uint32_t)(v >> 48) == epoch;
+}
+
+// Collect `count` published words starting at w (count even, w 8-byte
+// aligned) into dst (LDS, 16-bit values), cooperatively: thread t takes the
+// word pairs t, t + nthreads, ...  B pair loads are issued together, then
+// the ones not yet current are re-read until they are.  `budget` is the
+// calling thread's remaining poll allowance for the launch.
+template <int B>
+__device__ __forceinline__ void collect(const uint32_t *w, int count, int t, int nthreads, uint32_t epoch,
+                                        uint32_t *err, uint32_t &budget, uint16_t *dst) {
+    const int pairs = count >> 1;
+    for (int j0 = t; j0 < pairs; j0 += B * nthreads) {
+        uint64_t v[B];
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const int j = j0 + b * nthreads;
+            v[b] = j < pairs ? load_pair(w + 2 * j) : 0;
+        }
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const int j = j0 + b * nthreads;
+            if (j >= pairs) continue;
+            while (!pair_ready(v[b], epoch)) {
+                if (budget == 0) {
+                    __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+                --budget;
+                __builtin_amdgcn_s_sleep(1);
+                v[b] = load_pair(w + 2 * j);
+            }
+            dst[2 * j] = (uint16_t)v[b];
+            dst[2 * j + 1] = (uint16_t)(v[b] >> 32);
+        }
+    }
+}
+
+// NCH: 16-byte chunks per lane of an H row (>= H/8/64); P: gate/up row pairs
+// per wave (>= k*I / waves); DC: 16-byte chunks per half-wave lane of a
+// down row (>= I/8/32).  Larger values than needed are masked.
+template <int NCH, int P, int DC>
+__global__ __launch_bounds__(256, 2) void decode_layer_kernel(
+    const uint16_t *__restrict__ x, const uint16_t *__restrict__ gate, const float *__restrict__ bias, int H,
+    int E, int k, int normalize, const uint16_t *const *__restrict__ slots, int I, uint16_t *__restrict__ logits,
+    int32_t *__restrict__ ids, uint16_t *__restrict__ weights, float *__restrict__ probs,
+    uint16_t *__restrict__ h_ws, uint16_t *__restrict__ out, uint32_t *ws) {
+    extern __shared__ uint4 s_h[];       // k * I bf16
+    __shared__ float s_logit[kDecodeMaxE];
+    __shared__ uint32_t s_pub[16];
+    __shared__ float s_y[kDecodeMaxK * 4];
+    __shared__ const uint16_t *s_slot[kDecodeMaxE];
+    __shared__ TopkScratch s_tk;
+    __shared__ uint32_t s_epoch;
+
+    const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
+    const int C = H >> 3, CI = I >> 3;
+    const int RB = (E + 3) / 4;
+    uint32_t *err = ws + kWsError;
+    uint32_t budget = kSpinBudget;
+
+    if (tid == 0) {
+        uint32_t ep = (__hip_atomic_load(ws + kWsEpoch + blockIdx.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u) &
+                      0xffffu;
+        s_epoch = ep ? ep : 1u;
+    }
+    // router rows first (blocks 0 .. RB-1): their latency starts the chain
+    const int e_route = blockIdx.x * 4 + wave;
+    const bool routes = (int)blockIdx.x < RB;
+    uint4 wv[NCH];
+    if (routes) {
+        const uint4 *wrow = reinterpret_cast<const uint4 *>(gate + (size_t)min(e_route, E - 1) * H);
+#pragma unroll
+        for (int j = 0; j < NCH; ++j) wv[j] = wrow[min(lane + 64 * j, C - 1)];
+    }
+    uint4 xv[NCH];
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) xv[j] = reinterpret_cast<const uint4 *>(x)[min(lane + 64 * j, C - 1)];
+    for (int e = tid; e < E; e += blockDim.x) s_slot[e] = slots[e];
+    __syncthreads();
+    const uint32_t epoch = s_epoch;
+
+    // ---- 1. router logits: block r computes experts 4r..4r+3 and publishes
+    // them as one 16-byte write into a 128-byte line of its own (one writer
+    // per line: partial writes of one line by many agents serialise)
+    if (routes) {
+        const int e = e_route;
+        uint32_t b = 0;
+        if (e < E) {
+            float a = 0.0f;
+#pragma unroll
+            for (int j = 0; j < NCH; ++j)
+                if (lane + 64 * j < C) a = dot8(xv[j], wv[j], a);
+            a = wave_sum(a);
+            b = f2bf(a);
+            if (lane == 0) logits[e] = (uint16_t)b;
+        }
+        if (lane == 0) s_pub[wave] = (epoch << 16) | b;
+        __syncthreads();
+        if (tid == 0) {
+            uint64_t *line = reinterpret_cast<uint64_t *>(ws + kWsLogit + blockIdx.x * 32);
+            __hip_atomic_store(line, (uint64_t)s_pub[0] | ((uint64_t)s_pub[1] << 32), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(line + 1, (uint64_t)s_pub[2] | ((uint64_t)s_pub[3] << 32), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+
+    // ---- 2. routing, computed by every block from the published logits
+    // (one wave collects them: pair j holds experts 2j, 2j+1 and sits in the
+    // line of route block j/2)
+    if (wave == 0) {
+        for (int j = lane; j < 2 * RB; j += 64) {
+            const uint32_t *w = ws + kWsLogit + (j >> 1) * 32 + (j & 1) * 2;
+            uint64_t v = load_pair(w);
+            while (!pair_ready(v, epoch)) {
+                if (budget == 0) {
+                    __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+                --budget;
+                __builtin_amdgcn_s_sleep(1);
+                v = load_pair(w);
+            }
+            if (2 * j < E) s_logit[2 * j] = bf2f((uint32_t)v & 0xffffu);
+            if (2 * j + 1 < E) s_logit[2 * j + 1] = bf2f((uint32_t)(v >> 32) & 0xffffu);
+        }
+    }
+    __syncthreads();
+    {
+        const bool pub = blockIdx.x == 0;
+        if (E <= 128)
+            topk_block<2>(s_logit, bias, E, k, normalize, pub ? ids : nullptr, pub ? weights : nullptr,
+                          pub ? probs : nullptr, &s_tk);
+        else
+            topk_block<4>(s_logit, bias, E, k, normalize, pub ? ids : nullptr, pub ? weights : nullptr,
+                          pub ? probs : nullptr, &s_tk);
+    }
+
+    // ---- 3. issue the gate/up weight loads of this wave; block b owns the
+    // 4P consecutive (gate, up) row pairs q = 4P*b + P*wave + p
+    const int KI = k * I;
+    const int q0 = blockIdx.x * 4 * P + wave * P;
+    uint4 gv[P][NCH], uv[P][NCH];
+    bool has[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const int q = min(q0 + p, KI - 1);
+        const int s = q / I, i = q - s * I;
+        const uint16_t *base = s_slot[s_tk.seli[s]];
+        // an expert without a ready copy reads the activation row instead
+        // (H elements, in bounds) and contributes h = 0
+        has[p] = base != nullptr;
+        const uint16_t *grow = base ? base + (size_t)i * H : x;
+        const uint16_t *urow = base ? base + (size_t)(I + i) * H : x;
+#pragma unroll
+        for (int j = 0; j < NCH; ++j) {
+            gv[p][j] = ld_nt(grow + 8 * min(lane + 64 * j, C - 1));
+            uv[p][j] = ld_nt(urow + 8 * min(lane + 64 * j, C - 1));
+        }
+    }
+    // ---- 4. gate/up -> h
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        float g = 0.0f, u = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NCH; ++j) {
+            if (lane + 64 * j < C) {
+                g = dot8(gv[p][j], xv[j], g);
+                u = dot8(uv[p][j], xv[j], u);
+            }
+        }
+        g = wave_sum(g);
+        u = wave_sum(u);
+        const int q = q0 + p;
+        if (lane == 0) {
+            const float a = bf16_round(silu_f32(bf16_round(g)));
+            const uint32_t hb = has[p] ? f2bf(a * bf16_round(u)) : 0u;
+            if (q < KI) h_ws[q] = (uint16_t)hb;
+            s_pub[wave * P + p] = (epoch << 16) | hb;
+        }
+    }
+    // down rows, issued once the gate/up rows are consumed (fewer loads in
+    // flight per wave streams faster; they land during the h hand-off):
+    // block b owns output columns 4b..4b+3; half-wave (wave w, half h) owns
+    // slot s = 2w + h and reads that expert's 4 rows, so a wave touches two
+    // experts' pages instead of k
+    const int half = lane >> 5, hl = lane & 31;
+    const int slot = 2 * wave + half;
+    const size_t IH2 = 2 * (size_t)I * H;
+    const uint16_t *dbase = slot < k ? s_slot[s_tk.seli[slot]] : nullptr;
+    const bool dhas = dbase != nullptr;
+    uint4 dv[4][DC];
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4) {
+        const int col = min((int)blockIdx.x * 4 + c4, H - 1);
+        // no copy (or no expert): read the router rows instead (E*H >= I elements, in bounds)
+        const uint16_t *row = dhas ? dbase + IH2 + (size_t)col * I : gate;
+#pragma unroll
+        for (int c = 0; c < DC; ++c) dv[c4][c] = ld_nt(row + 8 * min(hl + 32 * c, CI - 1));
+    }
+
+    // the block's 4P words go out as 8-byte writes by one thread
+    __syncthreads();
+    if (tid < 2 * P) {
+        const int qb = blockIdx.x * 4 * P + 2 * tid;
+        if (qb < KI)
+            __hip_atomic_store(reinterpret_cast<uint64_t *>(ws + kWsH + qb),
+                               (uint64_t)s_pub[2 * tid] | ((uint64_t)s_pub[2 * tid + 1] << 32), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
+
+    // ---- 5. collect h, then down + merge
+    collect<6>(ws + kWsH, KI, tid, blockDim.x, epoch, err, budget, reinterpret_cast<uint16_t *>(s_h));
+    __syncthreads();
+    // y[s][c] = bf16(h_s . down_s[col c]), each half-wave its own slot
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4) {
+        float acc = 0.0f;
+        if (slot < k) {
+#pragma unroll
+            for (int c = 0; c < DC; ++c) {
+                const int ch = hl + 32 * c;
+                if (ch < CI) acc = dot8(dv[c4][c], s_h[slot * CI + ch], acc);
+            }
+            if (!dhas) acc = 0.0f;
+        }
+        acc = half_sum(acc);
+        if (hl == 0 && slot < k) s_y[slot * 4 + c4] = bf16_round(acc);
+    }
+    __syncthreads();
+    // merge in slot order, one lane per column
+    if (tid < 4) {
+        const int col = blockIdx.x * 4 + tid;
+        float total = 0.0f;
+        for (int s2 = 0; s2 < k; ++s2) total = __builtin_fmaf(bf2f(s_tk.selw[s2]), s_y[s2 * 4 + tid], total);
+        if (col < H) out[col] = (uint16_t)f2bf(total);
+    }
+    if (tid == 0) __hip_atomic_store(ws + kWsEpoch + blockIdx.x, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+typedef void (*DecodeLayerFn)(const uint16_t *, const uint16_t *, const float *, int, int, int, int,
+                              const uint16_t *const *, int, uint16_t *, int32_t *, uint16_t *, float *, uint16_t *,
+                              uint16_t *, uint32_t *);
+
+struct DecodePlan {
+    DecodeLayerFn fn;
+    int blocks;
+    size_t lds;
+};
+
+// Instantiations (NCH, P, DC), chosen as the smallest that covers the shape
+// with P * NCH <= 16 (register budget of two blocks per CU).
+static int pick_decode(int H, int I, int k, DecodePlan *plan, std::string *why) {
+    const int C = H / 8, CI = I / 8;
+    const int blocks = (H + 3) / 4;
+    const int waves = blocks * 4;
+    const int nch_need = (C + 63) / 64, p_need = (k * I + waves - 1) / waves, dc_need = (CI + 31) / 32;
+    const int nch = nch_need <= 2 ? 2 : nch_need <= 4 ? 4 : nch_need <= 8 ? 8 : 0;
+    const int dc = dc_need <= 3 ? 3 : dc_need <= 6 ? 6 : 0;
+    int p = p_need <= 2 ? 2 : p_need <= 3 ? 3 : p_need <= 4 ? 4 : 0;
+    if (nch == 8 && p > 2) p = 0;
+    if (!nch || !dc || !p || blocks > kDecodeMaxBlocks || k * I > kDecodeMaxKI) {
+        *why = "decode_layer: shape outside the fused kernel (needs H <= 4096, I <= 1536, k*I <= 4*H)";
+        return kEInval;
+    }
+    DecodeLayerFn fn = nullptr;
+#define PD_DL(N, PP, D) \
+    if (nch == N && p == PP && dc == D) fn = decode_layer_kernel<N, PP, D>;
+    PD_DL(2, 2, 3) PD_DL(2, 3, 3) PD_DL(2, 4, 3) PD_DL(2, 2, 6) PD_DL(2, 3, 6) PD_DL(2, 4, 6)
+    PD_DL(4, 2, 3) PD_DL(4, 3, 3) PD_DL(4, 4, 3) PD_DL(4, 2, 6) PD_DL(4, 3, 6) PD_DL(4, 4, 6)
+    PD_DL(8, 2, 3) PD_DL(8, 2, 6)
+#undef PD_DL
+    if (!fn) {
+        *why = "decode_layer: no instantiation for this shape";
+        return kEInval;
+    }
+    plan->fn = fn;
+    plan->blocks = blocks;
+    plan->lds = (size_t)k * I * 2;
+    return kOk;
+}
+
+// Blocks of `fn` that can be resident at once on the current device.
+static int resident_blocks(DecodeLayerFn fn, size_t lds, std::string *why) {
+    static std::mutex mu;
+    static std::unordered_map<uint64_t, int> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        *why = "decode_layer: hipGetDevice failed";
+        return -1;
+    }
+    const uint64_t key = ((uint64_t)(uintptr_t)fn * 31u + lds) * 64u + (uint64_t)dev;
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        auto it = cache.find(key);
+        if (it != cache.end()) return it->second;
+    }
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(fn), 256, lds) !=
+            hipSuccess) {
+        *why = "decode_layer: occupancy query failed";
+        return -1;
+    }
+    const int n = cus * per_cu;
+    std::lock_guard<std::mutex> lock(mu);
+    cache[key] = n;
+    return n;
+}
+
+}  // namespace pd
+
+using namespace pd;
+
+PD_API size_t pdscope_decode_workspace_bytes(void) { return (size_t)kWsWords * 4; }
+
+PD_API int pdscope_decode_layer_supported(int H, int I, int E, int k) {
+    if (H < 16 || H % 16 || I < 8 || I % 8 || E < 2 || E > kDecodeMaxE || E % 2 || k < 1 || k > kDecodeMaxK ||
+        k > E)
+        return 0;
+    if ((size_t)I > (size_t)E * H || (E + 3) / 4 > (H + 3) / 4) return 0;
+    DecodePlan plan;
+    std::string why;
+    if (pick_decode(H, I, k, &plan, &why) != kOk) return 0;
+    const int n = resident_blocks(plan.fn, plan.lds, &why);
+    return n >= plan.blocks ? 1 : 0;
+}
+
+PD_API int pdscope_decode_layer(const void *x, const void *gate, const float *bias, int H, int E, int k,
+                                int normalize, const void *const *slots, int I, void *logits, int32_t *ids,
+                                void *weights, float *probs, void *h_ws, void *out, void *workspace,
+                                void *stream) {
+    if (!x || !gate || !slots || !logits || !ids || !weights || !h_ws || !out || !workspace)
+        return fail(kEInval, "decode_layer: null pointer");
+    if (H < 16 || H % 16) return fail(kEInval, "decode_layer: need H % 16 == 0");
+    if (I < 8 || I % 8) return fail(kEInval, "decode_layer: need I % 8 == 0");
+    if (E < 2 || E > kDecodeMaxE || E % 2) return fail(kEInval, "decode_layer: need even E <= 256");
+    if (k < 1 || k > kDecodeMaxK || k > E) return fail(kEInval, "decode_layer: need 1 <= k <= min(E, 8)");
+    if ((size_t)I > (size_t)E * H) return fail(kEInval, "decode_layer: need I <= E*H");
+    if ((size_t)k * I * 2 > 64 * 1024) return fail(kEInval, "decode_layer: k*I*2 must fit 64 KiB of LDS");
+    if ((E + 3) / 4 > (H + 3) / 4) return fail(kEInval, "decode_layer: need E <= H");
+    DecodePlan plan;
+    std::string why;
+    if (pick_decode(H, I, k, &plan, &why) != kOk) return fail(kEInval, why);
+    const int resident = resident_blocks(plan.fn, plan.lds, &why);
+    if (resident < 0) return fail(kEHip, why);
+    if (resident < plan.blocks)
+        return fail(kEInval, "decode_layer: the grid would not be resident at once on this device");
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    plan.fn<<<plan.blocks, 256, plan.lds, s>>>(
+        (const uint16_t *)x, (const uint16_t *)gate, bias, H, E, k, normalize, (const uint16_t *const *)slots, I,
+        (uint16_t *)logits, ids, (uint16_t *)weights, probs, (uint16_t *)h_ws, (uint16_t *)out,
+        (uint32_t *)workspace);
+    return check_launch("decode_layer_kernel");
+}

@@ -88,10 +88,8 @@ __global__ __launch_bounds__(256, 2) void grouped_kernel(
     u32x4_t ra[A_PER], rb[B_PER];
 #define PD_GLOAD(k0)                                                                            \
     do {                                                                                        \
-        _Pragma("unroll") for (int q = 0; q < A_PER; ++q) ra[q] =                              \
-            *reinterpret_cast<const u32x4_t *>(a_ptr[q] + (k0));                                \
-        _Pragma("unroll") for (int q = 0; q < B_PER; ++q) rb[q] =                              \
-            *reinterpret_cast<const u32x4_t *>(b_ptr[q] + (k0));                                \
+        _Pragma("unroll") for (int q = 0; q < A_PER; ++q) ra[q] = *gptr(a_ptr[q] + (k0));      \
+        _Pragma("unroll") for (int q = 0; q < B_PER; ++q) rb[q] = *gptr(b_ptr[q] + (k0));      \
     } while (0)
 #define PD_LSTORE(buf)                                                                          \
     do {                                                                                        \

@@ -2,103 +2,9 @@
 // Restates expertbench/adapters/qwen.py:140-152 (route) on gfx950, and the
 // predictor histogram of expertbench/pdscope_runtime.py:245-249.
 #include "common.h"
+#include "topk.h"
 
 namespace pd {
-
-// Per-wave LDS scratch of the top-k selection.
-struct TopkScratch {
-    uint64_t key[256];
-    float selp[16];
-    int seli[16];
-};
-
-// Make this wave's LDS writes visible to its other lanes before they read.
-__device__ __forceinline__ void wave_lds_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// Softmax + top-k + renormalisation for one token, executed by one wave64.
-// lrow: E logits of the token (bf16 values held as fp32, in LDS).
-// Lane l owns experts l, l+64, ...; the softmax denominator is summed per
-// lane in that order and then by an xor butterfly, an order that is fixed
-// and reproduced by the host-side checker.  Selection: every candidate gets
-// the key (p, ~id) and its rank = number of larger keys (a total order:
-// higher probability first, lower expert id on ties); ranks < k are the
-// top-k, already sorted.
-template <int J>
-__device__ __forceinline__ void topk_token(const float *lrow, const float *__restrict__ bias, int E, int k,
-                                           int normalize, int t, int32_t *__restrict__ ids,
-                                           uint16_t *__restrict__ weights, float *__restrict__ probs,
-                                           TopkScratch *sc) {
-#pragma clang fp contract(off)
-    const int lane = lane_id();
-    float v[J], p[J];
-    float m = -__builtin_inff();
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-        int e = lane + 64 * j;
-        float val = -__builtin_inff();
-        if (e < E) {
-            val = lrow[e];
-            if (bias) val = val + bias[e];
-        }
-        v[j] = val;
-        m = fmaxf(m, val);
-    }
-    m = wave_max(m);
-    float acc = 0.0f;
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-        int e = lane + 64 * j;
-        float ex = 0.0f;
-        if (e < E) {
-            ex = route_expf(v[j] - m);
-            acc = acc + ex;
-        }
-        p[j] = ex;
-    }
-    const float S = wave_sum(acc);
-    uint64_t key[J];
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-        p[j] = p[j] / S;
-        const int e = lane + 64 * j;
-        key[j] = ((uint64_t)__float_as_uint(p[j]) << 32) | (0xffffffffu - (uint32_t)e);
-        if (e < E) {
-            sc->key[e] = key[j];
-            if (probs) probs[(size_t)t * E + e] = p[j];
-        }
-    }
-    wave_lds_sync();
-    int rank[J];
-#pragma unroll
-    for (int j = 0; j < J; ++j) rank[j] = 0;
-    for (int e2 = 0; e2 < E; e2 += 2) {
-        const uint64_t k0 = sc->key[e2], k1 = sc->key[e2 + 1];
-#pragma unroll
-        for (int j = 0; j < J; ++j) rank[j] += (int)(k0 > key[j]) + (int)(k1 > key[j]);
-    }
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-        const int e = lane + 64 * j;
-        if (e < E && rank[j] < k) {
-            sc->selp[rank[j]] = p[j];
-            sc->seli[rank[j]] = e;
-        }
-    }
-    wave_lds_sync();
-    float denom = 0.0f;
-    if (normalize)
-        for (int r = 0; r < k; ++r) denom = denom + sc->selp[r];
-    if (lane < k) {
-        const float pv = sc->selp[lane];
-        ids[(size_t)t * k + lane] = sc->seli[lane];
-        weights[(size_t)t * k + lane] = (uint16_t)f2bf(normalize ? pv / denom : pv);
-    }
-    wave_lds_sync();
-}
 
 template <int J>
 __device__ __forceinline__ void topk_tokens_block(const float *s_logit, int ntok, int E, const float *bias, int k,

@@ -1,0 +1,149 @@
+// Softmax + top-k + renormalisation of one token's router logits by one
+// wave64 (the selection of expertbench/adapters/qwen.py:148-151).
+#pragma once
+
+#include "common.h"
+
+namespace pd {
+
+// Per-wave LDS scratch of the top-k selection.  After topk_token returns,
+// seli[0..k) holds the selected experts in rank order, selp[0..k) their
+// probabilities and selw[0..k) their final bf16 weights.
+struct TopkScratch {
+    float selp[16];
+    int seli[16];
+    uint16_t selw[16];
+};
+
+// Make this wave's LDS writes visible to its other lanes before they read.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Wave-wide max through DPP (no LDS round trips): row_shr 1/2/4/8 leave
+// each row's max in its lane 15, row_bcast 15/31 carry it to lane 63, which
+// is read back as a uniform value.  Lanes without a DPP source keep their
+// own value (bound_ctrl off), so max is taken over real values only.
+__device__ __forceinline__ int dpp_max_i32(int v) {
+    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x111, 0xf, 0xf, false));  // row_shr:1
+    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x112, 0xf, 0xf, false));  // row_shr:2
+    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x114, 0xf, 0xf, false));  // row_shr:4
+    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x118, 0xf, 0xf, false));  // row_shr:8
+    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x142, 0xa, 0xf, false));  // row_bcast:15
+    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x143, 0xc, 0xf, false));  // row_bcast:31
+    return __builtin_amdgcn_readlane(v, 63);
+}
+
+__device__ __forceinline__ float dpp_max_f32(float f) {
+    int v = __float_as_int(f);
+#define PD_FMAX_STEP(ctrl, rmask)                                                                          \
+    v = __float_as_int(                                                                                    \
+        fmaxf(__int_as_float(v), __int_as_float(__builtin_amdgcn_update_dpp(v, v, ctrl, rmask, 0xf, false))))
+    PD_FMAX_STEP(0x111, 0xf);
+    PD_FMAX_STEP(0x112, 0xf);
+    PD_FMAX_STEP(0x114, 0xf);
+    PD_FMAX_STEP(0x118, 0xf);
+    PD_FMAX_STEP(0x142, 0xa);
+    PD_FMAX_STEP(0x143, 0xc);
+#undef PD_FMAX_STEP
+    return __int_as_float(__builtin_amdgcn_readlane(v, 63));
+}
+
+// lrow: E logits of the token (bf16 values held as fp32, in LDS).
+// Lane l owns experts l, l+64, ...; the softmax denominator is summed per
+// lane in that order and then by an xor butterfly over offsets 32..1, an
+// order that is fixed and reproduced by the host-side checker.
+// Selection: k rounds of a wave-wide max over the probabilities' bit
+// patterns (p >= 0, so integer order is float order; taken candidates drop
+// to -1); among equal maxima the lowest expert id wins (ballot, first set
+// lane of the lowest j).  This is the total order "higher probability
+// first, lower expert id on ties", so the k rounds give the sorted top-k.
+// ids / weights / probs (global, row t) are written when non-null.
+template <int J>
+__device__ __forceinline__ void topk_token(const float *lrow, const float *__restrict__ bias, int E, int k,
+                                           int normalize, int t, int32_t *__restrict__ ids,
+                                           uint16_t *__restrict__ weights, float *__restrict__ probs,
+                                           TopkScratch *sc) {
+#pragma clang fp contract(off)
+    const int lane = lane_id();
+    float v[J], p[J];
+    float m = -__builtin_inff();
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        int e = lane + 64 * j;
+        float val = -__builtin_inff();
+        if (e < E) {
+            val = lrow[e];
+            if (bias) val = val + bias[e];
+        }
+        v[j] = val;
+        m = fmaxf(m, val);
+    }
+    m = dpp_max_f32(m);
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        int e = lane + 64 * j;
+        float ex = 0.0f;
+        if (e < E) {
+            ex = route_expf(v[j] - m);
+            acc = acc + ex;
+        }
+        p[j] = ex;
+    }
+    const float S = wave_sum(acc);
+    int hi[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        p[j] = p[j] / S;
+        const int e = lane + 64 * j;
+        hi[j] = e < E ? (int)__float_as_uint(p[j]) : -1;
+        if (e < E && probs) probs[(size_t)t * E + e] = p[j];
+    }
+    float myp = 0.0f, denom = 0.0f;
+    int myid = 0;
+    for (int r = 0; r < k; ++r) {
+        int lm = hi[0];
+#pragma unroll
+        for (int j = 1; j < J; ++j) lm = max(lm, hi[j]);
+        const int mx = dpp_max_i32(lm);
+        int sel = -1;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const unsigned long long b = __ballot(hi[j] == mx);
+            if (sel < 0 && b) sel = 64 * j + __ffsll(b) - 1;
+        }
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+            if (lane + 64 * j == sel) hi[j] = -1;
+        const float pv = __int_as_float(mx);
+        if (normalize) denom = denom + pv;
+        if (lane == r) {
+            myp = pv;
+            myid = sel;
+        }
+    }
+    if (lane < k) {
+        const uint16_t wb = (uint16_t)f2bf(normalize ? myp / denom : myp);
+        sc->selp[lane] = myp;
+        sc->seli[lane] = myid;
+        sc->selw[lane] = wb;
+        if (ids) ids[(size_t)t * k + lane] = myid;
+        if (weights) weights[(size_t)t * k + lane] = wb;
+    }
+    wave_lds_sync();
+}
+
+// Block-level wrapper for one token: wave 0 routes, the block waits.  Must
+// be reached by the whole block; sc is then valid for every thread.
+template <int J>
+__device__ __forceinline__ void topk_block(const float *lrow, const float *__restrict__ bias, int E, int k,
+                                           int normalize, int32_t *__restrict__ ids, uint16_t *__restrict__ weights,
+                                           float *__restrict__ probs, TopkScratch *sc) {
+    if (threadIdx.x < 64) topk_token<J>(lrow, bias, E, k, normalize, 0, ids, weights, probs, sc);
+    __syncthreads();
+}
+
+}  // namespace pd

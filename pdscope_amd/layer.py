@@ -73,8 +73,20 @@ def experts_resident(x, ids, weights, slots, ws: MoEWorkspace, out=None, *, bloc
     return out
 
 
-def moe_forward(x, gate, slots, ws: MoEWorkspace, *, normalize=True, bias=None, block_m=None):
-    """Full layer: returns (out [T,H] bf16, logits, ids int32 [T,k], weights bf16 [T,k])."""
+def moe_forward(x, gate, slots, ws: MoEWorkspace, *, normalize=True, bias=None, block_m=None, fused_decode=True):
+    """Full layer: returns (out [T,H] bf16, logits, ids int32 [T,k], weights bf16 [T,k]).
+
+    T == 1 runs the single-launch decode kernel (K4f) when the shape and the
+    device allow it (fused_decode), else route (K1) + decode GEMV (K4).
+    """
+    T = x.shape[0]
+    if (T == 1 and fused_decode and ws.k <= 8
+            and ops.decode_layer_supported(ws.H, ws.I, ws.E, ws.k, x.device)):
+        logits, ids, weights, _ = ws.views(1)
+        out = ws.out[:1]
+        ops.decode_layer(x, gate, slots, ws.I, ws.k, normalize, bias=bias, out=out, logits=logits, ids=ids,
+                         weights=weights, h_ws=ws.h_ws)
+        return out, logits, ids, weights
     logits, ids, weights = route(x, gate, ws, normalize=normalize, bias=bias)
     out = experts_resident(x, ids, weights, slots, ws, block_m=block_m)
     return out, logits, ids, weights

@@ -181,6 +181,71 @@ def swiglu_decode(x, ids, w, slots, H, I, h_ws, out):
     return out
 
 
+_decode_ws = {}
+_decode_ok = {}
+
+
+DECODE_WS_ERROR_WORD = 1024
+
+
+def decode_workspace(device, H) -> torch.Tensor:
+    """Zero-filled hand-off words of the fused decode kernel for hidden size H
+    on `device` (its per-block epochs assume one grid size, i.e. one H, and
+    launches on one stream at a time)."""
+    device = torch.device(device)
+    if device.index is None:
+        device = torch.device(device.type, torch.cuda.current_device())
+    key = (device, int(H))
+    ws = _decode_ws.get(key)
+    if ws is None:
+        n = int(_lib.load().pdscope_decode_workspace_bytes())
+        ws = torch.zeros(n // 4, dtype=torch.int32, device=key[0])
+        _decode_ws[key] = ws
+    return ws
+
+
+def decode_workspace_error(device, H) -> int:
+    """Sticky error word of the fused decode kernel (non-zero after a bounded wait gave up)."""
+    return int(decode_workspace(device, H)[DECODE_WS_ERROR_WORD].item())
+
+
+def decode_layer_supported(H, I, E, k, device) -> bool:
+    device = torch.device(device)
+    if device.index is None:
+        device = torch.device(device.type, torch.cuda.current_device())
+    key = (device, H, I, E, k)
+    ok = _decode_ok.get(key)
+    if ok is None:
+        with torch.cuda.device(key[0]):
+            ok = bool(_lib.load().pdscope_decode_layer_supported(H, I, E, k))
+        _decode_ok[key] = ok
+    return ok
+
+
+def decode_layer(x, gate, slots, I, top_k, normalize, *, bias=None, out, logits, ids, weights, h_ws, probs=None):
+    """K4f: route + top-k + SwiGLU GEMV + down/merge of one token in one launch."""
+    _need(x, "inputs", BF16)
+    dev = x.device
+    _need(gate, "gate", BF16, 2, dev)
+    _need(slots, "slots", torch.int64, 1, dev)
+    E, H = gate.shape
+    if x.numel() != H or out.numel() != H or logits.numel() != E or ids.numel() != top_k or weights.numel() != top_k:
+        raise ValueError("decode_layer expects one token: x/out [H], logits [E], ids/weights [k]")
+    if h_ws.numel() < top_k * I or slots.numel() < E:
+        raise ValueError("decode_layer: h_ws must hold k*I values and slots E entries")
+    _need(ids, "ids", torch.int32, None, dev)
+    for t, n in ((out, "out"), (logits, "logits"), (weights, "weights"), (h_ws, "h_ws")):
+        _need(t, n, BF16, None, dev)
+    if bias is not None:
+        _need(bias, "bias", torch.float32, 1, dev)
+    if probs is not None:
+        _need(probs, "probs", torch.float32, None, dev)
+    _lib.call("pdscope_decode_layer", _p(x), _p(gate), _p(bias), H, E, top_k, int(bool(normalize)), _p(slots), I,
+              _p(logits), _p(ids), _p(weights), _p(probs), _p(h_ws), _p(out), _p(decode_workspace(dev, H)),
+              _stream(dev))
+    return out
+
+
 # --------------------------------------------------------------------- A8/A9
 
 def merge(y, row_of, w, out, add_in=None):

@@ -378,19 +378,18 @@ class PDScopeCudaRuntime:
         if g is None:
             gws = L.MoEWorkspace(1, self.H, self.I, self.E, k, self.device)
             xin = torch.empty_like(x)
-            gout = torch.empty_like(out)
+            gout = gws.out[:1]
             xin.copy_(x)
             torch.cuda.synchronize(self.device)
             side = torch.cuda.Stream(self.device)
             side.wait_stream(torch.cuda.current_stream(self.device))
+            # whole layer (fused single-launch decode where the device allows)
             with torch.cuda.stream(side):
-                L.route(xin, gate, gws, normalize=normalize)
-                ops.swiglu_decode(xin, gws.ids[:1], gws.weights[:1], slots_dev, self.H, self.I, gws.h_ws, gout)
+                L.moe_forward(xin, gate, slots_dev, gws, normalize=normalize)
             torch.cuda.current_stream(self.device).wait_stream(side)
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
-                L.route(xin, gate, gws, normalize=normalize)
-                ops.swiglu_decode(xin, gws.ids[:1], gws.weights[:1], slots_dev, self.H, self.I, gws.h_ws, gout)
+                L.moe_forward(xin, gate, slots_dev, gws, normalize=normalize)
             g = (graph, xin, gout, gws, slots_dev)
             self._graphs[gkey] = g
         graph, xin, gout, gws, _ = g

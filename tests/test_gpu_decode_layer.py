@@ -1,0 +1,185 @@
+"""Single-launch decode layer (K4f, pdscope_decode_layer) through the C-ABI.
+
+The fused kernel keeps the per-lane arithmetic order of the three-launch
+path (pdscope_route_topk + pdscope_swiglu_decode), so logits, ids, weights
+and the layer output must be bitwise equal to it; the three-launch path is
+itself checked against the oracle in test_gpu_kernels.py, and the fused
+path is checked against the oracle here too (routing bit-exact given the
+logits, output within bf16 tolerance).  The sync workspace must come back
+zero with no wait having given up, also across hipGraph replays.
+"""
+import numpy as np
+import pytest
+import torch
+
+from tests.gpu_helpers import (MAX_REL, MEAN_ABS, err_metrics, logits_within_accumulation_error,
+                               oracle_layer_given_routing, u16)
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module")
+def pd():
+    from pdscope_amd import layer, ops, synthetic
+    return ops, layer, synthetic
+
+
+def _three_launch(ops, x, gate, slots, I, k, normalize, bias=None):
+    E, H = gate.shape
+    logits = torch.empty((1, E), dtype=torch.bfloat16, device=DEV)
+    ids = torch.empty((1, k), dtype=torch.int32, device=DEV)
+    w = torch.empty((1, k), dtype=torch.bfloat16, device=DEV)
+    ops.route_topk(x, gate, k, normalize, bias=bias, out=(logits, ids, w))
+    h = torch.empty(k * I, dtype=torch.bfloat16, device=DEV)
+    out = torch.empty((1, H), dtype=torch.bfloat16, device=DEV)
+    ops.swiglu_decode(x, ids, w, slots, H, I, h, out)
+    return logits, ids, w, out
+
+
+def _fused(ops, x, gate, slots, I, k, normalize, bias=None):
+    E, H = gate.shape
+    logits = torch.empty((1, E), dtype=torch.bfloat16, device=DEV)
+    ids = torch.empty((1, k), dtype=torch.int32, device=DEV)
+    w = torch.empty((1, k), dtype=torch.bfloat16, device=DEV)
+    h = torch.empty(k * I, dtype=torch.bfloat16, device=DEV)
+    out = torch.empty((1, H), dtype=torch.bfloat16, device=DEV)
+    probs = torch.empty((1, E), dtype=torch.float32, device=DEV)
+    ops.decode_layer(x, gate, slots, I, k, normalize, bias=bias, out=out, logits=logits, ids=ids, weights=w,
+                     h_ws=h, probs=probs)
+    return logits, ids, w, out, probs
+
+
+def _assert_sync_clean(ops, H=2048):
+    """No bounded wait gave up, and every block of the grid ran every launch
+    (all per-block epochs equal)."""
+    ws = ops.decode_workspace(DEV, H)
+    torch.cuda.synchronize()
+    words = ws.cpu().numpy()
+    assert words[ops.DECODE_WS_ERROR_WORD] == 0, "a bounded wait of the fused decode kernel gave up"
+    ep = words[:H // 4]
+    assert ep[0] != 0 and (ep == ep[0]).all(), "per-block epochs diverged"
+
+
+SHAPES = [
+    dict(H=2048, I=768, E=128, k=8, normalize=True),    # Qwen3-30B-A3B
+    dict(H=1024, I=512, E=64, k=4, normalize=True),
+    dict(H=2048, I=1408, E=64, k=2, normalize=False),  # DeepSeek-V2-Lite widths, k within the fused limits
+    dict(H=4096, I=256, E=32, k=3, normalize=True),
+]
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: f"H{s['H']}_I{s['I']}_E{s['E']}_k{s['k']}")
+def test_fused_equals_three_launch(pd, shape):
+    ops, layer, synthetic = pd
+    H, I, E, k, nrm = shape["H"], shape["I"], shape["E"], shape["k"], shape["normalize"]
+    if not ops.decode_layer_supported(H, I, E, k, DEV):
+        pytest.skip("shape not resident on this device")
+    lay = synthetic.make_layer(H, I, E, k, nrm, seed=900 + H + I, device=DEV)
+    slots = ops.slot_table([lay.experts[e] for e in range(E)], DEV)
+    for seed in (1, 2, 3, 4):
+        x = synthetic.make_tokens(1, H, seed=seed * 31 + E, device=DEV)
+        a = _three_launch(ops, x, lay.gate, slots, I, k, nrm)
+        b = _fused(ops, x, lay.gate, slots, I, k, nrm)
+        torch.cuda.synchronize()
+        for name, u, v in zip(("logits", "ids", "weights", "out"), a, b[:4]):
+            assert torch.equal(u.view(torch.int16) if u.dtype == torch.bfloat16 else u,
+                               v.view(torch.int16) if v.dtype == torch.bfloat16 else v), (name, seed)
+    _assert_sync_clean(ops, H)
+
+
+def test_fused_matches_oracle_qwen(orc, pd):
+    ops, layer, synthetic = pd
+    lay = synthetic.make_layer(**synthetic.QWEN, device=DEV)
+    if not ops.decode_layer_supported(2048, 768, 128, 8, DEV):
+        pytest.skip("shape not resident on this device")
+    slots = ops.slot_table([lay.experts[e] for e in range(128)], DEV)
+    experts = u16(lay.experts)
+    for seed in (11, 12, 13):
+        x = synthetic.make_tokens(1, 2048, seed=seed, device=DEV)
+        logits, ids, w, out, probs = _fused(ops, x, lay.gate, slots, 768, 8, True)
+        torch.cuda.synchronize()
+        oi, ow, op = orc.route_from_logits(u16(logits), 8, True, None, want_probs=True)
+        assert np.array_equal(ids.cpu().numpy(), oi)
+        assert np.array_equal(u16(w), ow)
+        assert np.array_equal(probs.cpu().numpy().view(np.uint32), op.view(np.uint32))
+        exact = orc.route_logits(u16(x), u16(lay.gate))
+        ok, _ = logits_within_accumulation_error(u16(logits), exact, u16(x), u16(lay.gate), orc.bf16_to_f32)
+        assert ok, "logit mismatch beyond fp32 accumulation error"
+        ref, _, _ = oracle_layer_given_routing(orc, u16(x), oi, ow, experts, 2048, 768)
+        m = err_metrics(orc.bf16_to_f32(u16(out)), orc.bf16_to_f32(ref))
+        assert m["max_rel"] <= MAX_REL and m["mean_abs"] <= MEAN_ABS, m
+    _assert_sync_clean(ops)
+
+
+def test_fused_zipf_bias_and_missing_copies(pd):
+    """Router bias (Zipf workload) and slots without a ready copy (address 0 ->
+    the expert contributes nothing) behave as on the three-launch path."""
+    ops, layer, synthetic = pd
+    lay = synthetic.make_layer(**synthetic.QWEN, seed=77, device=DEV)
+    if not ops.decode_layer_supported(2048, 768, 128, 8, DEV):
+        pytest.skip("shape not resident on this device")
+    bias, _ = synthetic.zipf_bias(128, device=DEV)
+    ptrs = [lay.experts[e].data_ptr() for e in range(128)]
+    for e in range(0, 128, 3):
+        ptrs[e] = 0
+    slots = torch.tensor(ptrs, dtype=torch.int64, device=DEV)
+    for seed in (5, 6, 7):
+        x = synthetic.make_tokens(1, 2048, seed=seed, device=DEV)
+        a = _three_launch(ops, x, lay.gate, slots, 768, 8, True, bias=bias)
+        b = _fused(ops, x, lay.gate, slots, 768, 8, True, bias=bias)
+        torch.cuda.synchronize()
+        assert torch.equal(a[1], b[1])
+        assert torch.equal(a[3].view(torch.int16), b[3].view(torch.int16))
+    _assert_sync_clean(ops)
+
+
+def test_fused_graph_replay(pd):
+    """Captured once, replayed with new inputs: every replay equals eager, and
+    the self-resetting counters leave the workspace clean."""
+    ops, layer, synthetic = pd
+    lay = synthetic.make_layer(**synthetic.QWEN, seed=78, device=DEV)
+    if not ops.decode_layer_supported(2048, 768, 128, 8, DEV):
+        pytest.skip("shape not resident on this device")
+    slots = ops.slot_table([lay.experts[e] for e in range(128)], DEV)
+    ws = layer.MoEWorkspace(1, 2048, 768, 128, 8, DEV)
+    xin = synthetic.make_tokens(1, 2048, seed=100, device=DEV)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        layer.moe_forward(xin, lay.gate, slots, ws)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        layer.moe_forward(xin, lay.gate, slots, ws)
+    torch.cuda.synchronize()
+    for seed in range(101, 109):
+        x = synthetic.make_tokens(1, 2048, seed=seed, device=DEV)
+        eager = _three_launch(ops, x, lay.gate, slots, 768, 8, True)
+        torch.cuda.synchronize()
+        xin.copy_(x)
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(ws.ids[:1], eager[1])
+        assert torch.equal(ws.out[:1].view(torch.int16), eager[3].view(torch.int16)), seed
+    _assert_sync_clean(ops)
+
+
+def test_unsupported_shape_falls_back(pd):
+    """DeepSeek-V2-Lite top-6 with I=1408 exceeds the fused kernel's register
+    plan: moe_forward falls back to route + decode GEMV, which still matches."""
+    ops, layer, synthetic = pd
+    assert not ops.decode_layer_supported(2048, 1408, 64, 6, DEV)
+    lay = synthetic.make_layer(2048, 1408, 64, 6, False, seed=5, device=DEV)
+    slots = ops.slot_table([lay.experts[e] for e in range(64)], DEV)
+    x = synthetic.make_tokens(1, 2048, seed=3, device=DEV)
+    with pytest.raises(ValueError):
+        _fused(ops, x, lay.gate, slots, 1408, 6, False)
+    ws = layer.MoEWorkspace(1, 2048, 1408, 64, 6, DEV)
+    out, logits, ids, w = layer.moe_forward(x, lay.gate, slots, ws, normalize=False)
+    a = _three_launch(ops, x, lay.gate, slots, 1408, 6, False)
+    torch.cuda.synchronize()
+    assert torch.equal(ids, a[1])
+    assert torch.equal(out.view(torch.int16), a[3].view(torch.int16))
