@@ -141,4 +141,11 @@ __device__ __forceinline__ float route_expf(float x) {
 
 __device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
 
+// silu with the hardware exp2 and reciprocal (about 1 ulp each): for epilogues
+// whose result is rounded to bf16 right away
+__device__ __forceinline__ float silu_fast(float g) {
+    const float e = __builtin_amdgcn_exp2f(-g * 0x1.715476p+0f);
+    return g * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
 }  // namespace pd

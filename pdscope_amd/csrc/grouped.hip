@@ -10,103 +10,157 @@
 //             epilogue pairs accumulators of the same lane;
 //   down    : y[r,n] = bf16(h_r . down_n)
 // Both operands are K-contiguous ([rows, K] activations, [out, in] weights),
-// so every 16-byte global load feeds one MFMA lane directly.  Tiles go
-// through double-buffered LDS with a 16-byte-chunk XOR swizzle
-// (chunk c of row r lives at c ^ (r & 7)) so the 32 lanes reading one
-// column of chunks hit distinct banks.  MFMA: v_mfma_f32_32x32x16_bf16.
+// so every 16-byte chunk feeds one MFMA lane directly.  Tiles stream into a
+// 3- or 4-stage LDS ring by direct-to-LDS loads (global_load_lds_dwordx4)
+// with a 16-byte-chunk XOR swizzle applied on the source side (chunk c of
+// row r lives at c ^ (r & 7)), so fragment reads are bank-conflict free.
+// MFMA: v_mfma_f32_32x32x16_bf16, fp32 accumulation.
+#include <type_traits>
+
 #include "common.h"
 
 namespace pd {
 
-constexpr int kBK = 64;  // K elements per LDS stage (8 chunks of 16 B)
+// LDS tile geometry for a K step of BK bf16 elements: a tile row is BK * 2
+// bytes (CPR chunks of 16 B); one wave-wide direct-to-LDS load fills 1 KB,
+// i.e. RPI consecutive rows.  With 64 banks of 4 bytes, a 16-byte fragment
+// read serves 16 lanes (16 consecutive rows, one logical chunk) per cycle;
+// rows share a 256-byte bank line in groups of RPL, so chunk c of row r is
+// stored in slot c ^ ((r / RPL) % CPR) and the 16 rows of a fragment read
+// land in 16 distinct 16-byte bank groups (conflict free).
+template <int BK>
+struct Geo {
+    static constexpr int RB = BK * 2;
+    static constexpr int CPR = BK / 8;
+    static constexpr int RPI = 1024 / RB;
+    static constexpr int RPL = 256 / RB;
+    static __device__ __forceinline__ int key(int r) { return (r / RPL) % CPR; }
+    static __device__ __forceinline__ int off(int r, int c) { return r * RB + ((c ^ key(r)) << 4); }
+};
 
-__device__ __forceinline__ int swz(int row, int chunk) { return row * kBK + ((chunk ^ (row & 7)) << 3); }
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) const void g_void_t;
 
-template <int BM, int BN, int WM, int WN, bool GATEUP>
-__global__ __launch_bounds__(256, 2) void grouped_kernel(
+// One wave-wide direct-to-LDS load: lane l's 16 bytes at src land at
+// dst + 16 l (dst is wave-uniform), bypassing the registers.
+__device__ __forceinline__ void load_lds16(const uint16_t *src, uint8_t *dst) {
+    __builtin_amdgcn_global_load_lds((g_void_t *)(uintptr_t)src, (lds_void_t *)(uint32_t)(uintptr_t)dst, 16, 0, 0);
+}
+
+// Wait until at most n vector-memory operations of this wave are in flight
+// (n is a compile-time constant in every use).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier for the LDS ring.  __syncthreads() would also wait for
+// every outstanding direct-to-LDS load (its release fence covers them) and
+// drain the pipeline; here the caller waits for exactly the stage it needs
+// (wait_stage), this wave's LDS reads are complete (lgkmcnt 0) before the
+// slot they read can be refilled, and the memory clobber keeps the
+// compiler from moving LDS accesses across the barrier.
+__device__ __forceinline__ void ring_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+template <int S, int LPW>
+__device__ __forceinline__ void wait_stage(int younger) {
+    // `younger` stages were issued after the one to be consumed
+    if constexpr (S >= 4) {
+        if (younger >= 2) { wait_vm<2 * LPW>(); return; }
+    }
+    if constexpr (S >= 3) {
+        if (younger >= 1) { wait_vm<LPW>(); return; }
+    }
+    wait_vm<0>();
+}
+
+// Tile BM x BN x BK, WM x WN waves (4 or 8: with 8, two waves share each
+// SIMD so one wave's MFMAs cover the other's LDS reads, waits and
+// epilogue), S-stage LDS ring filled by direct-to-LDS loads (the stage
+// S-1 ahead is in flight while one stage is consumed).  Tiles are numbered (m-tile, n-tile) with n fastest and the
+// tile range is cut into 8 contiguous pieces, one per XCD (block b runs on
+// XCD b % 8): all n-tiles of an m-tile share the gathered activation rows
+// in one L2, and the m-tiles of one expert read the same weight tiles at
+// the same time from one L2.
+template <int BM, int BN, int BK, int WM, int WN, int S, bool GATEUP>
+__global__ __launch_bounds__(64 * WM * WN, 1) void grouped_kernel(
     const uint16_t *__restrict__ a_src, const int32_t *__restrict__ perm_token,
     const int32_t *__restrict__ offsets, const int32_t *__restrict__ sel, int nsel,
     const int32_t *__restrict__ tile_start, const uint16_t *const *__restrict__ slots, int H, int I,
     uint16_t *__restrict__ out) {
-    static_assert(WM * WN == 4, "4 waves");
+    constexpr int NW = WM * WN;
+    static_assert(NW == 4 || NW == 8, "4 or 8 waves");
     constexpr int TM = BM / WM, TN = BN / WN;  // wave tile
     constexpr int MB = TM / 32, NB = TN / 32;  // 32x32 MFMA blocks per wave
     static_assert(MB >= 1 && NB >= 1 && (!GATEUP || NB % 2 == 0), "wave tiling");
-    constexpr int A_PER = BM * 8 / 256, B_PER = BN * 8 / 256;  // 16-byte chunks per thread per stage
-    static_assert(A_PER >= 1 && B_PER >= 1, "tile too small");
+    typedef Geo<BK> G;
+    constexpr int AL = BM / G::RPI / NW, BL = BN / G::RPI / NW;  // 1 KB load instructions per wave per stage
+    static_assert(AL >= 1 && BL >= 1 && AL * G::RPI * NW == BM && BL * G::RPI * NW == BN, "tile / load shape");
+    constexpr int LPW = AL + BL;
+    constexpr int STAGE = (BM + BN) * G::RB;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[S * STAGE];
 
-    __shared__ __attribute__((aligned(16))) uint16_t s_a[2][BM * kBK];
-    __shared__ __attribute__((aligned(16))) uint16_t s_b[2][BN * kBK];
-
-    // ---- XCD-aware tile order: blocks are dispatched round-robin over the 8
-    // XCDs (block b -> XCD b % 8).  m-tile mt is pinned to XCD mt % 8 and its
-    // n-tiles are consecutive blocks of that XCD, so the gathered activation
-    // rows of an m-tile are fetched into one L2 and reused by every n-tile.
-    const int ntn = GATEUP ? I / (BN / 2) : H / BN;
-    const int xcd = blockIdx.x & 7, pos = blockIdx.x >> 3;
-    const int jm = pos / ntn, nt = pos - jm * ntn;
-    const int bx = jm * 8 + xcd;
-    if (bx >= tile_start[nsel]) return;
-    // ---- locate (expert, m-tile): binary search over the tile prefix
+    // ---- tile -> (m-tile, n-tile)
+    const int NT = GATEUP ? I / (BN / 2) : H / BN;
+    const int total = tile_start[nsel] * NT;
+    const int per_xcd = (total + 7) >> 3;
+    const int pos = blockIdx.x >> 3;
+    if (pos >= per_xcd) return;
+    const int t = (blockIdx.x & 7) * per_xcd + pos;
+    if (t >= total) return;
+    const int mt = t / NT, nt = t - mt * NT;
     int lo = 0, hi = nsel - 1;
     while (lo < hi) {
-        int mid = (lo + hi + 1) >> 1;
-        if (tile_start[mid] <= bx) lo = mid;
+        const int mid = (lo + hi + 1) >> 1;
+        if (tile_start[mid] <= mt) lo = mid;
         else hi = mid - 1;
     }
     const int e = sel[lo];
     const int row_end = offsets[e + 1];
-    const int m0 = offsets[e] + (bx - tile_start[lo]) * BM;
+    const int m0 = offsets[e] + (mt - tile_start[lo]) * BM;
     const int K = GATEUP ? H : I;
     const int n0 = nt * (GATEUP ? BN / 2 : BN);  // first intermediate (gate/up) or output column
     const uint16_t *base = slots[e];
     if (base == nullptr) return;  // no ready copy of this expert: never dereference
     const size_t IH = (size_t)I * H;
 
-    // ---- per-thread global row pointers (fixed over the K loop)
-    const int tid = threadIdx.x;
-    const uint16_t *a_ptr[A_PER];
-    const uint16_t *b_ptr[B_PER];
+    // ---- per-lane source rows: load instruction q of this wave covers tile
+    // rows RPI(wave + NW q) .. +RPI-1; lane l takes row +l/CPR and the
+    // logical chunk that belongs in slot l % CPR of that row (the swizzle)
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int rl = lane / G::CPR, slot = lane % G::CPR;
+    const uint16_t *ap[AL];
+    const uint16_t *bp[BL];
 #pragma unroll
-    for (int q = 0; q < A_PER; ++q) {
-        const int id = q * 256 + tid, r = id >> 3, c = id & 7;
-        const int row = min(m0 + r, row_end - 1);
-        if (GATEUP) a_ptr[q] = a_src + (size_t)perm_token[row] * H + c * 8;
-        else a_ptr[q] = a_src + (size_t)row * I + c * 8;
+    for (int q = 0; q < AL; ++q) {
+        const int row = (wave + NW * q) * G::RPI + rl;
+        const int cs = slot ^ G::key(row);
+        const int gr = min(m0 + row, row_end - 1);
+        ap[q] = GATEUP ? a_src + (size_t)perm_token[gr] * H + cs * 8 : a_src + (size_t)gr * I + cs * 8;
     }
 #pragma unroll
-    for (int q = 0; q < B_PER; ++q) {
-        const int id = q * 256 + tid, r = id >> 3, c = id & 7;
+    for (int q = 0; q < BL; ++q) {
+        const int rb = (wave + NW * q) * G::RPI + rl;
+        const int cs = slot ^ G::key(rb);
         if (GATEUP) {
-            const int i = n0 + (r < BN / 2 ? r : r - BN / 2);
-            b_ptr[q] = base + (r < BN / 2 ? 0 : IH) + (size_t)i * H + c * 8;
+            const int i = n0 + (rb < BN / 2 ? rb : rb - BN / 2);
+            bp[q] = base + (rb < BN / 2 ? 0 : IH) + (size_t)i * H + cs * 8;
         } else {
-            b_ptr[q] = base + 2 * IH + (size_t)(n0 + r) * I + c * 8;
+            bp[q] = base + 2 * IH + (size_t)(n0 + rb) * I + cs * 8;
         }
     }
+    auto issue = [&](int kt) {
+        uint8_t *st = smem + (kt % S) * STAGE;
+        const int k0 = kt * BK;
+#pragma unroll
+        for (int q = 0; q < AL; ++q) load_lds16(ap[q] + k0, st + (wave + NW * q) * 1024);
+#pragma unroll
+        for (int q = 0; q < BL; ++q) load_lds16(bp[q] + k0, st + BM * G::RB + (wave + NW * q) * 1024);
+    };
 
-    u32x4_t ra[A_PER], rb[B_PER];
-#define PD_GLOAD(k0)                                                                            \
-    do {                                                                                        \
-        _Pragma("unroll") for (int q = 0; q < A_PER; ++q) ra[q] = *gptr(a_ptr[q] + (k0));      \
-        _Pragma("unroll") for (int q = 0; q < B_PER; ++q) rb[q] = *gptr(b_ptr[q] + (k0));      \
-    } while (0)
-#define PD_LSTORE(buf)                                                                          \
-    do {                                                                                        \
-        _Pragma("unroll") for (int q = 0; q < A_PER; ++q) {                                    \
-            const int id_ = q * 256 + tid;                                                      \
-            *reinterpret_cast<u32x4_t *>(&s_a[buf][swz(id_ >> 3, id_ & 7)]) = ra[q];          \
-        }                                                                                       \
-        _Pragma("unroll") for (int q = 0; q < B_PER; ++q) {                                    \
-            const int id_ = q * 256 + tid;                                                      \
-            *reinterpret_cast<u32x4_t *>(&s_b[buf][swz(id_ >> 3, id_ & 7)]) = rb[q];          \
-        }                                                                                       \
-    } while (0)
-
-    const int lane = lane_id(), wave = tid >> 6;
     const int wm = wave / WN, wn = wave % WN;
     const int lrow = lane & 31, lhalf = lane >> 5;
-
     f32x16_t acc[MB][NB];
 #pragma unroll
     for (int i = 0; i < MB; ++i)
@@ -114,44 +168,66 @@ __global__ __launch_bounds__(256, 2) void grouped_kernel(
         for (int j = 0; j < NB; ++j) acc[i][j] = f32x16_t{};
 
     // B-tile row of the wave's n-block nb (gate/up pairs share a lane layout)
-#define PD_BROW(nb)                                                                              \
-    (GATEUP ? ((nb) < NB / 2 ? wn * (TN / 2) + (nb) * 32 : BN / 2 + wn * (TN / 2) + ((nb) - NB / 2) * 32) \
-            : wn * TN + (nb) * 32)
+    auto brow = [&](int nb) {
+        return GATEUP ? (nb < NB / 2 ? wn * (TN / 2) + nb * 32 : BN / 2 + wn * (TN / 2) + (nb - NB / 2) * 32)
+                      : wn * TN + nb * 32;
+    };
 
-    const int KT = K / kBK;
-    PD_GLOAD(0);
-    PD_LSTORE(0);
-    __syncthreads();
-    for (int kt = 0; kt < KT; ++kt) {
-        const int buf = kt & 1;
-        if (kt + 1 < KT) PD_GLOAD((kt + 1) * kBK);
+    // 32-row blocks of this wave that hold rows of the expert: a tail m-tile
+    // of a few rows runs MFMAs and fragment reads on its live blocks only.
+    // The count is wave-uniform; the K loop is specialised for each count so
+    // every version stays straight-line code.
+    const int mb_live = __builtin_amdgcn_readfirstlane(min(MB, max(0, (row_end - m0 - wm * TM + 31) / 32)));
+    const int KT = K / BK;
+    auto kloop = [&](auto live) {
+        constexpr int L = decltype(live)::value;
 #pragma unroll
-        for (int kk = 0; kk < kBK / 16; ++kk) {
-            const int chunk = kk * 2 + lhalf;
-            bf16x8_t af[MB], bfr[NB];
+        for (int s0 = 0; s0 < S - 1; ++s0)
+            if (s0 < KT) issue(s0);
+        for (int kt = 0; kt < KT; ++kt) {
+            wait_stage<S, LPW>(min(S - 2, KT - 1 - kt));
+            ring_barrier();  // stage kt landed for every wave; stage kt-1 fully consumed
+            if (kt + S - 1 < KT) issue(kt + S - 1);
+            const uint8_t *st = smem + (kt % S) * STAGE;
+            // fragments of k sub-step kk + 1 are read while sub-step kk's MFMAs run
+            bf16x8_t af[2][MB], bfr[2][NB];
+            auto read_frags = [&](int kk, int buf) {
+                const int c = kk * 2 + lhalf;
 #pragma unroll
-            for (int i = 0; i < MB; ++i) {
-                const int row = wm * TM + i * 32 + lrow;
-                af[i] = *reinterpret_cast<const bf16x8_t *>(&s_a[buf][swz(row, chunk)]);
-            }
-#pragma unroll
-            for (int j = 0; j < NB; ++j) {
-                const int row = PD_BROW(j) + lrow;
-                bfr[j] = *reinterpret_cast<const bf16x8_t *>(&s_b[buf][swz(row, chunk)]);
-            }
-#pragma unroll
-            for (int i = 0; i < MB; ++i)
+                for (int i = 0; i < L; ++i)
+                    af[buf][i] = *reinterpret_cast<const bf16x8_t *>(st + G::off(wm * TM + i * 32 + lrow, c));
 #pragma unroll
                 for (int j = 0; j < NB; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+                    bfr[buf][j] = *reinterpret_cast<const bf16x8_t *>(st + BM * G::RB + G::off(brow(j) + lrow, c));
+            };
+            if constexpr (L > 0) {
+                read_frags(0, 0);
+#pragma unroll
+                for (int kk = 0; kk < BK / 16; ++kk) {
+                    if (kk + 1 < BK / 16) read_frags(kk + 1, (kk + 1) & 1);
+                    __builtin_amdgcn_sched_barrier(0);  // keep the next reads ahead of this step's MFMAs
+#pragma unroll
+                    for (int i = 0; i < L; ++i)
+#pragma unroll
+                        for (int j = 0; j < NB; ++j)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[kk & 1][i], bfr[kk & 1][j],
+                                                                                acc[i][j], 0, 0, 0);
+                }
+            }
         }
-        if (kt + 1 < KT) PD_LSTORE(buf ^ 1);
-        __syncthreads();
+    };
+    if (mb_live >= MB) kloop(std::integral_constant<int, MB>{});
+    else if (mb_live == 0) kloop(std::integral_constant<int, 0>{});
+    else if constexpr (MB >= 2) {
+        if (mb_live == 1) kloop(std::integral_constant<int, 1>{});
+        else if constexpr (MB >= 3) {
+            if (mb_live == 2) kloop(std::integral_constant<int, 2>{});
+            else if constexpr (MB >= 4) {
+                if (mb_live == 3) kloop(std::integral_constant<int, 3>{});
+            }
+        }
     }
 
-#undef PD_GLOAD
-#undef PD_LSTORE
-#undef PD_BROW
     // ---- epilogue: lane holds column (lane & 31), rows (r/4)*8 + (lane/32)*4 + r%4
 #pragma unroll
     for (int i = 0; i < MB; ++i) {
@@ -165,7 +241,7 @@ __global__ __launch_bounds__(256, 2) void grouped_kernel(
                     const int col = n0 + wn * (TN / 2) + j * 32 + lrow;
                     const float g = bf16_round(acc[i][j][r]);
                     const float u = bf16_round(acc[i][j + NB / 2][r]);
-                    const float a = bf16_round(silu_f32(g));
+                    const float a = bf16_round(silu_fast(g));
                     out[(size_t)row * I + col] = (uint16_t)f2bf(a * u);
                 }
             } else {
@@ -180,22 +256,27 @@ __global__ __launch_bounds__(256, 2) void grouped_kernel(
 }
 
 // phase: 1 = gate/up only, 2 = down only, 3 = both
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int BK, int WM, int WN, int S>
 int launch_grouped(int phase, const uint16_t *x, const int32_t *perm_token, const int32_t *offsets,
                    const int32_t *sel, int nsel, const int32_t *tile_start, int max_tiles,
                    const uint16_t *const *slots, int H, int I, uint16_t *h_ws, uint16_t *y, hipStream_t s) {
-    if (I % (BN / 2) || H % BN) return fail(kEInval, "grouped: I must divide by BN/2 and H by BN");
+    if (I % (BN / 2) || H % BN || H % BK || I % BK)
+        return fail(kEInval, "grouped: I must divide by BN/2, H by BN, and both by the K step");
+    // grid: every (m-tile, n-tile) the bound allows, a multiple of 8 so each
+    // XCD's contiguous piece of the tile range has blocks
     if (phase & 1) {
-        const unsigned g1 = (unsigned)((max_tiles + 7) / 8 * 8) * (unsigned)(I / (BN / 2));
-        grouped_kernel<BM, BN, WM, WN, true><<<g1, 256, 0, s>>>(x, perm_token, offsets, sel, nsel, tile_start,
-                                                                 slots, H, I, h_ws);
+        const size_t n1 = (size_t)max_tiles * (size_t)(I / (BN / 2));
+        const unsigned g1 = (unsigned)((n1 + 7) / 8 * 8);
+        grouped_kernel<BM, BN, BK, WM, WN, S, true><<<g1, 64 * WM * WN, 0, s>>>(x, perm_token, offsets, sel, nsel, tile_start,
+                                                                    slots, H, I, h_ws);
         int rc = check_launch("grouped_kernel<gateup>");
         if (rc) return rc;
     }
     if (phase & 2) {
-        const unsigned g2 = (unsigned)((max_tiles + 7) / 8 * 8) * (unsigned)(H / BN);
-        grouped_kernel<BM, BN, WM, WN, false><<<g2, 256, 0, s>>>(h_ws, nullptr, offsets, sel, nsel, tile_start,
-                                                                  slots, H, I, y);
+        const size_t n2 = (size_t)max_tiles * (size_t)(H / BN);
+        const unsigned g2 = (unsigned)((n2 + 7) / 8 * 8);
+        grouped_kernel<BM, BN, BK, WM, WN, S, false><<<g2, 64 * WM * WN, 0, s>>>(h_ws, nullptr, offsets, sel, nsel, tile_start,
+                                                                     slots, H, I, y);
         return check_launch("grouped_kernel<down>");
     }
     return kOk;
@@ -215,16 +296,19 @@ int grouped_entry(int phase, const void *x, const int32_t *perm_token, const int
     const uint16_t *const *sp = (const uint16_t *const *)slots;
     switch (block_m) {
     case 32:
-        return launch_grouped<32, 256, 1, 4>(phase, xp, perm_token, offsets, sel, nsel, tile_start, max_tiles, sp, H,
-                                             I, (uint16_t *)h_ws, (uint16_t *)y, s);
+        return launch_grouped<32, 256, 64, 1, 4, 4>(phase, xp, perm_token, offsets, sel, nsel, tile_start, max_tiles, sp,
+                                                H, I, (uint16_t *)h_ws, (uint16_t *)y, s);
     case 64:
-        return launch_grouped<64, 128, 2, 2>(phase, xp, perm_token, offsets, sel, nsel, tile_start, max_tiles, sp, H,
-                                             I, (uint16_t *)h_ws, (uint16_t *)y, s);
+        return launch_grouped<64, 128, 64, 2, 2, 4>(phase, xp, perm_token, offsets, sel, nsel, tile_start, max_tiles, sp,
+                                                H, I, (uint16_t *)h_ws, (uint16_t *)y, s);
     case 128:
-        return launch_grouped<128, 128, 2, 2>(phase, xp, perm_token, offsets, sel, nsel, tile_start, max_tiles, sp,
-                                              H, I, (uint16_t *)h_ws, (uint16_t *)y, s);
+        return launch_grouped<128, 128, 64, 2, 2, 4>(phase, xp, perm_token, offsets, sel, nsel, tile_start, max_tiles,
+                                                 sp, H, I, (uint16_t *)h_ws, (uint16_t *)y, s);
+    case 256:
+        return launch_grouped<256, 256, 32, 2, 4, 4>(phase, xp, perm_token, offsets, sel, nsel, tile_start, max_tiles,
+                                                 sp, H, I, (uint16_t *)h_ws, (uint16_t *)y, s);
     default:
-        return fail(kEInval, "grouped: block_m must be 32, 64 or 128");
+        return fail(kEInval, "grouped: block_m must be 32, 64, 128 or 256");
     }
 }
 
@@ -232,12 +316,13 @@ int grouped_entry(int phase, const void *x, const int32_t *perm_token, const int
 
 using namespace pd;
 
-// Weights are re-read once per m-tile of an expert, so the row tile should
-// cover a typical expert in one tile; 32 only for very thin experts.
+// The row tile should cover a typical expert in one tile (weights are then
+// read once per expert and n-tile); 32 only for very thin experts.
 PD_API int pdscope_grouped_block_m(int rows_hint) {
     if (rows_hint <= 16) return 32;
-    if (rows_hint <= 80) return 64;
-    return 128;
+    if (rows_hint <= 64) return 64;
+    if (rows_hint <= 160) return 128;
+    return 256;
 }
 
 PD_API int pdscope_swiglu_grouped(const void *x, const int32_t *perm_token, const int32_t *offsets,

@@ -174,7 +174,8 @@ PD_API int pdscope_pack(const int32_t *ids, int T, int k, int E, int32_t *counts
 PD_API int pdscope_schedule(const int32_t *counts, const int32_t *sel, int nsel, int block_m,
                             int32_t *tile_start, void *stream) {
     if (!counts || !sel || !tile_start || nsel < 0) return fail(kEInval, "schedule: bad arguments");
-    if (block_m != 32 && block_m != 64 && block_m != 128) return fail(kEInval, "schedule: block_m must be 32, 64 or 128");
+    if (block_m != 32 && block_m != 64 && block_m != 128 && block_m != 256)
+        return fail(kEInval, "schedule: block_m must be 32, 64, 128 or 256");
     schedule_kernel<<<1, 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(counts, sel, nsel, block_m, tile_start);
     return check_launch("schedule_kernel");
 }

@@ -201,9 +201,9 @@ def test_layer_prefill_qwen(orc, pd, qwen, qwen_host, T):
     assert m["max_rel"] <= MAX_REL and m["mean_abs"] <= MEAN_ABS, m
 
 
-@pytest.mark.parametrize("bm", [32, 64, 128])
+@pytest.mark.parametrize("bm", [32, 64, 128, 256])
 def test_grouped_block_m_variants(orc, pd, bm):
-    """All three row tiles on a small layer with ragged expert sizes (0..many rows)."""
+    """Every row tile on a small layer with ragged expert sizes (0..many rows)."""
     ops, layer, synthetic = pd
     H, I, E, k, T = 256, 128, 32, 4, 150
     lay = synthetic.make_layer(H, I, E, k, True, seed=900 + bm, device=DEV)
@@ -219,6 +219,29 @@ def test_grouped_block_m_variants(orc, pd, bm):
     ik, wk = ids.cpu().numpy(), u16(w)
     ref, _, p = _oracle_layer_given_routing(orc, u16(x), ik, wk, u16(lay.experts), H, I)
     assert p["counts"].max() >= 100  # one expert holds most tokens: many row tiles
+    m = err_metrics(orc.bf16_to_f32(u16(out)), orc.bf16_to_f32(ref))
+    assert m["max_rel"] <= MAX_REL and m["mean_abs"] <= MEAN_ABS, m
+
+
+@pytest.mark.parametrize("bm", [128, 256])
+def test_grouped_qwen_multi_tile_experts(orc, pd, qwen, qwen_host, bm):
+    """Qwen shape with a skewed router: hot experts span several row tiles
+    (and the weight tiles they share), cold ones a partial tile or none."""
+    ops, layer, synthetic = pd
+    T = 600
+    x = synthetic.make_tokens(T, 2048, seed=950 + bm)
+    ws = layer.MoEWorkspace(T, 2048, 768, 128, 8, DEV)
+    slots = ops.slot_table([qwen.experts[e] for e in range(128)], DEV)
+    bias = torch.zeros(128, device=DEV)
+    bias[5], bias[77], bias[100] = 6.0, 5.0, 4.0
+    out, logits, ids, w = layer.moe_forward(x, qwen.gate, slots, ws, bias=bias, block_m=bm)
+    torch.cuda.synchronize()
+    ik, wk = ids.cpu().numpy(), u16(w)
+    ref, y_ref, p = _oracle_layer_given_routing(orc, u16(x), ik, wk, qwen_host["experts"], 2048, 768)
+    assert p["counts"].max() > 2 * bm // 2
+    y_k = u16(ws.y[:T * 8 * 2048]).reshape(T * 8, 2048)
+    m_y = err_metrics(orc.bf16_to_f32(y_k), orc.bf16_to_f32(y_ref))
+    assert m_y["max_rel"] <= MAX_REL and m_y["mean_abs"] <= MEAN_ABS, m_y
     m = err_metrics(orc.bf16_to_f32(u16(out)), orc.bf16_to_f32(ref))
     assert m["max_rel"] <= MAX_REL and m["mean_abs"] <= MEAN_ABS, m
 
