@@ -82,7 +82,7 @@ def run_prefill(T, steps, warmup, n_layers, device, seed0):
         lay, slots = layers[i % n_layers]
         x = xs[i % n_layers]
         logits, ids, w = layer.route(x, lay.gate, ws)
-        ops.pack(ids, E, out=packed)
+        ops.pack(ids, E, out=packed, workspace=ws.pack_ws)
         bm = ops.grouped_block_m(n // E)
         ops.schedule(packed.counts, ws.sel_all, bm, out=ws.tile_start)
         max_tiles = (n + bm - 1) // bm + E

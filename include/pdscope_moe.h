@@ -35,9 +35,14 @@ const char *pdscope_last_error(void);
 /* Library version string. */
 const char *pdscope_version(void);
 
-/* Bytes of zero-initialised device workspace pdscope_route_topk needs
- * (the caller zero-fills it once at allocation; the kernels leave it zeroed). */
+/* Bytes of zero-initialised device workspace pdscope_route_topk needs for
+ * T <= 8 tokens (the caller zero-fills it once; the kernels leave it zeroed). */
 size_t pdscope_route_workspace_bytes(void);
+
+/* Bytes of workspace pdscope_route_topk needs for T tokens of hidden size H
+ * and E experts: the zeroed 256-byte block above, followed (T > 8) by the
+ * split-K partial logits.  Zero-fill once at allocation. */
+size_t pdscope_route_workspace_size(int T, int H, int E);
 
 /*
  * A1 router: replaces `route` (expertbench/adapters/qwen.py:140-152).
@@ -48,7 +53,9 @@ size_t pdscope_route_workspace_bytes(void);
  * x [T,H] bf16, gate [E,H] bf16, bias [E] fp32 or NULL, logits [T,E] bf16,
  * ids [T,k] int32, weights [T,k] bf16, probs [T,E] fp32 or NULL.
  * Limits: E % 32 == 0, E <= 256, 1 <= k <= min(E, 16), H % 16 == 0.
- * workspace: pdscope_route_workspace_bytes() zeroed bytes (used when T <= 8).
+ * workspace: pdscope_route_workspace_size(T, H, E) bytes, zero-filled once.
+ * T > 8 runs two launches (split-K MFMA partial logits, then one wave per
+ * token sums them in a fixed order and routes); T <= 8 one GEMV launch.
  */
 int pdscope_route_topk(const void *x, const void *gate, const float *bias, int T, int H, int E,
                        int k, int normalize, void *logits, int32_t *ids, void *weights,
@@ -69,9 +76,12 @@ int pdscope_route_hist(const int32_t *ids, int n, int E, int32_t *hist, void *st
  * ascending.  Outputs: counts[E], offsets[E+1] (exclusive prefix sum),
  * perm_token[T*k] (token of each grouped row), perm_pos[T*k] (= t*k + s) and
  * row_of[T*k] (grouped row of position t*k+s).  Requires E <= 256.
+ * workspace: pdscope_pack_workspace_size(T, k, E) bytes (NULL when that is
+ * 0: small inputs run one workgroup; larger ones two multi-block launches).
  */
+size_t pdscope_pack_workspace_size(int T, int k, int E);
 int pdscope_pack(const int32_t *ids, int T, int k, int E, int32_t *counts, int32_t *offsets,
-                 int32_t *perm_token, int32_t *perm_pos, int32_t *row_of, void *stream);
+                 int32_t *perm_token, int32_t *perm_pos, int32_t *row_of, void *workspace, void *stream);
 
 /*
  * Tile schedule for pdscope_swiglu_grouped over a subset of experts:

@@ -20,9 +20,11 @@ SIGNATURES = {
     "pdscope_last_error": ([], ctypes.c_char_p),
     "pdscope_version": ([], ctypes.c_char_p),
     "pdscope_route_workspace_bytes": ([], _sz),
+    "pdscope_route_workspace_size": ([_i32, _i32, _i32], _sz),
     "pdscope_route_topk": ([_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp], _i32),
     "pdscope_route_hist": ([_vp, _i32, _i32, _vp, _vp], _i32),
-    "pdscope_pack": ([_vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp], _i32),
+    "pdscope_pack": ([_vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp], _i32),
+    "pdscope_pack_workspace_size": ([_i32, _i32, _i32], _sz),
     "pdscope_schedule": ([_vp, _vp, _i32, _i32, _vp, _vp], _i32),
     "pdscope_grouped_block_m": ([_i32], _i32),
     "pdscope_swiglu_grouped": ([_vp, _vp, _vp, _vp, _i32, _vp, _i32, _i32, _vp, _i32, _i32, _vp, _vp, _vp], _i32),

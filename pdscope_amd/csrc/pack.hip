@@ -2,6 +2,8 @@
 // (expertbench/pdscope_runtime.py:16-39): a stable sort of the slot-major
 // flat expert ids (f = s*T + t), i.e. a counting sort.
 //
+// Up to one chunk of ids (small T): one workgroup of 16 waves (below);
+// larger inputs: one workgroup per chunk in two launches (further down).
 // One workgroup of 16 waves.  Each wave owns a contiguous segment of the
 // flat index space.  Pass 1 counts the segment per expert: a wave splits its
 // 64 ids into equal-id groups with 8 ballots (one per id bit); the lowest
@@ -135,6 +137,130 @@ __global__ __launch_bounds__(1024) void pack_kernel(const int32_t *__restrict__ 
     }
 }
 
+// Multi-block variant for large T*k: the flat index space is cut into
+// chunks of kPackWaves * 64 * kChunkRC ids (one chunk per block, one
+// 64*kChunkRC segment per wave).  pack_count_kernel writes each chunk's
+// per-expert counts to hist[chunk][e]; pack_scatter_kernel recounts its
+// chunk per wave, turns hist into the chunk's bases (expert offset plus the
+// counts of earlier chunks) and scatters exactly as the single-block kernel,
+// so the grouping is identical.
+constexpr int kChunkRC = 2;
+constexpr int kChunkIds = kPackWaves * 64 * kChunkRC;
+
+__device__ __forceinline__ void chunk_load(const int32_t *__restrict__ ids, int T, int k, int E, int beg, int end,
+                                           int lane, int (&idv)[kChunkRC]) {
+    const int last = max(end - 1, 0);
+    int raw[kChunkRC];
+#pragma unroll
+    for (int c = 0; c < kChunkRC; ++c) {
+        const int f = min(beg + c * 64 + lane, last);
+        const int s = f / T, t = f - s * T;
+        raw[c] = ids[(size_t)t * k + s];
+    }
+#pragma unroll
+    for (int c = 0; c < kChunkRC; ++c) {
+        const int f = beg + c * 64 + lane;
+        const int e = raw[c];
+        idv[c] = (f < end && e >= 0 && e < E) ? e : -1;
+    }
+}
+
+// per-wave counts of this wave's segment into s_cnt[wave][*] (zeroed here)
+__device__ __forceinline__ void chunk_count(const int (&idv)[kChunkRC], int beg, int end, int E, int wave, int lane,
+                                            int32_t (*s_cnt)[kPackMaxE]) {
+    const uint64_t below = (1ull << lane) - 1ull;
+    for (int e = lane; e < E; e += 64) s_cnt[wave][e] = 0;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int c = 0; c < kChunkRC; ++c) {
+        if (beg + c * 64 >= end) break;
+        const int e = idv[c];
+        const uint64_t m = group_mask(e < 0 ? 0 : e, e >= 0);
+        if (e >= 0 && !(m & below)) s_cnt[wave][e] += __popcll(m);
+    }
+}
+
+__global__ __launch_bounds__(1024) void pack_count_kernel(const int32_t *__restrict__ ids, int T, int k, int E,
+                                                          int32_t *__restrict__ hist) {
+    __shared__ int32_t s_cnt[kPackWaves][kPackMaxE];
+    const int n = T * k;
+    const int wave = threadIdx.x >> 6, lane = lane_id();
+    const int beg = min((int)blockIdx.x * kChunkIds + wave * 64 * kChunkRC, n);
+    const int end = min(beg + 64 * kChunkRC, n);
+    int idv[kChunkRC];
+    chunk_load(ids, T, k, E, beg, end, lane, idv);
+    chunk_count(idv, beg, end, E, wave, lane, s_cnt);
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+        int tot = 0;
+        for (int w = 0; w < kPackWaves; ++w) tot += s_cnt[w][e];
+        hist[(size_t)blockIdx.x * E + e] = tot;
+    }
+}
+
+__global__ __launch_bounds__(1024) void pack_scatter_kernel(const int32_t *__restrict__ ids, int T, int k, int E,
+                                                            const int32_t *__restrict__ hist, int nchunk,
+                                                            int32_t *__restrict__ counts,
+                                                            int32_t *__restrict__ offsets,
+                                                            int32_t *__restrict__ perm_token,
+                                                            int32_t *__restrict__ perm_pos,
+                                                            int32_t *__restrict__ row_of) {
+    __shared__ int32_t s_cnt[kPackWaves][kPackMaxE];
+    __shared__ int s_wsum[4];
+    const int n = T * k;
+    const int wave = threadIdx.x >> 6, lane = lane_id();
+    const int beg = min((int)blockIdx.x * kChunkIds + wave * 64 * kChunkRC, n);
+    const int end = min(beg + 64 * kChunkRC, n);
+    const uint64_t below = (1ull << lane) - 1ull;
+    int idv[kChunkRC];
+    chunk_load(ids, T, k, E, beg, end, lane, idv);
+    chunk_count(idv, beg, end, E, wave, lane, s_cnt);
+    int tot = 0, pre = 0;
+    if (threadIdx.x < E) {
+        const int e = threadIdx.x;
+        for (int b = 0; b < nchunk; ++b) {
+            const int c = hist[(size_t)b * E + e];
+            tot += c;
+            if (b < (int)blockIdx.x) pre += c;
+        }
+    }
+    __syncthreads();
+    const int incl = block_scan256(threadIdx.x < 256 ? tot : 0, s_wsum);
+    if (threadIdx.x < E) {
+        const int e = threadIdx.x;
+        const int off = incl - tot;
+        if (blockIdx.x == 0) {
+            counts[e] = tot;
+            offsets[e] = off;
+            if (e == E - 1) offsets[E] = incl;
+        }
+        int run = off + pre;
+        for (int w = 0; w < kPackWaves; ++w) {
+            const int c = s_cnt[w][e];
+            s_cnt[w][e] = run;
+            run += c;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < kChunkRC; ++c) {
+        if (beg + c * 64 >= end) break;
+        const int e = idv[c];
+        const uint64_t m = group_mask(e < 0 ? 0 : e, e >= 0);
+        if (e >= 0) {
+            const int f = beg + c * 64 + lane;
+            const int s = f / T, t = f - s * T;
+            const int pos = s_cnt[wave][e] + __popcll(m & below);
+            perm_token[pos] = t;
+            perm_pos[pos] = t * k + s;
+            row_of[(size_t)t * k + s] = pos;
+            if (!(m & below)) s_cnt[wave][e] += __popcll(m);
+        }
+    }
+}
+
 __global__ __launch_bounds__(256) void schedule_kernel(const int32_t *__restrict__ counts,
                                                        const int32_t *__restrict__ sel, int nsel, int bm,
                                                        int32_t *__restrict__ tile_start) {
@@ -160,15 +286,37 @@ __global__ __launch_bounds__(256) void schedule_kernel(const int32_t *__restrict
 
 using namespace pd;
 
+// above this many ids the two-launch multi-block path is used
+constexpr int kPackMultiMin = kChunkIds;
+
+PD_API size_t pdscope_pack_workspace_size(int T, int k, int E) {
+    if (T < 1 || k < 1 || E < 1) return 0;
+    const int64_t n = (int64_t)T * k;
+    if (n <= kPackMultiMin) return 0;
+    return (size_t)((n + kChunkIds - 1) / kChunkIds) * (size_t)E * sizeof(int32_t);
+}
+
 PD_API int pdscope_pack(const int32_t *ids, int T, int k, int E, int32_t *counts, int32_t *offsets,
-                        int32_t *perm_token, int32_t *perm_pos, int32_t *row_of, void *stream) {
+                        int32_t *perm_token, int32_t *perm_pos, int32_t *row_of, void *workspace, void *stream) {
     if (!ids || !counts || !offsets || !perm_token || !perm_pos || !row_of)
         return fail(kEInval, "pack: null pointer");
     if (T < 1 || k < 1 || E < 1 || E > kPackMaxE) return fail(kEInval, "pack: need T,k >= 1 and 1 <= E <= 256");
     if ((int64_t)T * k > (1ll << 30)) return fail(kEInval, "pack: T*k too large");
-    pack_kernel<<<1, 1024, 0, reinterpret_cast<hipStream_t>(stream)>>>(ids, T, k, E, counts, offsets,
-                                                                       perm_token, perm_pos, row_of);
-    return check_launch("pack_kernel");
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const int n = T * k;
+    if (n <= kPackMultiMin) {
+        pack_kernel<<<1, 1024, 0, s>>>(ids, T, k, E, counts, offsets, perm_token, perm_pos, row_of);
+        return check_launch("pack_kernel");
+    }
+    if (!workspace) return fail(kEInval, "pack: T*k above the single-block size needs pdscope_pack_workspace_size bytes");
+    const int nchunk = (n + kChunkIds - 1) / kChunkIds;
+    int32_t *hist = static_cast<int32_t *>(workspace);
+    pack_count_kernel<<<nchunk, 1024, 0, s>>>(ids, T, k, E, hist);
+    int rc = check_launch("pack_count_kernel");
+    if (rc) return rc;
+    pack_scatter_kernel<<<nchunk, 1024, 0, s>>>(ids, T, k, E, hist, nchunk, counts, offsets, perm_token, perm_pos,
+                                                row_of);
+    return check_launch("pack_scatter_kernel");
 }
 
 PD_API int pdscope_schedule(const int32_t *counts, const int32_t *sel, int nsel, int block_m,

@@ -1,6 +1,9 @@
 // K1: router logits + fp32 softmax + top-k (ties -> lower id) + renorm.
 // Restates expertbench/adapters/qwen.py:140-152 (route) on gfx950, and the
 // predictor histogram of expertbench/pdscope_runtime.py:245-249.
+// T <= 8: one GEMV launch whose last block routes every token.  T > 8:
+// split-K MFMA partial logits, then one wave per token sums them in a fixed
+// order and routes.
 #include "common.h"
 #include "topk.h"
 
@@ -77,79 +80,82 @@ __global__ __launch_bounds__(256) void route_gemv_kernel(
     if (threadIdx.x == 0) atomicExch(counter, 0u);
 }
 
-// Prefill path: a block owns 32 tokens and all E = 32*NB experts.  The four
-// waves split H into quarters; each wave runs NB independent
-// v_mfma_f32_32x32x16_bf16 accumulator chains over its quarter with the next
-// step's operands prefetched into registers.  The four partial sums are
-// added in LDS in wave order (a fixed order, so logits are deterministic),
-// rounded to bf16 and routed in the same block.
-template <int NB>
-__global__ __launch_bounds__(256) void route_mfma_kernel(
-    const uint16_t *__restrict__ x, const uint16_t *__restrict__ gate, const float *__restrict__ bias,
-    int T, int H, int k, int normalize, uint16_t *__restrict__ logits, int32_t *__restrict__ ids,
-    uint16_t *__restrict__ weights, float *__restrict__ probs) {
-    constexpr int E = NB * 32;
-    extern __shared__ float s_part[];  // [32][E]: summed partials, then bf16-rounded logits
-    __shared__ TopkScratch s_tk[4];
-    const int lane = lane_id();
-    const int wave = threadIdx.x >> 6;
-    const int t0 = blockIdx.x * 32;
-    const int ntok = min(32, T - t0);
-    const int trow = t0 + min(lane & 31, ntok - 1);
-    const int kq = H >> 2;
-    const int kbase = wave * kq + (lane >> 5) * 8;
-    const uint16_t *xrow = x + (size_t)trow * H + kbase;
-    const uint16_t *grow = gate + (size_t)(lane & 31) * H + kbase;
-    const size_t gstride = (size_t)32 * H;
+// Prefill path, two launches.
+// route_partial_kernel: split-K logits.  Block (token tile of 32, K chunk ks)
+// has E/32 waves; wave w computes the 32 x 32 tile of tokens x experts
+// [32w, 32w + 32) over its K chunk of 16*STEPS elements with
+// v_mfma_f32_32x32x16_bf16, all operand loads issued up front (one memory
+// latency per block), and stores the fp32 partial to part[ks][t][e].
+template <int STEPS>
+__global__ __launch_bounds__(512) void route_partial_kernel(const uint16_t *__restrict__ x,
+                                                            const uint16_t *__restrict__ gate, int T, int H, int E,
+                                                            float *__restrict__ part) {
+    const int lane = lane_id(), wave = threadIdx.x >> 6;
+    const int t0 = blockIdx.x * 32, ks = blockIdx.y;
+    const int k0 = ks * STEPS * 16 + (lane >> 5) * 8;
+    const int trow = min(t0 + (lane & 31), T - 1);
+    const int e = wave * 32 + (lane & 31);
+    const uint16_t *xa = x + (size_t)trow * H + k0;
+    const uint16_t *gb = gate + (size_t)e * H + k0;
+    bf16x8_t a[STEPS], b[STEPS];
+#pragma unroll
+    for (int st = 0; st < STEPS; ++st) {
+        a[st] = *reinterpret_cast<const bf16x8_t *>(xa + 16 * st);
+        b[st] = *reinterpret_cast<const bf16x8_t *>(gb + 16 * st);
+    }
+    f32x16_t acc = f32x16_t{};
+#pragma unroll
+    for (int st = 0; st < STEPS; ++st) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[st], b[st], acc, 0, 0, 0);
+    // lane holds expert column e, token rows (r/4)*8 + (lane/32)*4 + r%4
+    float *dst = part + (size_t)ks * T * E + e;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int t = t0 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+        if (t < T) dst[(size_t)t * E] = acc[r];
+    }
+}
 
-    f32x16_t acc[NB];
+// route_finish_kernel: one wave per token sums the KS partials in chunk
+// order, rounds to the bf16 logit and runs the softmax / top-k / renorm.
+template <int J>
+__global__ __launch_bounds__(256) void route_finish_kernel(const float *__restrict__ part, int KS, int T, int E,
+                                                           const float *__restrict__ bias, int k, int normalize,
+                                                           uint16_t *__restrict__ logits, int32_t *__restrict__ ids,
+                                                           uint16_t *__restrict__ weights, float *__restrict__ probs) {
+    __shared__ float s_logit[4][64 * J];
+    __shared__ TopkScratch s_tk[4];
+    const int lane = lane_id(), wave = threadIdx.x >> 6;
+    const int t = blockIdx.x * 4 + wave;
+    if (t >= T) return;
+    float v[J];
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x16_t{};
-    bf16x8_t a_cur = *reinterpret_cast<const bf16x8_t *>(xrow);
-    bf16x8_t b_cur[NB];
+    for (int j = 0; j < J; ++j) v[j] = 0.0f;
+    for (int ks = 0; ks < KS; ++ks) {
+        const float *row = part + ((size_t)ks * T + t) * E;
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) b_cur[nb] = *reinterpret_cast<const bf16x8_t *>(grow + nb * gstride);
-    for (int k0 = 16; k0 <= kq; k0 += 16) {
-        bf16x8_t a_nxt = a_cur, b_nxt[NB];
-        const bool more = k0 < kq;
-        if (more) a_nxt = *reinterpret_cast<const bf16x8_t *>(xrow + k0);
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            b_nxt[nb] = b_cur[nb];
-            if (more) b_nxt[nb] = *reinterpret_cast<const bf16x8_t *>(grow + nb * gstride + k0);
+        for (int j = 0; j < J; ++j) {
+            const int e = lane + 64 * j;
+            if (e < E) v[j] = v[j] + row[e];
         }
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-            acc[nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_cur, b_cur[nb], acc[nb], 0, 0, 0);
-        a_cur = a_nxt;
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) b_cur[nb] = b_nxt[nb];
     }
-    // fixed-order reduction ((p0 + p1) + p2) + p3: the waves add their
-    // partials into one LDS tile in turn
-#pragma unroll 1
-    for (int w = 0; w < 4; ++w) {
-        if (wave == w) {
 #pragma unroll
-            for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int tt = (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-                    float *dst = s_part + tt * E + nb * 32 + (lane & 31);
-                    *dst = (w == 0) ? acc[nb][r] : *dst + acc[nb][r];
-                }
+    for (int j = 0; j < J; ++j) {
+        const int e = lane + 64 * j;
+        if (e < E) {
+            const uint32_t hb = f2bf(v[j]);
+            logits[(size_t)t * E + e] = (uint16_t)hb;
+            s_logit[wave][e] = bf2f(hb);
         }
-        __syncthreads();
     }
-    for (int i = threadIdx.x; i < 32 * E; i += 256) {
-        const uint32_t hb = f2bf(s_part[i]);
-        s_part[i] = bf2f(hb);
-        const int tt = i / E;
-        if (tt < ntok) logits[(size_t)(t0 + tt) * E + (i - tt * E)] = (uint16_t)hb;
-    }
-    __syncthreads();
-    topk_tokens_block<(NB * 32 + 63) / 64>(s_part, ntok, E, bias, k, normalize, t0, ids,
-                                                                 weights, probs, s_tk);
+    wave_lds_sync();
+    topk_token<J>(s_logit[wave], bias, E, k, normalize, t, ids, weights, probs, &s_tk[wave]);
+}
+
+// K chunk of the split-K router: 256 elements (16 MFMA steps) when H allows.
+static int route_kchunk(int H) {
+    for (int kc = 256; kc >= 16; kc >>= 1)
+        if (H % kc == 0) return kc;
+    return 0;
 }
 
 __global__ __launch_bounds__(1024) void route_hist_kernel(const int32_t *__restrict__ ids, int n, int E,
@@ -171,6 +177,16 @@ using namespace pd;
 
 PD_API size_t pdscope_route_workspace_bytes(void) { return 256; }
 
+// Bytes of workspace pdscope_route_topk needs for T tokens: the zeroed
+// 256-byte counter of the small-T path, then (T > 8) the split-K partial
+// logits (fp32, H / kchunk x T x E).
+PD_API size_t pdscope_route_workspace_size(int T, int H, int E) {
+    if (T <= kGemvMaxT) return 256;
+    const int kc = route_kchunk(H);
+    if (kc == 0 || E < 1) return 256;
+    return 256 + (size_t)(H / kc) * (size_t)T * (size_t)E * sizeof(float);
+}
+
 PD_API int pdscope_route_topk(const void *x, const void *gate, const float *bias, int T, int H, int E,
                               int k, int normalize, void *logits, int32_t *ids, void *weights,
                               float *probs, void *workspace, void *stream) {
@@ -178,9 +194,9 @@ PD_API int pdscope_route_topk(const void *x, const void *gate, const float *bias
     if (T < 1 || H < 16 || H % 16) return fail(kEInval, "route: need T >= 1 and H % 16 == 0");
     if (E < 32 || E > 256 || E % 32) return fail(kEInval, "route: need E % 32 == 0 and E <= 256");
     if (k < 1 || k > 16 || k > E) return fail(kEInval, "route: need 1 <= k <= min(E, 16)");
+    if (!workspace) return fail(kEInval, "route: workspace (pdscope_route_workspace_size bytes) is required");
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     if (T <= kGemvMaxT) {
-        if (!workspace) return fail(kEInval, "route: small-T path needs the zeroed workspace");
         const int nch = (H / 8 + 63) / 64;
         switch (nch) {
 #define PD_RG(N)                                                                                           \
@@ -196,22 +212,34 @@ PD_API int pdscope_route_topk(const void *x, const void *gate, const float *bias
         }
         return check_launch("route_gemv_kernel");
     }
-    if (H % 64) return fail(kEInval, "route: prefill path needs H % 64 == 0");
-    const size_t lds = (size_t)32 * E * sizeof(float);
-    const int blocks = (T + 31) / 32;
-    switch (E / 32) {
-#define PD_RT(NB)                                                                                          \
-    case NB:                                                                                               \
-        route_mfma_kernel<NB><<<blocks, 256, lds, s>>>((const uint16_t *)x, (const uint16_t *)gate, bias, T, H, k, \
-                                                      normalize, (uint16_t *)logits, ids, (uint16_t *)weights,     \
-                                                      probs);                                              \
+    const int kc = route_kchunk(H);
+    const int KS = H / kc;
+    float *part = reinterpret_cast<float *>(static_cast<char *>(workspace) + 256);
+    const dim3 g1((T + 31) / 32, KS);
+    const int threads = (E / 32) * 64;
+    switch (kc / 16) {
+#define PD_RP(ST)                                                                                           \
+    case ST:                                                                                                \
+        route_partial_kernel<ST><<<g1, threads, 0, s>>>((const uint16_t *)x, (const uint16_t *)gate, T, H, E, part); \
         break;
-        PD_RT(1) PD_RT(2) PD_RT(3) PD_RT(4) PD_RT(5) PD_RT(6) PD_RT(7) PD_RT(8)
-#undef PD_RT
+        PD_RP(1) PD_RP(2) PD_RP(4) PD_RP(8) PD_RP(16)
+#undef PD_RP
     default:
-        return fail(kEInval, "route: unsupported E");
+        return fail(kEInval, "route: unsupported K chunk");
     }
-    return check_launch("route_mfma_kernel");
+    int rc = check_launch("route_partial_kernel");
+    if (rc) return rc;
+    const int g2 = (T + 3) / 4;
+    if (E <= 64)
+        route_finish_kernel<1><<<g2, 256, 0, s>>>(part, KS, T, E, bias, k, normalize, (uint16_t *)logits, ids,
+                                                 (uint16_t *)weights, probs);
+    else if (E <= 128)
+        route_finish_kernel<2><<<g2, 256, 0, s>>>(part, KS, T, E, bias, k, normalize, (uint16_t *)logits, ids,
+                                                 (uint16_t *)weights, probs);
+    else
+        route_finish_kernel<4><<<g2, 256, 0, s>>>(part, KS, T, E, bias, k, normalize, (uint16_t *)logits, ids,
+                                                 (uint16_t *)weights, probs);
+    return check_launch("route_finish_kernel");
 }
 
 PD_API int pdscope_route_hist(const int32_t *ids, int n, int E, int32_t *hist, void *stream) {

@@ -38,7 +38,9 @@ class MoEWorkspace:
         self.y = torch.empty(rows * H, dtype=BF16, device=device)
         self.out = torch.empty((1 if route_only else max_tokens, H), dtype=BF16, device=device)
         self.hist = torch.empty(E, **i32)
-        ops.route_workspace(device)
+        self.route_ws = ops.new_route_workspace(max_tokens, H, E, device)
+        self.pack_ws = torch.empty(max(ops.pack_workspace_size(max_tokens, k, E), 4), dtype=torch.uint8,
+                                   device=device)
 
     def views(self, T: int):
         if not 0 < T <= self.max_tokens:
@@ -50,7 +52,7 @@ class MoEWorkspace:
 
 def route(x, gate, ws: MoEWorkspace, *, normalize=True, bias=None):
     logits, ids, weights, _ = ws.views(x.shape[0])
-    ops.route_topk(x, gate, ws.k, normalize, bias=bias, out=(logits, ids, weights))
+    ops.route_topk(x, gate, ws.k, normalize, bias=bias, out=(logits, ids, weights), workspace=ws.route_ws)
     return logits, ids, weights
 
 
@@ -63,7 +65,7 @@ def experts_resident(x, ids, weights, slots, ws: MoEWorkspace, out=None, *, bloc
         ops.swiglu_decode(x, ids, weights, slots, H, I, ws.h_ws, out)
         return out
     _, _, _, packed = ws.views(T)
-    ops.pack(ids, E, out=packed)
+    ops.pack(ids, E, out=packed, workspace=ws.pack_ws)
     bm = block_m or ops.grouped_block_m((T * k) // E)
     ops.schedule(packed.counts, ws.sel_all, bm, out=ws.tile_start)
     max_tiles = (T * k + bm - 1) // bm + E

@@ -42,13 +42,26 @@ def _need(t, name, dtype=None, ndim=None, device=None):
 _route_ws = {}
 
 
-def route_workspace(device) -> torch.Tensor:
-    """Zero-filled device scratch for the small-T router (kept zero by the kernel)."""
+def route_workspace_size(T: int, H: int, E: int) -> int:
+    return int(_lib.load().pdscope_route_workspace_size(int(T), int(H), int(E)))
+
+
+def new_route_workspace(T: int, H: int, E: int, device) -> torch.Tensor:
+    """Router scratch for up to T tokens: a zeroed counter (kept zero by the
+    small-T kernel) followed by the split-K partial logits."""
+    return torch.zeros(route_workspace_size(T, H, E), dtype=torch.uint8, device=device)
+
+
+def route_workspace(device, T: int = 1, H: int = 16, E: int = 32) -> torch.Tensor:
+    """Shared per-device router scratch, grown to cover (T, H, E) (not for
+    graph capture: capture with a workspace you own)."""
     device = torch.device(device)
+    if device.index is None:
+        device = torch.device(device.type, torch.cuda.current_device())
+    need = route_workspace_size(T, H, E)
     ws = _route_ws.get(device)
-    if ws is None:
-        n = int(_lib.load().pdscope_route_workspace_bytes())
-        ws = torch.zeros(n, dtype=torch.uint8, device=device)
+    if ws is None or ws.numel() < need:
+        ws = torch.zeros(need, dtype=torch.uint8, device=device)
         _route_ws[device] = ws
     return ws
 
@@ -60,7 +73,7 @@ def slot_table(tensors, device) -> torch.Tensor:
 
 # --------------------------------------------------------------------- A1/A2
 
-def route_topk(x, gate, top_k, normalize, *, bias=None, capture_probabilities=False, out=None):
+def route_topk(x, gate, top_k, normalize, *, bias=None, capture_probabilities=False, out=None, workspace=None):
     """K1 router.  Returns (logits bf16 [T,E], ids int32 [T,k], weights bf16 [T,k], probs|None)."""
     _need(x, "inputs", BF16, 2)
     _need(gate, "gate", BF16, 2, x.device)
@@ -81,8 +94,12 @@ def route_topk(x, gate, top_k, normalize, *, bias=None, capture_probabilities=Fa
     else:
         logits, ids, weights = out
     probs = torch.empty((T, E), dtype=torch.float32, device=x.device) if capture_probabilities else None
+    if workspace is None:
+        workspace = route_workspace(x.device, T, H, E)
+    elif workspace.numel() < route_workspace_size(T, H, E):
+        raise ValueError("router workspace too small for this token count")
     _lib.call("pdscope_route_topk", _p(x), _p(gate), _p(bias), T, H, E, top_k, int(bool(normalize)),
-              _p(logits), _p(ids), _p(weights), _p(probs), _p(route_workspace(x.device)), _stream(x.device))
+              _p(logits), _p(ids), _p(weights), _p(probs), _p(workspace), _stream(x.device))
     return logits, ids, weights, probs
 
 
@@ -104,7 +121,11 @@ class Packed:
     row_of: torch.Tensor      # int32 [T*k]
 
 
-def pack(ids, E, out: Packed | None = None) -> Packed:
+def pack_workspace_size(T: int, k: int, E: int) -> int:
+    return int(_lib.load().pdscope_pack_workspace_size(int(T), int(k), int(E)))
+
+
+def pack(ids, E, out: Packed | None = None, workspace=None) -> Packed:
     _need(ids, "ids", torch.int32, 2)
     T, k = ids.shape
     dev = ids.device
@@ -113,8 +134,11 @@ def pack(ids, E, out: Packed | None = None) -> Packed:
         out = Packed(torch.empty(E, dtype=torch.int32, device=dev), torch.empty(E + 1, dtype=torch.int32, device=dev),
                      torch.empty(n, dtype=torch.int32, device=dev), torch.empty(n, dtype=torch.int32, device=dev),
                      torch.empty(n, dtype=torch.int32, device=dev))
+    need = pack_workspace_size(T, k, E)
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
     _lib.call("pdscope_pack", _p(ids), T, k, E, _p(out.counts), _p(out.offsets), _p(out.perm_token),
-              _p(out.perm_pos), _p(out.row_of), _stream(dev))
+              _p(out.perm_pos), _p(out.row_of), _p(workspace) if need else None, _stream(dev))
     return out
 
 

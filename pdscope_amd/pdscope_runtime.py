@@ -200,7 +200,7 @@ class PDScopeCudaRuntime:
             ops.route_hist(nids, E, out=nws.hist)
         _, _, _, packed = ws.views(T)
         if T > 1:
-            ops.pack(ids, E, out=packed)
+            ops.pack(ids, E, out=packed, workspace=ws.pack_ws)
             counts_dev = packed.counts
         else:
             counts_dev = ids.reshape(-1)
@@ -250,7 +250,7 @@ class PDScopeCudaRuntime:
                 raise AssertionError(f"experts {missing} of layer {layer} have no ready device copy")
         decode_fast = (T == 1 and not demand and not graph_path)
         if T == 1 and demand:
-            ops.pack(ids, E, out=packed)  # decode misses take the grouped path
+            ops.pack(ids, E, out=packed, workspace=ws.pack_ws)  # decode misses take the grouped path
         if graph_path:
             # the replay already produced `out`; account the uses it made
             tasks.append(ex.gpu_group([key(e) for e in resident], lambda: None, wait_for=cur))

@@ -40,7 +40,7 @@ def test_invalid_arguments_raise_before_any_launch():
     """Argument validation happens on the host and maps to ValueError."""
     from pdscope_amd import _lib
     with pytest.raises(ValueError):
-        _lib.call("pdscope_pack", None, 1, 1, 1, None, None, None, None, None, None)
+        _lib.call("pdscope_pack", None, 1, 1, 1, None, None, None, None, None, None, None)
     with pytest.raises(ValueError):
         _lib.call("pdscope_route_topk", None, None, None, 1, 2048, 128, 8, 1, None, None, None, None, None, None)
     with pytest.raises(ValueError):

@@ -139,7 +139,7 @@ def _pack_check(orc, ops, ids_np, E):
 
 
 @pytest.mark.parametrize("T,k,E", [(1, 8, 128), (7, 8, 128), (512, 8, 128), (4096, 8, 128), (1304, 6, 64),
-                                   (3, 1, 32), (1000, 16, 256)])
+                                   (3, 1, 32), (1000, 16, 256), (4099, 8, 128), (20000, 6, 64), (16384, 8, 128)])
 def test_pack_uniform(orc, pd, T, k, E):
     ops, _, _ = pd
     rng = np.random.default_rng(T * 31 + k)
