@@ -48,7 +48,34 @@ def parse():
     ap.add_argument("--no-extra", action="store_true", help="only the main workload")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, cpus) - 1")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run 5 device copies of 1 GiB (calibrates the FETCH_SIZE / WRITE_SIZE counters)")
     return ap.parse_args()
+
+
+def calibrate_copy():
+    """Five dst.copy_(src) of 1 GiB each: a kernel with known HBM traffic
+    (1 GiB read + 1 GiB written per dispatch) for counter calibration."""
+    import torch
+    n = 1 << 30
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "device copy", "bytes_read": n, "bytes_written": n, "dispatches": 5}))
+
+
+def traffic_from_profiles(name):
+    """HBM bytes per launch of the dominant kernel, from the committed counter
+    summary profiles/<name> (line 'traffic_bytes_per_launch: N'), or None."""
+    import re
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", name)
+    try:
+        m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(path).read())
+    except OSError:
+        return None
+    return float(m.group(1)) if m else None
 
 
 def log(msg):
@@ -318,6 +345,9 @@ def main():
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the MoE layer path here is "
               "single-GPU and multi-GPU figures are not measured", file=sys.stderr)
         sys.exit(2)
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
     import torch
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from pdscope_amd import _lib
@@ -363,7 +393,7 @@ def main():
     else:
         roof = dict(main["hbm"])
     roof["kernel"] = main["kernel"]
-    roof["traffic"] = None
+    roof["traffic"] = traffic_from_profiles(f"{args.workload}_traffic.md")
     cfg_name = {"prefill512": "Qwen3-30B-A3B-shaped MoE layer, prefill T=512 uniform routing, 128 experts resident",
                 "decode": "Qwen3-30B-A3B-shaped MoE layer, decode T=1, 128 experts resident (hipGraph per layer)",
                 "prefill4096": "Qwen3-30B-A3B-shaped MoE layer, prefill T=4096 uniform routing, 128 experts resident"}
