@@ -44,7 +44,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="prefill512", choices=["prefill512", "decode", "prefill4096"])
+    ap.add_argument("--workload", default="prefill512", choices=["prefill512", "decode", "prefill4096", "dsv2_mixed"])
     ap.add_argument("--no-extra", action="store_true", help="only the main workload")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, cpus) - 1")
@@ -215,6 +215,60 @@ def run_decode(steps, warmup, n_layers, device, seed0):
                 layers=n_layers, first_layer=layers[0], first_x=xs[0], ws=wss[0])
 
 
+def run_dsv2_mixed(steps, warmup, n_layers, device, seed0):
+    """DeepSeek-V2-Lite layer (64 routed experts of 1408, top-6 without
+    renormalisation, 2 shared experts as one 2816 MLP) on one mixed ragged
+    batch: 48 decode tokens + chunked-prefill segments of 256 and 1000 tokens
+    in one launch (the MoE math is per token, so segments only set T)."""
+    import torch
+    from pdscope_amd import layer, ops, synthetic
+    cfg = synthetic.DSV2
+    Hd, Id, Ed, kd, Is = cfg["H"], cfg["I"], cfg["E"], cfg["k"], cfg["shared_I"]
+    T = 48 + 256 + 1000
+    lays = []
+    for i in range(n_layers):
+        lay = synthetic.make_layer(Hd, Id, Ed, kd, False, seed=seed0 + 5000 + 1000 * i, device=device, shared_I=Is)
+        lays.append((lay, ops.slot_table([lay.experts[e] for e in range(Ed)], device),
+                     ops.slot_table([lay.shared], device)))
+    xs = [synthetic.make_tokens(T, Hd, seed=seed0 + 5007 + 1000 * i, device=device) for i in range(n_layers)]
+    ws = layer.MoEWorkspace(T, Hd, Id, Ed, kd, device, shared_I=Is)
+    stream = torch.cuda.current_stream(device)
+
+    def step(i):
+        lay, slots, shared = lays[i % n_layers]
+        layer.moe_forward(xs[i % n_layers], lay.gate, slots, ws, normalize=False, shared_slot=shared)
+
+    touched = []
+    for i in range(n_layers):
+        step(i)
+        torch.cuda.synchronize(device)
+        touched.append(int((ws.counts > 0).sum().item()))
+    for i in range(warmup):
+        step(i)
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    torch.cuda.synchronize(device)
+    t0 = time.perf_counter()
+    events[0].record(stream)
+    for i in range(steps):
+        step(i)
+        events[i + 1].record(stream)
+    torch.cuda.synchronize(device)
+    wall = time.perf_counter() - t0
+    layer_ms = [events[i].elapsed_time(events[i + 1]) for i in range(steps)]
+    mean_touched = sum(touched[i % n_layers] for i in range(steps)) / steps
+    expert = 3 * Id * Hd * 2
+    layer_bytes = mean_touched * expert + 3 * Is * Hd * 2 + Ed * Hd * 2 + 2 * T * Hd * 2
+    layer_flops = 2.0 * T * kd * 3 * Id * Hd + 2.0 * T * 3 * Is * Hd + 2.0 * T * Ed * Hd
+    t = statistics.mean(layer_ms) / 1e3
+    hbm = dict(bound="hbm", achieved=layer_bytes / t / 1e9, peak=HBM_PEAK_GBS, unit="GB/s")
+    hbm["frac"] = hbm["achieved"] / hbm["peak"]
+    return dict(tok_s=T * steps / wall, ms_per_step=wall / steps * 1e3, kernel="whole layer (events per step)",
+                kernel_ms_mean=statistics.mean(layer_ms), kernel_ms_median=statistics.median(layer_ms),
+                experts_touched=mean_touched, tokens=T, layers_rotated=n_layers, hbm=hbm,
+                layer_tflops=layer_flops / t / 1e12, layer_bytes=layer_bytes,
+                shape=dict(hidden=Hd, experts=Ed, intermediate=Id, top_k=kd, shared_intermediate=Is))
+
+
 # ----------------------------------------------------------------------------- CPU baseline
 
 def cpu_threads(requested):
@@ -356,20 +410,24 @@ def main():
     torch.cuda.set_device(device)
     threads = cpu_threads(args.cpu_threads)
 
-    plan = {"prefill512": ("prefill", 512, 4), "decode": ("decode", 1, 16), "prefill4096": ("prefill", 4096, 2)}
+    plan = {"prefill512": ("prefill", 512, 4), "decode": ("decode", 1, 16), "prefill4096": ("prefill", 4096, 2),
+            "dsv2_mixed": ("dsv2", 1304, 4)}
     order = [args.workload] + ([] if args.no_extra else [w for w in plan if w != args.workload])
     records, raw = {}, {}
     for wl in order:
         kind, T, nl = plan[wl]
         main_leg = wl == args.workload
-        steps = args.steps if main_leg else {"prefill512": 200, "decode": 2000, "prefill4096": 50}[wl]
-        warmup = args.warmup if main_leg else {"prefill512": 20, "decode": 200, "prefill4096": 5}[wl]
+        steps = args.steps if main_leg else {"prefill512": 200, "decode": 2000, "prefill4096": 50, "dsv2_mixed": 100}[wl]
+        warmup = args.warmup if main_leg else {"prefill512": 20, "decode": 200, "prefill4096": 5, "dsv2_mixed": 10}[wl]
         if kind == "decode":
             steps = max(steps, 1)
         log(f"[bench] {wl}: T={T} layers={nl} steps={steps} warmup={warmup}")
         if kind == "prefill":
             res = run_prefill(T, steps, warmup, nl, device, 20261011)
             rec = prefill_record(res)
+        elif kind == "dsv2":
+            res = run_dsv2_mixed(steps, warmup, nl, device, 20261011)
+            rec = dict(res)
         else:
             res = run_decode(steps, warmup, nl, device, 20261011)
             rec = decode_record(res)
@@ -394,7 +452,9 @@ def main():
         roof = dict(main["hbm"])
     roof["kernel"] = main["kernel"]
     roof["traffic"] = traffic_from_profiles(f"{args.workload}_traffic.md")
-    cfg_name = {"prefill512": "Qwen3-30B-A3B-shaped MoE layer, prefill T=512 uniform routing, 128 experts resident",
+    cfg_name = {"dsv2_mixed": "DeepSeek-V2-Lite-shaped MoE layer (64 x 1408 routed top-6, 2 shared), mixed batch "
+                              "48 decode + 256 + 1000 prefill tokens",
+                "prefill512": "Qwen3-30B-A3B-shaped MoE layer, prefill T=512 uniform routing, 128 experts resident",
                 "decode": "Qwen3-30B-A3B-shaped MoE layer, decode T=1, 128 experts resident (hipGraph per layer)",
                 "prefill4096": "Qwen3-30B-A3B-shaped MoE layer, prefill T=4096 uniform routing, 128 experts resident"}
     kind, T, nl = plan[args.workload]
@@ -411,8 +471,9 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (seeded random bf16 weights ~N(0,0.02), activations ~N(0,1))",
-        "config": {"workload": cfg_name[args.workload], "tokens": T, "hidden": H, "experts": E,
-                   "intermediate": I, "top_k": K_TOP, "layers_rotated": nl, "parallelism": "single GPU"},
+        "config": {"workload": cfg_name[args.workload], "tokens": T,
+                   **main.get("shape", dict(hidden=H, experts=E, intermediate=I, top_k=K_TOP)),
+                   "layers_rotated": nl, "parallelism": "single GPU"},
         "roofline": roof,
         "cpu_baseline": {k: v for k, v in main.get("cpu_baseline", {}).items() if k in
                          ("value", "unit", "cores", "kind", "sample")} or None,

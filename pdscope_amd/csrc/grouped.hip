@@ -61,11 +61,20 @@ __device__ __forceinline__ void wait_vm() {
 // (wait_stage), this wave's LDS reads are complete (lgkmcnt 0) before the
 // slot they read can be refilled, and the memory clobber keeps the
 // compiler from moving LDS accesses across the barrier.
-__device__ __forceinline__ void ring_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+__device__ __forceinline__ void ring_barrier() {
+    // lgkmcnt(0) through the builtin, so the compiler's own wait analysis
+    // knows every earlier LDS read has completed here
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    asm volatile("s_barrier" ::: "memory");
+}
 
+// Wait until the stage to be consumed has landed, `younger` (0 .. S-2)
+// later stages being allowed to stay in flight.
 template <int S, int LPW>
 __device__ __forceinline__ void wait_stage(int younger) {
-    // `younger` stages were issued after the one to be consumed
+    if constexpr (S >= 5) {
+        if (younger >= 3) { wait_vm<3 * LPW>(); return; }
+    }
     if constexpr (S >= 4) {
         if (younger >= 2) { wait_vm<2 * LPW>(); return; }
     }
@@ -179,42 +188,65 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void grouped_kernel(
     // every version stays straight-line code.
     const int mb_live = __builtin_amdgcn_readfirstlane(min(MB, max(0, (row_end - m0 - wm * TM + 31) / 32)));
     const int KT = K / BK;
+    // Software-pipelined K loop.  Slot kt % S holds stage kt; stages kt+1 ..
+    // kt+S-1 are in flight while stage kt is consumed.  Each iteration waits
+    // for stage kt+1, synchronises the block (every wave has then also
+    // finished reading stage kt, whose fragments are in registers), refills
+    // slot kt % S with stage kt+S, reads stage kt+1's fragments from LDS and
+    // then runs stage kt's MFMAs, so the LDS reads overlap the MFMAs.
     auto kloop = [&](auto live) {
         constexpr int L = decltype(live)::value;
-#pragma unroll
-        for (int s0 = 0; s0 < S - 1; ++s0)
-            if (s0 < KT) issue(s0);
-        for (int kt = 0; kt < KT; ++kt) {
-            wait_stage<S, LPW>(min(S - 2, KT - 1 - kt));
-            ring_barrier();  // stage kt landed for every wave; stage kt-1 fully consumed
-            if (kt + S - 1 < KT) issue(kt + S - 1);
+        constexpr int KK = BK / 16;
+        bf16x8_t af[2][KK][MB], bfr[2][KK][NB];
+        auto read_frags = [&](int kt, int buf) {
             const uint8_t *st = smem + (kt % S) * STAGE;
-            // fragments of k sub-step kk + 1 are read while sub-step kk's MFMAs run
-            bf16x8_t af[2][MB], bfr[2][NB];
-            auto read_frags = [&](int kk, int buf) {
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk) {
                 const int c = kk * 2 + lhalf;
 #pragma unroll
                 for (int i = 0; i < L; ++i)
-                    af[buf][i] = *reinterpret_cast<const bf16x8_t *>(st + G::off(wm * TM + i * 32 + lrow, c));
+                    af[buf][kk][i] = *reinterpret_cast<const bf16x8_t *>(st + G::off(wm * TM + i * 32 + lrow, c));
 #pragma unroll
                 for (int j = 0; j < NB; ++j)
-                    bfr[buf][j] = *reinterpret_cast<const bf16x8_t *>(st + BM * G::RB + G::off(brow(j) + lrow, c));
-            };
-            if constexpr (L > 0) {
-                read_frags(0, 0);
-#pragma unroll
-                for (int kk = 0; kk < BK / 16; ++kk) {
-                    if (kk + 1 < BK / 16) read_frags(kk + 1, (kk + 1) & 1);
-                    __builtin_amdgcn_sched_barrier(0);  // keep the next reads ahead of this step's MFMAs
-#pragma unroll
-                    for (int i = 0; i < L; ++i)
-#pragma unroll
-                        for (int j = 0; j < NB; ++j)
-                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[kk & 1][i], bfr[kk & 1][j],
-                                                                                acc[i][j], 0, 0, 0);
-                }
+                    bfr[buf][kk][j] =
+                        *reinterpret_cast<const bf16x8_t *>(st + BM * G::RB + G::off(brow(j) + lrow, c));
             }
+        };
+        auto mfmas = [&](int buf) {
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+                for (int i = 0; i < L; ++i)
+#pragma unroll
+                    for (int j = 0; j < NB; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[buf][kk][i], bfr[buf][kk][j],
+                                                                            acc[i][j], 0, 0, 0);
+        };
+#pragma unroll
+        for (int s0 = 0; s0 < S; ++s0)
+            if (s0 < KT) issue(s0);
+        wait_stage<S + 1, LPW>(min(S - 1, KT - 1));
+        ring_barrier();
+        if constexpr (L > 0) read_frags(0, 0);
+        // one pipeline step consuming stage kt from fragment buffer CUR
+        auto step = [&](int kt, auto cur_c) {
+            constexpr int CUR = decltype(cur_c)::value;
+            if (kt + 1 < KT) {
+                wait_stage<S, LPW>(min(S - 2, KT - 2 - kt));  // stage kt+1 landed
+                ring_barrier();
+                if (kt + S < KT) issue(kt + S);  // into slot kt % S, read out before the barrier
+                if constexpr (L > 0) read_frags(kt + 1, CUR ^ 1);
+            }
+            __builtin_amdgcn_sched_barrier(0);  // keep the next stage's reads ahead of these MFMAs
+            if constexpr (L > 0) mfmas(CUR);
+        };
+        // unrolled by two so the fragment buffers are indexed statically
+        int kt = 0;
+        for (; kt + 1 < KT; kt += 2) {
+            step(kt, std::integral_constant<int, 0>{});
+            step(kt + 1, std::integral_constant<int, 1>{});
         }
+        if (kt < KT) step(kt, std::integral_constant<int, 0>{});
     };
     if (mb_live >= MB) kloop(std::integral_constant<int, MB>{});
     else if (mb_live == 0) kloop(std::integral_constant<int, 0>{});

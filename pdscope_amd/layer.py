@@ -18,7 +18,8 @@ BF16 = torch.bfloat16
 class MoEWorkspace:
     """Device buffers for up to ``max_tokens`` tokens of one layer shape."""
 
-    def __init__(self, max_tokens: int, H: int, I: int, E: int, k: int, device, *, route_only: bool = False):
+    def __init__(self, max_tokens: int, H: int, I: int, E: int, k: int, device, *, route_only: bool = False,
+                 shared_I: int | None = None):
         device = torch.device(device)
         n = max_tokens * k
         i32 = dict(dtype=torch.int32, device=device)
@@ -41,6 +42,15 @@ class MoEWorkspace:
         self.route_ws = ops.new_route_workspace(max_tokens, H, E, device)
         self.pack_ws = torch.empty(max(ops.pack_workspace_size(max_tokens, k, E), 4), dtype=torch.uint8,
                                    device=device)
+        # always-on shared experts (one fused MLP of intermediate shared_I over every token)
+        self.shared_I = shared_I
+        if shared_I:
+            self.h_shared = torch.empty(max_tokens * shared_I, dtype=BF16, device=device)
+            self.y_shared = torch.empty((max_tokens, H), dtype=BF16, device=device)
+            self.shared_rows = torch.arange(max_tokens, **i32)
+            self.shared_offsets = torch.zeros(2, **i32)
+            self.shared_tiles = torch.zeros(2, **i32)
+            self.shared_sel = torch.zeros(1, **i32)
 
     def views(self, T: int):
         if not 0 < T <= self.max_tokens:
@@ -56,12 +66,43 @@ def route(x, gate, ws: MoEWorkspace, *, normalize=True, bias=None):
     return logits, ids, weights
 
 
-def experts_resident(x, ids, weights, slots, ws: MoEWorkspace, out=None, *, block_m=None):
-    """K4 (T == 1) or K2+K3+K5 (T > 1) over experts that are all addressable in `slots`."""
+# column width of the gate|up tile for each row-tile height of the grouped kernel
+_GATEUP_COLS = {32: 128, 64: 64, 128: 64, 256: 128}
+
+
+def shared_block_m(T: int, I: int, min_tiles: int = 512) -> int:
+    """Row-tile height for a single dense expert over T rows: the tallest tile
+    whose gate|up launch still has min_tiles workgroups (two per CU), since
+    one expert with few row tiles cannot fill 256 CUs with 256-row tiles."""
+    for bm in (256, 128, 64):
+        if I % _GATEUP_COLS[bm] == 0 and ((T + bm - 1) // bm) * (I // _GATEUP_COLS[bm]) >= min_tiles:
+            return bm
+    return 32 if T <= 16 else 64
+
+
+def shared_forward(x, shared_slot, ws: MoEWorkspace):
+    """Always-on shared experts (DeepSeek-V2 `shared_experts`, one MLP of
+    intermediate ws.shared_I applied to every token, unweighted): the grouped
+    SwiGLU kernel with a single 'expert' whose rows are all T tokens in order.
+    shared_slot: int64 [1] device table holding the shared gate|up|down block.
+    Returns y_shared [T, H] bf16."""
+    T = x.shape[0]
+    H, Is = ws.H, ws.shared_I
+    bm = shared_block_m(T, Is)
+    ws.shared_offsets[1:].fill_(T)
+    ws.shared_tiles[1:].fill_((T + bm - 1) // bm)
+    ops.swiglu_grouped(x, ws.shared_rows[:T], ws.shared_offsets, ws.shared_sel, ws.shared_tiles,
+                       (T + bm - 1) // bm, bm, shared_slot, H, Is, ws.h_shared, ws.y_shared)
+    return ws.y_shared[:T]
+
+
+def experts_resident(x, ids, weights, slots, ws: MoEWorkspace, out=None, *, block_m=None, add_in=None):
+    """K4 (T == 1) or K2+K3+K5 (T > 1) over experts that are all addressable in `slots`.
+    add_in [T, H] bf16 (shared-expert output) is added unweighted in the merge."""
     T = x.shape[0]
     H, I, E, k = ws.H, ws.I, ws.E, ws.k
     out = ws.out[:T] if out is None else out
-    if T == 1:
+    if T == 1 and add_in is None:
         ops.swiglu_decode(x, ids, weights, slots, H, I, ws.h_ws, out)
         return out
     _, _, _, packed = ws.views(T)
@@ -71,17 +112,27 @@ def experts_resident(x, ids, weights, slots, ws: MoEWorkspace, out=None, *, bloc
     max_tiles = (T * k + bm - 1) // bm + E
     ops.swiglu_grouped(x, packed.perm_token, packed.offsets, ws.sel_all, ws.tile_start, max_tiles, bm, slots, H, I,
                        ws.h_ws, ws.y)
-    ops.merge(ws.y, packed.row_of, weights, out)
+    ops.merge(ws.y, packed.row_of, weights, out, add_in=add_in)
     return out
 
 
-def moe_forward(x, gate, slots, ws: MoEWorkspace, *, normalize=True, bias=None, block_m=None, fused_decode=True):
+def moe_forward(x, gate, slots, ws: MoEWorkspace, *, normalize=True, bias=None, block_m=None, fused_decode=True,
+                shared_slot=None):
     """Full layer: returns (out [T,H] bf16, logits, ids int32 [T,k], weights bf16 [T,k]).
 
     T == 1 runs the single-launch decode kernel (K4f) when the shape and the
     device allow it (fused_decode), else route (K1) + decode GEMV (K4).
+    shared_slot (int64 [1] device table) adds always-on shared experts
+    (DeepSeek-V2); the workspace must have been built with shared_I.
     """
     T = x.shape[0]
+    if shared_slot is not None:
+        if not ws.shared_I:
+            raise ValueError("shared experts need a workspace built with shared_I")
+        logits, ids, weights = route(x, gate, ws, normalize=normalize, bias=bias)
+        y_shared = shared_forward(x, shared_slot, ws)
+        out = experts_resident(x, ids, weights, slots, ws, block_m=block_m, add_in=y_shared)
+        return out, logits, ids, weights
     if (T == 1 and fused_decode and ws.k <= 8
             and ops.decode_layer_supported(ws.H, ws.I, ws.E, ws.k, x.device)):
         logits, ids, weights, _ = ws.views(1)

@@ -318,3 +318,35 @@ def test_stage_merge_matches_bf16_index_add(pd):
         ref = (ref.float() + prod[r].float()).to(torch.bfloat16)
     assert torch.equal(out.cpu()[0], ref)
     assert torch.equal(scratch.cpu(), block)
+
+
+def test_deepseek_v2_lite_layer_with_shared_experts(orc, pd):
+    """DeepSeek-V2-Lite layer: 64 routed experts of 1408, top-6 without
+    renormalisation, plus 2 shared experts (one 2816-wide MLP over every
+    token, added unweighted in the merge).  Routing bit-exact given the
+    logits; routed rows and the layer output within bf16 tolerance."""
+    ops, layer, synthetic = pd
+    cfg = dict(synthetic.DSV2)
+    H, I, E, k, Is = cfg["H"], cfg["I"], cfg["E"], cfg["k"], cfg["shared_I"]
+    lay = synthetic.make_layer(H, I, E, k, False, seed=321, device=DEV, shared_I=Is)
+    T = 40
+    x = synthetic.make_tokens(T, H, seed=322)
+    ws = layer.MoEWorkspace(T, H, I, E, k, DEV, shared_I=Is)
+    slots = ops.slot_table([lay.experts[e] for e in range(E)], DEV)
+    shared_slot = ops.slot_table([lay.shared], DEV)
+    out, logits, ids, w = layer.moe_forward(x, lay.gate, slots, ws, normalize=False, shared_slot=shared_slot)
+    torch.cuda.synchronize()
+    ik, wk = ids.cpu().numpy(), u16(w)
+    oi, ow = orc.route_from_logits(u16(logits), k, False)
+    assert np.array_equal(ik, oi) and np.array_equal(wk, ow)
+    xu = u16(x)
+    _, y_ref, p = _oracle_layer_given_routing(orc, xu, ik, wk, u16(lay.experts), H, I)
+    sh = u16(lay.shared)
+    IsH = Is * H
+    shared_ref = orc.expert_forward(xu, sh[:IsH].reshape(Is, H), sh[IsH:2 * IsH].reshape(Is, H),
+                                    sh[2 * IsH:].reshape(H, Is))
+    m_s = err_metrics(orc.bf16_to_f32(u16(ws.y_shared[:T])), orc.bf16_to_f32(shared_ref))
+    assert m_s["max_rel"] <= MAX_REL and m_s["mean_abs"] <= MEAN_ABS, m_s
+    ref = orc.merge(y_ref, p["row_of"], wk, add_in=shared_ref)
+    m = err_metrics(orc.bf16_to_f32(u16(out)), orc.bf16_to_f32(ref))
+    assert m["max_rel"] <= MAX_REL and m["mean_abs"] <= MEAN_ABS, m
