@@ -1,7 +1,8 @@
 #!/usr/bin/env python3
 """MoE-layer benchmark on one MI355X: Qwen3-30B-A3B-shaped layers, seeded random weights.
 
-    python bench.py [--steps K] [--warmup W] [--workload prefill512|decode|prefill4096]
+    python bench.py [--steps K] [--warmup W]
+                    [--workload prefill512|decode|prefill4096|prefill4096_zipf|dsv2_mixed]
 
 A step is one MoE layer forward over one batch of synthetic tokens whose
 inputs and weights are already resident in HBM: route (K1) -> pack (K2) ->
@@ -12,7 +13,9 @@ independently seeded layer copies so the 256 MB Infinity Cache cannot hold
 the streamed weights between steps.
 
 The default workload is the T = 512 prefill (128 experts, top-8, all resident).
-The same JSON line also carries the T = 1 decode and T = 4096 prefill results
+The same JSON line also carries the T = 1 decode, the T = 4096 prefill (all
+resident, and Zipf-skewed with 32 resident experts and 8 demand staging slots
+through the runtime) and the DeepSeek-V2-Lite mixed-batch results
 ("workloads"), each with its own roofline figure, and a CPU baseline: the
 AVX2 bf16 SwiGLU expert kernel under oracle/ (a stand-in for ktransformers'
 AVX2BF16_MOE, which is not available offline) timed on this host's cores on
@@ -44,7 +47,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="prefill512", choices=["prefill512", "decode", "prefill4096", "dsv2_mixed"])
+    ap.add_argument("--workload", default="prefill512",
+                    choices=["prefill512", "decode", "prefill4096", "prefill4096_zipf", "dsv2_mixed"])
     ap.add_argument("--no-extra", action="store_true", help="only the main workload")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, cpus) - 1")
@@ -213,6 +217,122 @@ def run_decode(steps, warmup, n_layers, device, seed0):
                 layer_ms_mean=statistics.mean(layer_ms), layer_ms_median=statistics.median(layer_ms),
                 three_launch_layer_ms=statistics.median(layer_ms3), steps_run=n_steps,
                 layers=n_layers, first_layer=layers[0], first_x=xs[0], ws=wss[0])
+
+
+def run_zipf_staged(steps, warmup, n_layers, device, seed0):
+    """T = 4096 prefill through the drop-in runtime (PDScopeCudaRuntime.forward)
+    with a Zipf(1.1) router bias: per layer the 32 hottest experts are resident
+    in the cache pool and every other touched expert is copied from pinned
+    host memory into one of 8 demand staging slots, its grouped launch
+    following its copy while the next copies stream.  A step is one whole
+    layer call (host-synchronous, as the runtime is), timed by wall clock."""
+    import torch
+    from pdscope_amd import ops, synthetic
+    from pdscope_amd.cache import ExpertKey
+    from pdscope_amd.executor import masters_from_block
+    from pdscope_amd.pdscope_runtime import PDScopeCudaRuntime
+    T = 4096
+    bias, perm = synthetic.zipf_bias(E, 1.1, seed=seed0, device=device)
+    hottest = sorted(range(E), key=lambda e: int(perm[e]))[:32]
+    gates, masters, hot = [], {}, []
+    for i in range(n_layers):
+        lay = synthetic.make_layer(H, I, E, K_TOP, True, seed=seed0 + 9000 + 1000 * i, device=device)
+        masters.update(masters_from_block(i, lay.experts, E, H, I))
+        gates.append(lay.gate)
+        hot += [ExpertKey(i, e, "bf16") for e in hottest]
+        if i == 0:
+            lay0 = lay
+        del lay
+    torch.cuda.empty_cache()
+    xs = [synthetic.make_tokens(T, H, seed=seed0 + 9007 + 1000 * i, device=device) for i in range(n_layers)]
+    rt = PDScopeCudaRuntime(masters, hot_keys=hot, speculative_slots=0, demand_slots=8, device=device)
+    try:
+        def step(i):
+            # one request per pass over the rotated layers (the ledger orders events per request)
+            return rt.forward(xs[i % n_layers], gates[i % n_layers], layer=i % n_layers, step=0, top_k=K_TOP,
+                              request=f"bench{i // n_layers}", bias=bias, prefetch=False)
+
+        warmup = -(-warmup // n_layers) * n_layers  # whole passes, so timed passes start at layer 0
+        for i in range(warmup):
+            step(i)
+        torch.cuda.synchronize(device)
+        rows, times = [], []
+        t0 = time.perf_counter()
+        for i in range(warmup, warmup + steps):
+            a = time.perf_counter()
+            _, _, row = step(i)
+            torch.cuda.synchronize(device)
+            times.append(time.perf_counter() - a)
+            rows.append(row)
+        wall = time.perf_counter() - t0
+        n_demand = [len(r["decision"]["on_demand_queue"]) for r in rows]
+        n_touched = [len(r["token_counts"]) for r in rows]
+        h2d = [r["counters"].get("h2d_bytes_completed", 0) for r in rows]
+        max_rows = max(max(r["token_counts"].values()) for r in rows)
+        # the copy engine alone: the same number of expert blocks, back to back, into the staging slots
+        srcs = [masters[ExpertKey(0, e, "bf16")].flat for e in range(E) if e not in hottest]
+        dst = rt.executor.staging
+        s = torch.cuda.Stream(device)
+        nc = len(srcs)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for j, src in enumerate(srcs):
+            ops.stage_expert(dst[j % len(dst)][:EXPERT_BYTES], src.view(torch.uint8), stream=s)
+        e1.record(s)
+        torch.cuda.synchronize(device)
+        copy_gbs = nc * EXPERT_BYTES / (e0.elapsed_time(e1) / 1e3) / 1e9
+    finally:
+        rt.close()
+    gemm = zipf_gemm(lay0, xs[0], bias, device)
+    del lay0
+    t = statistics.mean(times)
+    h2d_mean = statistics.mean(h2d)
+    pcie = dict(bound="pcie_h2d", achieved=h2d_mean / t / 1e9, peak=copy_gbs, unit="GB/s",
+                peak_kind="measured back-to-back expert copies on this host")
+    pcie["frac"] = pcie["achieved"] / pcie["peak"]
+    flops = 2.0 * T * K_TOP * 3 * I * H
+    return dict(tok_s=T * steps / wall, ms_per_step=wall / steps * 1e3, kernel="whole layer through the runtime",
+                kernel_ms_mean=t * 1e3, kernel_ms_median=statistics.median(times) * 1e3,
+                resident_experts=len(hottest), demand_slots=8, experts_touched=statistics.mean(n_touched),
+                demand_experts=statistics.mean(n_demand), h2d_bytes_per_layer=h2d_mean,
+                max_rows_per_expert=max_rows, pcie=pcie, layer_tflops=flops / t / 1e12,
+                layers_rotated=n_layers, copy_only_ms=nc * EXPERT_BYTES / copy_gbs / 1e6, grouped_gemm=gemm)
+
+
+def zipf_gemm(lay, x, bias, device, reps=20):
+    """The grouped SwiGLU GEMM alone over the Zipf-skewed routing of one layer
+    with every expert in HBM: gate/up and down launches bracketed by HIP
+    events; useful flops = 2 * T * k * 3 * I * H (no tile padding)."""
+    import torch
+    from pdscope_amd import layer, ops
+    T = x.shape[0]
+    ws = layer.MoEWorkspace(T, H, I, E, K_TOP, device)
+    slots = ops.slot_table([lay.experts[e] for e in range(E)], device)
+    _, ids, _ = layer.route(x, lay.gate, ws, bias=bias)
+    _, _, _, packed = ws.views(T)
+    ops.pack(ids, E, out=packed, workspace=ws.pack_ws)
+    bm = ops.grouped_block_m((T * K_TOP) // E)
+    ops.schedule(packed.counts, ws.sel_all, bm, out=ws.tile_start)
+    max_tiles = (T * K_TOP + bm - 1) // bm + E
+    stream = torch.cuda.current_stream(device)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(reps + 2)]
+    for r in range(reps + 2):
+        ev[r][0].record(stream)
+        ops.swiglu_grouped_gateup(x, packed.perm_token, packed.offsets, ws.sel_all, ws.tile_start, max_tiles, bm,
+                                  slots, H, I, ws.h_ws)
+        ev[r][1].record(stream)
+        ops.swiglu_grouped_down(ws.h_ws, packed.offsets, ws.sel_all, ws.tile_start, max_tiles, bm, slots, H, I,
+                                ws.y)
+        ev[r][2].record(stream)
+    torch.cuda.synchronize(device)
+    gu = statistics.mean(ev[r][0].elapsed_time(ev[r][1]) for r in range(2, reps + 2))
+    dn = statistics.mean(ev[r][1].elapsed_time(ev[r][2]) for r in range(2, reps + 2))
+    counts = ws.counts.cpu().tolist()
+    flops = 2.0 * T * K_TOP * 3 * I * H
+    achieved = flops / ((gu + dn) / 1e3) / 1e12
+    return dict(gateup_ms=gu, down_ms=dn, block_m=bm, max_rows=max(counts), experts_touched=sum(c > 0 for c in counts),
+                mfma=dict(bound="mfma", achieved=achieved, peak=BF16_PEAK_TFLOPS, unit="TFLOP/s",
+                          frac=achieved / BF16_PEAK_TFLOPS))
 
 
 def run_dsv2_mixed(steps, warmup, n_layers, device, seed0):
@@ -411,14 +531,16 @@ def main():
     threads = cpu_threads(args.cpu_threads)
 
     plan = {"prefill512": ("prefill", 512, 4), "decode": ("decode", 1, 16), "prefill4096": ("prefill", 4096, 2),
-            "dsv2_mixed": ("dsv2", 1304, 4)}
+            "prefill4096_zipf": ("zipf", 4096, 2), "dsv2_mixed": ("dsv2", 1304, 4)}
     order = [args.workload] + ([] if args.no_extra else [w for w in plan if w != args.workload])
     records, raw = {}, {}
     for wl in order:
         kind, T, nl = plan[wl]
         main_leg = wl == args.workload
-        steps = args.steps if main_leg else {"prefill512": 200, "decode": 2000, "prefill4096": 50, "dsv2_mixed": 100}[wl]
-        warmup = args.warmup if main_leg else {"prefill512": 20, "decode": 200, "prefill4096": 5, "dsv2_mixed": 10}[wl]
+        steps = args.steps if main_leg else {"prefill512": 200, "decode": 2000, "prefill4096": 50, "prefill4096_zipf": 20,
+                                                       "dsv2_mixed": 100}[wl]
+        warmup = args.warmup if main_leg else {"prefill512": 20, "decode": 200, "prefill4096": 5, "prefill4096_zipf": 2,
+                                                        "dsv2_mixed": 10}[wl]
         if kind == "decode":
             steps = max(steps, 1)
         log(f"[bench] {wl}: T={T} layers={nl} steps={steps} warmup={warmup}")
@@ -428,12 +550,16 @@ def main():
         elif kind == "dsv2":
             res = run_dsv2_mixed(steps, warmup, nl, device, 20261011)
             rec = dict(res)
+        elif kind == "zipf":
+            res = run_zipf_staged(steps, warmup, nl, device, 20261011)
+            rec = dict(res)
         else:
             res = run_decode(steps, warmup, nl, device, 20261011)
             rec = decode_record(res)
         rec["steps"], rec["warmup"] = res.get("steps_run", steps), warmup
+        bw = rec.get("hbm") or rec["pcie"]
         log(f"[bench] {wl}: {rec['tok_s']:.1f} tok/s, {rec['ms_per_step']:.4f} ms/step, kernel "
-            f"{rec['kernel_ms_mean']:.4f} ms, {rec['hbm']['achieved']:.0f} GB/s")
+            f"{rec['kernel_ms_mean']:.4f} ms, {bw['achieved']:.0f} GB/s ({bw['bound']})")
         records[wl] = rec
         raw[wl] = res
         if not args.no_cpu_baseline and wl in ("prefill512", "decode"):
@@ -448,6 +574,8 @@ def main():
     main = records[args.workload]
     if args.workload == "prefill4096":
         roof = dict(main["mfma"])
+    elif args.workload == "prefill4096_zipf":
+        roof = dict(main["pcie"])
     else:
         roof = dict(main["hbm"])
     roof["kernel"] = main["kernel"]
@@ -456,7 +584,9 @@ def main():
                               "48 decode + 256 + 1000 prefill tokens",
                 "prefill512": "Qwen3-30B-A3B-shaped MoE layer, prefill T=512 uniform routing, 128 experts resident",
                 "decode": "Qwen3-30B-A3B-shaped MoE layer, decode T=1, 128 experts resident (hipGraph per layer)",
-                "prefill4096": "Qwen3-30B-A3B-shaped MoE layer, prefill T=4096 uniform routing, 128 experts resident"}
+                "prefill4096": "Qwen3-30B-A3B-shaped MoE layer, prefill T=4096 uniform routing, 128 experts resident",
+                "prefill4096_zipf": "Qwen3-30B-A3B-shaped MoE layer, prefill T=4096 with a Zipf(1.1) router bias, "
+                                    "32 experts resident, the rest staged through 8 demand slots"}
     kind, T, nl = plan[args.workload]
     line = {
         "metric": METRIC,

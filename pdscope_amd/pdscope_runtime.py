@@ -15,9 +15,10 @@ One layer call:
  3. every routed expert with a cache copy runs in ONE grouped launch (K3; K4
     for a fully resident decode token) on the compute stream;
  4. experts without a copy stream through the demand staging slots: copy on
-    the load stream, grouped launch over that slot when its event completed,
-    slot released after the compute event (ping-pong depth slots-1 for
-    prefill, 1 for decode, as pdscope_runtime.py:361);
+    the load stream, grouped launch over the staged batch when its copy
+    events completed, slots released after the compute event (ping-pong as
+    pdscope_runtime.py:361 with one expert per launch, or two halves of the
+    slot budget from 6 slots on, see _demand_pipeline);
  5. predicted next-layer experts are prefetched into the cache pool
     (speculative_slots bound, LRU eviction, never evicting the static hot set);
  6. the merge (K5) writes the layer output in token order.
@@ -231,16 +232,23 @@ class PDScopeCudaRuntime:
         observed = dict(self.prediction_counts[phase])
 
         # ---- plan: every expert on the GPU; resident first, misses through staging
-        resident = sorted((e for e in counts if self.cache.lookup(key(e)) is not None),
-                          key=lambda e: (-counts[e], e))
-        demand = sorted((e for e in counts if e not in set(resident)), key=lambda e: (-counts[e], e))
+        views = {e: self.cache.lookup(key(e)) for e in counts}
+        resident = sorted((e for e in counts if views[e] is not None), key=lambda e: (-counts[e], e))
+        demand = sorted((e for e in counts if views[e] is None), key=lambda e: (-counts[e], e))
         for e in resident:
-            view = self.cache.lookup(key(e))
-            if view.state == "loading":
-                self.executor.finish_load(view.ticket, wait=True)
+            if views[e].state == "loading":
+                self.executor.finish_load(views[e].ticket, wait=True)
                 self.pending.pop(key(e), None)
 
         ex = self.executor
+        # first demand copies go out before the resident launch is prepared
+        batches, inflight, nxt = [], [], 0
+        if demand:
+            group, held = self._demand_pipeline(phase)
+            batches = [demand[i:i + group] for i in range(0, len(demand), group)]
+            while nxt < min(held, len(batches)):
+                inflight.append([ex.load(key(e), admit=False) for e in batches[nxt]])
+                nxt += 1
         slots_dev = None
         tasks = []
 
@@ -265,36 +273,32 @@ class PDScopeCudaRuntime:
                 sel_dev = ex.upload_ints(resident, ex.compute_stream)
 
                 def launch():
-                    self._grouped(x, packed, sel_dev, T, k, slots_dev, ws)
+                    self._grouped(x, packed, sel_dev, [counts[e] for e in resident], slots_dev, ws)
             tasks.append(ex.gpu_group([key(e) for e in resident], launch, input_ref=x, wait_for=cur))
 
         # ---- demand misses through the staging slots
         ping_pong = []
         if demand:
-            depth = max(1, min(self.demand_slots - 1 if phase == "prefill" else 1, len(demand)))
-            inflight = []
-            nxt = 0
-            while nxt < depth:
-                inflight.append(ex.load(key(demand[nxt]), admit=False))
-                nxt += 1
-            for e in demand:
-                ticket = inflight.pop(0)
-                ex.finish_load(ticket, wait=True)
+            for batch in batches:
+                tickets = inflight.pop(0)
+                for ticket in tickets:
+                    ex.finish_load(ticket, wait=True)
                 ex.table(layer, E)
-                require_copies([e])
+                require_copies(batch)
                 tab = ex.upload_table(layer, E, ex.compute_stream)
-                sel_dev = ex.upload_ints([e], ex.compute_stream)
+                sel_dev = ex.upload_ints(batch, ex.compute_stream)
 
-                def launch(sel_dev=sel_dev, tab=tab):
-                    self._grouped(x, packed, sel_dev, T, k, tab, ws)
-                comp = ex.gpu_group([key(e)], launch, input_ref=x, wait_for=cur)
-                ping_pong.append(dict(expert=e, slot=ticket.slot, generation=ticket.generation))
-                if nxt < len(demand):
-                    inflight.append(ex.load(key(demand[nxt]), admit=False))
-                    nxt += 1
-                if len({t.slot for t in inflight}) != len(inflight):
+                def launch(sel_dev=sel_dev, tab=tab, rows=[counts[e] for e in batch]):
+                    self._grouped(x, packed, sel_dev, rows, tab, ws)
+                comp = ex.gpu_group([key(e) for e in batch], launch, input_ref=x, wait_for=cur)
+                ping_pong += [dict(expert=e, slot=t.slot, generation=t.generation) for e, t in zip(batch, tickets)]
+                live = [t.slot for b in inflight for t in b]
+                if len(set(live)) != len(live) or set(live) & {t.slot for t in tickets}:
                     raise AssertionError("an in-flight copy reuses a live consumer slot")
                 ex.finish_gpu(comp, wait=True)
+                if nxt < len(batches):
+                    inflight.append([ex.load(key(e), admit=False) for e in batches[nxt]])
+                    nxt += 1
 
         # ---- retire this layer's speculation, prefetch the next layer's forecast
         self._retire_current(layer, wait=True)
@@ -354,12 +358,34 @@ class PDScopeCudaRuntime:
                    measured_performance=False)
         return out, routing, row
 
-    def _grouped(self, x, packed, sel_dev, T, k, slots_dev, ws):
-        bm = ops.grouped_block_m((T * k) // max(1, self.E))
+    def _demand_pipeline(self, phase):
+        """(experts per grouped launch, batches whose staging slots are held at once).
+
+        The reference stages one expert per compute call with demand_slots-1
+        copies in flight beside it for prefill and 1 for decode
+        (pdscope_runtime.py:361), i.e. it holds demand_slots or 2 slots.  The
+        slot budget here is the same, but from 6 slots on a prefill layer
+        splits it into two halves: one half computes as ONE grouped launch
+        while the other half's copies stream.  The per-expert host work
+        (ledger, table upload, launches) then shrinks by the batch size and
+        stays below the copy time of a 9 MiB expert, so the copy engine does
+        not wait for the control thread.
+        """
+        if phase != "prefill":
+            return 1, 2
+        if self.demand_slots >= 6:
+            return self.demand_slots // 2, 2
+        return 1, self.demand_slots
+
+    def _grouped(self, x, packed, sel_dev, rows, slots_dev, ws):
+        """One grouped SwiGLU launch over the experts in sel_dev, whose routed
+        row counts (known on the host since the demand reveal) are `rows`:
+        the row-tile height follows their mean, the grid their exact tile count."""
+        bm = ops.grouped_block_m(sum(rows) // len(rows))
         nsel = sel_dev.numel()
         tile_start = ws.tile_start[:nsel + 1]
         ops.schedule(packed.counts, sel_dev, bm, out=tile_start)
-        max_tiles = (T * k + bm - 1) // bm + nsel
+        max_tiles = sum((r + bm - 1) // bm for r in rows)
         ops.swiglu_grouped(x, packed.perm_token, packed.offsets, sel_dev, tile_start, max_tiles, bm, slots_dev, self.H,
                            self.I, ws.h_ws, ws.y)
 
