@@ -2,7 +2,7 @@
 """MoE-layer benchmark on one MI355X: Qwen3-30B-A3B-shaped layers, seeded random weights.
 
     python bench.py [--steps K] [--warmup W]
-                    [--workload prefill512|decode|prefill4096|prefill4096_zipf|dsv2_mixed]
+                    [--workload prefill512|decode|prefill4096|prefill4096_zipf|dsv2_mixed|stack48]
 
 A step is one MoE layer forward over one batch of synthetic tokens whose
 inputs and weights are already resident in HBM: route (K1) -> pack (K2) ->
@@ -48,7 +48,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="prefill512",
-                    choices=["prefill512", "decode", "prefill4096", "prefill4096_zipf", "dsv2_mixed"])
+                    choices=["prefill512", "decode", "prefill4096", "prefill4096_zipf", "dsv2_mixed", "stack48"])
     ap.add_argument("--no-extra", action="store_true", help="only the main workload")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, cpus) - 1")
@@ -271,16 +271,8 @@ def run_zipf_staged(steps, warmup, n_layers, device, seed0):
         max_rows = max(max(r["token_counts"].values()) for r in rows)
         # the copy engine alone: the same number of expert blocks, back to back, into the staging slots
         srcs = [masters[ExpertKey(0, e, "bf16")].flat for e in range(E) if e not in hottest]
-        dst = rt.executor.staging
-        s = torch.cuda.Stream(device)
         nc = len(srcs)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(s)
-        for j, src in enumerate(srcs):
-            ops.stage_expert(dst[j % len(dst)][:EXPERT_BYTES], src.view(torch.uint8), stream=s)
-        e1.record(s)
-        torch.cuda.synchronize(device)
-        copy_gbs = nc * EXPERT_BYTES / (e0.elapsed_time(e1) / 1e3) / 1e9
+        copy_gbs = copy_engine_gbs(rt, srcs, device)
     finally:
         rt.close()
     gemm = zipf_gemm(lay0, xs[0], bias, device)
@@ -333,6 +325,121 @@ def zipf_gemm(lay, x, bias, device, reps=20):
     return dict(gateup_ms=gu, down_ms=dn, block_m=bm, max_rows=max(counts), experts_touched=sum(c > 0 for c in counts),
                 mfma=dict(bound="mfma", achieved=achieved, peak=BF16_PEAK_TFLOPS, unit="TFLOP/s",
                           frac=achieved / BF16_PEAK_TFLOPS))
+
+
+def rms_residual(out, x, eps=1e-6):
+    """Next-layer activation of the stack: attention is the identity, so the
+    block is h = x + moe(x) followed by RMSNorm (weight 1) in fp32."""
+    import torch
+    h = out.float() + x.float()
+    return (h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + eps)).to(torch.bfloat16)
+
+
+def run_stack(n_layers, device, seed0, T_prefill=2048, n_decode=64, cap_gib=24, hot_per_layer=40, demand_slots=8):
+    """48 Qwen3-30B-A3B-shaped MoE blocks through the drop-in runtime: the
+    expert masters live in pinned host memory (48 x 128 x 9 MiB), HBM holds at
+    most cap_gib of expert slots (a static hot set chosen by calibration
+    routing, speculative prefetch slots and 8 demand staging slots), the
+    gate-fallback predictor (layer l+1 gate on the layer-l activation)
+    prefetches, and decode layers replay their captured single-launch graph
+    over the resident set.  Prefill 2048 tokens, then 64 decode steps."""
+    import torch
+    from pdscope_amd import synthetic
+    from pdscope_amd.cache import ExpertKey
+    from pdscope_amd.executor import masters_from_block
+    from pdscope_amd.pdscope_runtime import PDScopeCudaRuntime
+    t_setup = time.perf_counter()
+    gates, masters, hot = [], {}, []
+    calib = synthetic.make_tokens(512, H, seed=seed0 + 30001, device=device)
+    from pdscope_amd import layer as LY
+    cws = LY.MoEWorkspace(512, H, I, E, K_TOP, device, route_only=True)
+    for l in range(n_layers):
+        lay = synthetic.make_layer(H, I, E, K_TOP, True, seed=seed0 + 20000 + 1000 * l, device=device)
+        masters.update(masters_from_block(l, lay.experts, E, H, I))
+        gates.append(lay.gate)
+        # static hot profile: the experts a seeded calibration batch routes to most
+        _, ids, _ = LY.route(calib, lay.gate, cws)
+        cnt = torch.bincount(ids.reshape(-1).long(), minlength=E).cpu().tolist()
+        hot += [ExpertKey(l, e, "bf16") for e in sorted(range(E), key=lambda e: (-cnt[e], e))[:hot_per_layer]]
+        del lay
+    torch.cuda.empty_cache()
+    slot_budget = (cap_gib << 30) // EXPERT_BYTES
+    speculative = slot_budget - demand_slots - len(hot)
+    if speculative < 0:
+        raise ValueError("hot set and staging slots exceed the HBM cap")
+    rt = PDScopeCudaRuntime(masters, hot_keys=hot, speculative_slots=speculative, demand_slots=demand_slots,
+                            resident_graphs=True, device=device)
+    setup_s = time.perf_counter() - t_setup
+    try:
+        def pass_(x, step):
+            rows = []
+            for l in range(n_layers):
+                out, _, row = rt.forward(x, gates[l], layer=l, step=step, request="stack",
+                                         next_gate=gates[l + 1] if l + 1 < n_layers else None, top_k=K_TOP)
+                rows.append(row)
+                x = rms_residual(out, x)
+            return x, rows
+
+        def phase_stats(rows, wall, tokens, before, after):
+            # whole-phase ledger totals: a copy that lands between two layer
+            # calls is completed by the next call's poll, outside any row
+            h2d = after.get("h2d_bytes_submitted", 0) - before.get("h2d_bytes_submitted", 0)
+            demand = sum(len(r["decision"]["on_demand_queue"]) for r in rows)
+            routed = sum(len(r["token_counts"]) for r in rows)
+            return dict(tok_s=tokens / wall, wall_s=wall, h2d_bytes=h2d, h2d_gbs=h2d / wall / 1e9,
+                        routed_experts=routed, demand_misses=demand, resident_hit_rate=1 - demand / max(1, routed),
+                        prefetch_issued=sum(len(r["prefetch_issued"]) for r in rows),
+                        **{kk: after.get(kk, 0) - before.get(kk, 0) for kk in
+                           ("demand_loads_submitted", "prefetch_loads_submitted", "unused_prefetch_evictions",
+                            "fresh_prefetch_hits", "loading_misses", "absent_misses")},
+                        paths=sorted({r.get("decode_path", "grouped") for r in rows}))
+
+        x = synthetic.make_tokens(T_prefill, H, seed=seed0 + 30002, device=device)
+        torch.cuda.synchronize(device)
+        st0 = rt.cache.stats()
+        t0 = time.perf_counter()
+        x, rows_p = pass_(x, 0)
+        torch.cuda.synchronize(device)
+        st1 = rt.cache.stats()
+        prefill = phase_stats(rows_p, time.perf_counter() - t0, T_prefill, st0, st1)
+        rows_d = []
+        t0 = time.perf_counter()
+        for step in range(1, n_decode + 1):
+            tok = synthetic.make_tokens(1, H, seed=seed0 + 30100 + step, device=device)
+            _, rows = pass_(tok, step)
+            rows_d += rows
+        torch.cuda.synchronize(device)
+        decode = phase_stats(rows_d, time.perf_counter() - t0, n_decode, st1, rt.cache.stats())
+        pred = {p: dict(v) for p, v in rt.prediction_counts.items()}
+        copy_gbs = copy_engine_gbs(rt, [masters[ExpertKey(0, e, "bf16")].flat for e in range(E)], device)
+        mem = dict(cache_slots=len(hot) + speculative, hot_slots=len(hot), speculative_slots=speculative,
+                   demand_slots=demand_slots, hbm_expert_bytes=(len(hot) + speculative + demand_slots) * EXPERT_BYTES,
+                   pinned_master_bytes=len(masters) * EXPERT_BYTES)
+    finally:
+        rt.close()
+    pcie = dict(bound="pcie_h2d", achieved=prefill["h2d_gbs"], peak=copy_gbs, unit="GB/s",
+                peak_kind="measured back-to-back expert copies on this host", phase="prefill")
+    pcie["frac"] = pcie["achieved"] / pcie["peak"]
+    return dict(tok_s=decode["tok_s"], ms_per_step=1e3 / decode["tok_s"], kernel="48-layer stack through the runtime",
+                kernel_ms_mean=1e3 * decode["wall_s"] / n_decode, prefill=prefill, decode=decode, predictor=pred,
+                memory=mem, layers=n_layers, setup_s=setup_s, tokens_prefill=T_prefill, decode_steps=n_decode,
+                pcie=pcie, steps_run=n_decode)
+
+
+def copy_engine_gbs(rt, srcs, device):
+    """Back-to-back expert copies from pinned host memory into the runtime's
+    staging slots on a side stream: the H2D rate the staging path can reach."""
+    import torch
+    from pdscope_amd import ops
+    dst = rt.executor.staging
+    s = torch.cuda.Stream(device)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for j, src in enumerate(srcs):
+        ops.stage_expert(dst[j % len(dst)][:EXPERT_BYTES], src.view(torch.uint8), stream=s)
+    e1.record(s)
+    torch.cuda.synchronize(device)
+    return len(srcs) * EXPERT_BYTES / (e0.elapsed_time(e1) / 1e3) / 1e9
 
 
 def run_dsv2_mixed(steps, warmup, n_layers, device, seed0):
@@ -531,8 +638,9 @@ def main():
     threads = cpu_threads(args.cpu_threads)
 
     plan = {"prefill512": ("prefill", 512, 4), "decode": ("decode", 1, 16), "prefill4096": ("prefill", 4096, 2),
-            "prefill4096_zipf": ("zipf", 4096, 2), "dsv2_mixed": ("dsv2", 1304, 4)}
-    order = [args.workload] + ([] if args.no_extra else [w for w in plan if w != args.workload])
+            "prefill4096_zipf": ("zipf", 4096, 2), "dsv2_mixed": ("dsv2", 1304, 4), "stack48": ("stack", 2048, 48)}
+    # the 48-layer stack pins 58 GB of host masters: it runs only when asked for
+    order = [args.workload] + ([] if args.no_extra else [w for w in plan if w not in (args.workload, "stack48")])
     records, raw = {}, {}
     for wl in order:
         kind, T, nl = plan[wl]
@@ -552,6 +660,9 @@ def main():
             rec = dict(res)
         elif kind == "zipf":
             res = run_zipf_staged(steps, warmup, nl, device, 20261011)
+            rec = dict(res)
+        elif kind == "stack":
+            res = run_stack(nl, device, 20261011)
             rec = dict(res)
         else:
             res = run_decode(steps, warmup, nl, device, 20261011)
@@ -574,7 +685,7 @@ def main():
     main = records[args.workload]
     if args.workload == "prefill4096":
         roof = dict(main["mfma"])
-    elif args.workload == "prefill4096_zipf":
+    elif args.workload in ("prefill4096_zipf", "stack48"):
         roof = dict(main["pcie"])
     else:
         roof = dict(main["hbm"])
@@ -586,7 +697,10 @@ def main():
                 "decode": "Qwen3-30B-A3B-shaped MoE layer, decode T=1, 128 experts resident (hipGraph per layer)",
                 "prefill4096": "Qwen3-30B-A3B-shaped MoE layer, prefill T=4096 uniform routing, 128 experts resident",
                 "prefill4096_zipf": "Qwen3-30B-A3B-shaped MoE layer, prefill T=4096 with a Zipf(1.1) router bias, "
-                                    "32 experts resident, the rest staged through 8 demand slots"}
+                                    "32 experts resident, the rest staged through 8 demand slots",
+                "stack48": "48 Qwen3-30B-A3B-shaped MoE blocks (identity attention + RMSNorm), prefill 2048 then 64 "
+                           "decode steps, 24 GiB expert-slot cap, gate-fallback prefetch, decode graph replay; "
+                           "value is decode tok/s"}
     kind, T, nl = plan[args.workload]
     line = {
         "metric": METRIC,

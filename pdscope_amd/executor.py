@@ -46,18 +46,29 @@ class ExpertWeights:
         return sum(t.numel() * t.element_size() for t in self.tensors.values())
 
 
-def masters_from_block(layer, block, E, H, I, *, pin=True):
+def masters_from_block(layer, block, E, H, I, *, pin=True, chunk_bytes=1 << 28):
     """ExpertWeights for one layer whose experts are rows of a [E, 3*I*H] bf16 tensor.
 
     The host copy is page-locked (pinned) so staging is one DMA per expert.
+    It is allocated in chunks of whole experts of at most chunk_bytes: the
+    pinned-memory allocator rounds every allocation up to a power of two, so
+    one [E, 3*I*H] buffer of 1.18 GB would hold 2 GiB of locked pages.
     """
-    host = block.detach().to("cpu")
-    if pin:
-        host = host.pin_memory()
+    block = block.detach()
+    per = max(1, chunk_bytes // (block.shape[1] * block.element_size())) if pin else E
+    rows = []
+    for e0 in range(0, E, per):
+        n = min(per, E - e0)
+        if pin:
+            host = torch.empty((n, block.shape[1]), dtype=block.dtype, pin_memory=True)
+            host.copy_(block[e0:e0 + n])
+        else:
+            host = block[e0:e0 + n].to("cpu")
+        rows += [host[j] for j in range(n)]
     IH = I * H
     out = {}
     for e in range(E):
-        row = host[e]
+        row = rows[e]
         tensors = {"gate_proj": row[:IH].view(I, H), "up_proj": row[IH:2 * IH].view(I, H),
                    "down_proj": row[2 * IH:].view(H, I)}
         key = ExpertKey(layer, e, "bf16")

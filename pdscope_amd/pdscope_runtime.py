@@ -85,6 +85,9 @@ class PDScopeCudaRuntime:
             raise ValueError("invalid decode CPU balance target")
         self.size = next(iter(sizes.values()))
         self.hot = set(hot_keys)
+        self._hot_by_layer = {}
+        for hk in hot_keys:
+            self._hot_by_layer.setdefault(hk.layer, []).append(hk)
         self.layers = {k.layer for k in masters}
         any_w = next(iter(masters.values()))
         self.I, self.H = any_w.tensors["gate_proj"].shape
@@ -184,12 +187,20 @@ class PDScopeCudaRuntime:
         nkey = lambda e: self._key(layer + 1, e)  # noqa: E731
         self.poll()
         before = self.cache.stats()
-        graph_path = (self.resident_graphs and phase == "decode" and next_gate is None and bias is None
-                      and self._layer_fully_resident(layer))
+        # decode replays the captured single-launch layer over the slot table
+        # (experts without a device copy have a null entry and contribute 0);
+        # misses, at most k <= demand_slots of them, are staged in one batch
+        # and the same graph is replayed once more over the completed table
+        # (with fewer slots than k only a fully resident layer replays)
+        graph_path = (self.resident_graphs and phase == "decode" and bias is None
+                      and ops.decode_layer_supported(H, self.I, E, k, self.device)
+                      and (k <= self.demand_slots or self._layer_fully_resident(layer)))
 
         # ---- 1-2: route (+ predictor), grouping, one D2H of the demand
         out = torch.empty((T, H), dtype=torch.bfloat16, device=self.device)
         if graph_path:
+            # entries the first replay saw (a copy still in flight reads as null)
+            replay_table = list(self.executor.table(layer, E)[1])
             logits, ids, weights = self._replay_decode_graph(layer, x, gate, normalize, k, out)
         else:
             logits, ids, weights = L.route(x, gate, ws, normalize=normalize, bias=bias)
@@ -244,7 +255,7 @@ class PDScopeCudaRuntime:
         # first demand copies go out before the resident launch is prepared
         batches, inflight, nxt = [], [], 0
         if demand:
-            group, held = self._demand_pipeline(phase)
+            group, held = (len(demand), 1) if graph_path else self._demand_pipeline(phase)
             batches = [demand[i:i + group] for i in range(0, len(demand), group)]
             while nxt < min(held, len(batches)):
                 inflight.append([ex.load(key(e), admit=False) for e in batches[nxt]])
@@ -257,11 +268,18 @@ class PDScopeCudaRuntime:
             if missing:
                 raise AssertionError(f"experts {missing} of layer {layer} have no ready device copy")
         decode_fast = (T == 1 and not demand and not graph_path)
-        if T == 1 and demand:
+        if T == 1 and demand and not graph_path:
             ops.pack(ids, E, out=packed, workspace=ws.pack_ws)  # decode misses take the grouped path
         if graph_path:
-            # the replay already produced `out`; account the uses it made
-            tasks.append(ex.gpu_group([key(e) for e in resident], lambda: None, wait_for=cur))
+            if not demand:  # with misses the demand batch below replays over the completed table
+                if any(replay_table[e] == 0 for e in counts):
+                    # a routed copy landed after the first replay: replay over the completed table
+                    def launch():
+                        self._replay_decode_graph(layer, x, gate, normalize, k, out)
+                else:
+                    def launch():  # the replay already produced `out`; account the uses it made
+                        pass
+                tasks.append(ex.gpu_group([key(e) for e in resident], launch, input_ref=x, wait_for=cur))
         elif resident:
             ex.table(layer, E)
             require_copies(resident if not decode_fast else sorted(counts))
@@ -285,12 +303,17 @@ class PDScopeCudaRuntime:
                     ex.finish_load(ticket, wait=True)
                 ex.table(layer, E)
                 require_copies(batch)
-                tab = ex.upload_table(layer, E, ex.compute_stream)
-                sel_dev = ex.upload_ints(batch, ex.compute_stream)
+                if graph_path:
+                    def launch():
+                        self._replay_decode_graph(layer, x, gate, normalize, k, out)
+                    comp = ex.gpu_group([key(e) for e in resident + batch], launch, input_ref=x, wait_for=cur)
+                else:
+                    tab = ex.upload_table(layer, E, ex.compute_stream)
+                    sel_dev = ex.upload_ints(batch, ex.compute_stream)
 
-                def launch(sel_dev=sel_dev, tab=tab, rows=[counts[e] for e in batch]):
-                    self._grouped(x, packed, sel_dev, rows, tab, ws)
-                comp = ex.gpu_group([key(e) for e in batch], launch, input_ref=x, wait_for=cur)
+                    def launch(sel_dev=sel_dev, tab=tab, rows=[counts[e] for e in batch]):
+                        self._grouped(x, packed, sel_dev, rows, tab, ws)
+                    comp = ex.gpu_group([key(e) for e in batch], launch, input_ref=x, wait_for=cur)
                 ping_pong += [dict(expert=e, slot=t.slot, generation=t.generation) for e, t in zip(batch, tickets)]
                 live = [t.slot for b in inflight for t in b]
                 if len(set(live)) != len(live) or set(live) & {t.slot for t in tickets}:
@@ -337,7 +360,9 @@ class PDScopeCudaRuntime:
         self.cache.end_demand(identity)
         self._retire_current(layer, wait=True)
         self.poll()
-        if self.diagnostics and any(self.cache.lookup(h) is None for h in self.hot):
+        # the ledger never chooses a static copy as a victim; checking the
+        # layer just served keeps the guard without a scan of every layer
+        if self.diagnostics and any(self.cache.lookup(h) is None for h in self._hot_by_layer.get(layer, ())):
             raise AssertionError("speculation evicted a charged static hot copy")
         after = self.cache.stats()
         delta = {kk: v - before.get(kk, 0) for kk, v in after.items()}
@@ -396,8 +421,6 @@ class PDScopeCudaRuntime:
         g = self._graphs.get(gkey)
         ex = self.executor
         ex.table(layer, self.E)
-        if any(ex.table_entry(layer, e) == 0 for e in range(self.E)):
-            raise AssertionError("decode graph replay needs every expert of the layer resident")
         # the table tensor is captured by address; refresh its contents (copies
         # may have moved between calls) on the replay stream
         slots_dev = ex.upload_table(layer, self.E, torch.cuda.current_stream(self.device))

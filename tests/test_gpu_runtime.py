@@ -118,6 +118,45 @@ def test_runtime_decode_graph_matches_eager(orc):
         rt.close()
 
 
+def test_runtime_partial_resident_decode_graph(orc):
+    """Decode graph over a partly resident layer: experts without a copy read as
+    null on the first replay; misses are staged in one batch and the graph is
+    replayed over the completed table.  The output equals the single-launch
+    layer over a fully resident table bit for bit; the predictor prefetches
+    the next layer's experts on the way."""
+    from pdscope_amd import layer, ops, synthetic
+    from pdscope_amd.cache import ExpertKey
+    from pdscope_amd.pdscope_runtime import PDScopeCudaRuntime
+    q = synthetic.QWEN
+    layers, masters = build(2, q["H"], q["I"], q["E"], q["k"], seed=95)
+    hot = [ExpertKey(l, e, "bf16") for l in range(2) for e in range(32)]
+    rt = PDScopeCudaRuntime(masters, hot_keys=hot, speculative_slots=8, demand_slots=8, resident_graphs=True)
+    full = [ops.slot_table([layers[l].experts[e] for e in range(q["E"])], DEV) for l in range(2)]
+    ws = layer.MoEWorkspace(1, q["H"], q["I"], q["E"], 8, DEV)
+    misses = 0
+    try:
+        x0 = synthetic.make_tokens(4, q["H"], seed=96)
+        for l in range(2):
+            rt.forward(x0, layers[l].gate, layer=l, step=0, next_gate=layers[1].gate if l == 0 else None)
+        for step in range(1, 6):
+            x = synthetic.make_tokens(1, q["H"], seed=96 + step)
+            for l in range(2):
+                out, routing, row = rt.forward(x, layers[l].gate, layer=l, step=step,
+                                               next_gate=layers[1].gate if l == 0 else None)
+                assert row["decode_path"] == "graph"
+                misses += len(row["decision"]["on_demand_queue"])
+                ref_out, _, ids, _ = layer.moe_forward(x, layers[l].gate, full[l], ws)
+                torch.cuda.synchronize()
+                assert torch.equal(routing.selected, ids.long())
+                assert torch.equal(out, ref_out)
+                check_output(orc, out, routing, x, layers[l], q["H"], q["I"], 8)
+        assert misses > 0
+        closure(rt)
+        assert rt.cache.stats().get("prefetch_loads_submitted", 0) > 0
+    finally:
+        rt.close()
+
+
 def test_runtime_rejects_bad_phase_shapes():
     from pdscope_amd.cache import ExpertKey
     from pdscope_amd.pdscope_runtime import PDScopeCudaRuntime
