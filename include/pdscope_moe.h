@@ -92,8 +92,9 @@ int pdscope_pack(const int32_t *ids, int T, int k, int E, int32_t *counts, int32
 int pdscope_schedule(const int32_t *counts, const int32_t *sel, int nsel, int block_m,
                      int32_t *tile_start, void *stream);
 
-/* Row tile (32, 64 or 128) pdscope_swiglu_grouped uses for `rows_hint`
- * average rows per selected expert. */
+/* Row tile (32, 64, 128 or 256) for `rows_hint` average rows per selected
+ * expert: the smallest listed tile that covers a typical expert in one
+ * m-tile (<= 16, 64, 160 rows; 256 above). */
 int pdscope_grouped_block_m(int rows_hint);
 
 /*
@@ -107,7 +108,9 @@ int pdscope_grouped_block_m(int rows_hint);
  *   y[r] = bf16(h[r] . down_e^T)                      (y [T*k, H] bf16)
  * bf16 MFMA with fp32 accumulation.  max_tiles bounds sum ceil(m_e/block_m)
  * (e.g. ceil(rows/block_m) + nsel); tiles beyond tile_start[nsel] exit.
- * Limits: H % 64 == 0, I % 64 == 0.
+ * block_m: 32, 64, 128 or 256, the row tile pdscope_schedule used.
+ * Limits: H % 64 == 0, I % 64 == 0; with block_m 32 or 256 (256-column
+ * tiles) also H % 256 == 0 and I % 128 == 0, with 64 or 128 H % 128 == 0.
  */
 int pdscope_swiglu_grouped(const void *x, const int32_t *perm_token, const int32_t *offsets,
                            const int32_t *sel, int nsel, const int32_t *tile_start,
