@@ -6,7 +6,7 @@
 
 A step is one MoE layer forward over one batch of synthetic tokens whose
 inputs and weights are already resident in HBM: route (K1) -> pack (K2) ->
-tile schedule -> grouped SwiGLU gate/up + down (K3) -> merge (K5) for
+balanced tile schedule -> grouped SwiGLU gate/up + down (K3) -> merge (K5) for
 prefill, route (K1) -> decode GEMV gate/up + down/merge (K4) for T = 1
 (decode steps replay one hipGraph per layer).  Steps rotate over several
 independently seeded layer copies so the 256 MB Infinity Cache cannot hold
@@ -115,15 +115,15 @@ def run_prefill(T, steps, warmup, n_layers, device, seed0):
         logits, ids, w = layer.route(x, lay.gate, ws)
         ops.pack(ids, E, out=packed, workspace=ws.pack_ws)
         bm = ops.grouped_block_m(n // E)
-        ops.schedule(packed.counts, ws.sel_all, bm, out=ws.tile_start)
+        ops.schedule(packed.counts, ws.sel_all, bm, out=ws.tile_start, order=ws.sel_order)
         max_tiles = (n + bm - 1) // bm + E
         if ev is not None:
             ev[0].record(stream)
-        ops.swiglu_grouped_gateup(x, packed.perm_token, packed.offsets, ws.sel_all, ws.tile_start, max_tiles, bm,
+        ops.swiglu_grouped_gateup(x, packed.perm_token, packed.offsets, ws.sel_order, ws.tile_start, max_tiles, bm,
                                   slots, H, I, ws.h_ws)
         if ev is not None:
             ev[1].record(stream)
-        ops.swiglu_grouped_down(ws.h_ws, packed.offsets, ws.sel_all, ws.tile_start, max_tiles, bm, slots, H, I,
+        ops.swiglu_grouped_down(ws.h_ws, packed.offsets, ws.sel_order, ws.tile_start, max_tiles, bm, slots, H, I,
                                 ws.y)
         ops.merge(ws.y, packed.row_of, w, ws.out[:T])
 
@@ -304,16 +304,16 @@ def zipf_gemm(lay, x, bias, device, reps=20):
     _, _, _, packed = ws.views(T)
     ops.pack(ids, E, out=packed, workspace=ws.pack_ws)
     bm = ops.grouped_block_m((T * K_TOP) // E)
-    ops.schedule(packed.counts, ws.sel_all, bm, out=ws.tile_start)
+    ops.schedule(packed.counts, ws.sel_all, bm, out=ws.tile_start, order=ws.sel_order)
     max_tiles = (T * K_TOP + bm - 1) // bm + E
     stream = torch.cuda.current_stream(device)
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(reps + 2)]
     for r in range(reps + 2):
         ev[r][0].record(stream)
-        ops.swiglu_grouped_gateup(x, packed.perm_token, packed.offsets, ws.sel_all, ws.tile_start, max_tiles, bm,
+        ops.swiglu_grouped_gateup(x, packed.perm_token, packed.offsets, ws.sel_order, ws.tile_start, max_tiles, bm,
                                   slots, H, I, ws.h_ws)
         ev[r][1].record(stream)
-        ops.swiglu_grouped_down(ws.h_ws, packed.offsets, ws.sel_all, ws.tile_start, max_tiles, bm, slots, H, I,
+        ops.swiglu_grouped_down(ws.h_ws, packed.offsets, ws.sel_order, ws.tile_start, max_tiles, bm, slots, H, I,
                                 ws.y)
         ev[r][2].record(stream)
     torch.cuda.synchronize(device)

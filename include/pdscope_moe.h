@@ -92,6 +92,20 @@ int pdscope_pack(const int32_t *ids, int T, int k, int E, int32_t *counts, int32
 int pdscope_schedule(const int32_t *counts, const int32_t *sel, int nsel, int block_m,
                      int32_t *tile_start, void *stream);
 
+/*
+ * Balanced tile schedule: the grouped kernels cut the tile list (in sel
+ * order) into 8 contiguous equal-count pieces, one per XCD.  This orders the
+ * experts so those pieces hold similar work and start with their largest
+ * experts: rank the selected experts by rows (descending, ties by position),
+ * deal rank r to group (r/8 even ? r%8 : 7-r%8), concatenate the groups.
+ * order[nsel] receives the experts in that order and tile_start[nsel+1] the
+ * m-tile prefix over order; pass `order` as sel to pdscope_swiglu_grouped*.
+ * No counterpart in the reference (its experts run one launch each).
+ * Limits: nsel <= 256.
+ */
+int pdscope_schedule_balanced(const int32_t *counts, const int32_t *sel, int nsel, int block_m,
+                              int32_t *order, int32_t *tile_start, void *stream);
+
 /* Row tile (32, 64, 128 or 256) for `rows_hint` average rows per selected
  * expert: the smallest listed tile that covers a typical expert in one
  * m-tile (<= 16, 64, 160 rows; 256 above). */

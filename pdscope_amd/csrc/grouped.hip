@@ -10,10 +10,10 @@
 //             epilogue pairs accumulators of the same lane;
 //   down    : y[r,n] = bf16(h_r . down_n)
 // Both operands are K-contiguous ([rows, K] activations, [out, in] weights),
-// so every 16-byte chunk feeds one MFMA lane directly.  Tiles stream into a
-// 3- or 4-stage LDS ring by direct-to-LDS loads (global_load_lds_dwordx4)
-// with a 16-byte-chunk XOR swizzle applied on the source side (chunk c of
-// row r lives at c ^ (r & 7)), so fragment reads are bank-conflict free.
+// so every 16-byte chunk feeds one MFMA lane directly.  Tiles stream into
+// multi-stage LDS rings by direct-to-LDS loads (global_load_lds_dwordx4)
+// with a 16-byte-chunk XOR swizzle applied on the source side (see Geo),
+// so fragment reads are bank-conflict free.
 // MFMA: v_mfma_f32_32x32x16_bf16, fp32 accumulation.
 #include <type_traits>
 
@@ -69,30 +69,36 @@ __device__ __forceinline__ void ring_barrier() {
 }
 
 // Wait until the stage to be consumed has landed, `younger` (0 .. S-2)
-// later stages being allowed to stay in flight.
-template <int S, int LPW>
+// later stages of LPW loads each being allowed to stay in flight.
+template <int S, int LPW, int Y = S - 2>
 __device__ __forceinline__ void wait_stage(int younger) {
-    if constexpr (S >= 5) {
-        if (younger >= 3) { wait_vm<3 * LPW>(); return; }
+    if constexpr (Y <= 0) {
+        wait_vm<0>();
+    } else {
+        if (younger >= Y) {
+            wait_vm<Y * LPW>();
+            return;
+        }
+        wait_stage<S, LPW, Y - 1>(younger);
     }
-    if constexpr (S >= 4) {
-        if (younger >= 2) { wait_vm<2 * LPW>(); return; }
-    }
-    if constexpr (S >= 3) {
-        if (younger >= 1) { wait_vm<LPW>(); return; }
-    }
-    wait_vm<0>();
 }
 
 // Tile BM x BN x BK, WM x WN waves (4 or 8: with 8, two waves share each
 // SIMD so one wave's MFMAs cover the other's LDS reads, waits and
-// epilogue), S-stage LDS ring filled by direct-to-LDS loads (the stage
-// S-1 ahead is in flight while one stage is consumed).  Tiles are numbered (m-tile, n-tile) with n fastest and the
+// epilogue).  The A tile (activation rows) and the B tile (weight rows)
+// stream into two LDS rings of SA and SB stages by direct-to-LDS loads.
+// With SA == SB every wave loads its share of both.  With SA != SB
+// (8 waves) the first half of the waves loads only A and the second half
+// only B: a wave's load counter completes in issue order, so a wave that
+// loads both operands cannot keep the slow weight stream (HBM) further
+// ahead than the fast activation gathers (L2 / Infinity Cache); split
+// roles let the B ring run SB-1 stages ahead on its own.  Every wave
+// computes.  Tiles are numbered (m-tile, n-tile) with n fastest and the
 // tile range is cut into 8 contiguous pieces, one per XCD (block b runs on
 // XCD b % 8): all n-tiles of an m-tile share the gathered activation rows
 // in one L2, and the m-tiles of one expert read the same weight tiles at
 // the same time from one L2.
-template <int BM, int BN, int BK, int WM, int WN, int S, bool GATEUP>
+template <int BM, int BN, int BK, int WM, int WN, int SA, int SB, bool GATEUP>
 __global__ __launch_bounds__(64 * WM * WN, 1) void grouped_kernel(
     const uint16_t *__restrict__ a_src, const int32_t *__restrict__ perm_token,
     const int32_t *__restrict__ offsets, const int32_t *__restrict__ sel, int nsel,
@@ -100,15 +106,20 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void grouped_kernel(
     uint16_t *__restrict__ out) {
     constexpr int NW = WM * WN;
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+    constexpr bool SPLIT = SA != SB;
+    static_assert(!SPLIT || NW == 8, "split load roles need 8 waves");
     constexpr int TM = BM / WM, TN = BN / WN;  // wave tile
     constexpr int MB = TM / 32, NB = TN / 32;  // 32x32 MFMA blocks per wave
     static_assert(MB >= 1 && NB >= 1 && (!GATEUP || NB % 2 == 0), "wave tiling");
     typedef Geo<BK> G;
-    constexpr int AL = BM / G::RPI / NW, BL = BN / G::RPI / NW;  // 1 KB load instructions per wave per stage
-    static_assert(AL >= 1 && BL >= 1 && AL * G::RPI * NW == BM && BL * G::RPI * NW == BN, "tile / load shape");
-    constexpr int LPW = AL + BL;
-    constexpr int STAGE = (BM + BN) * G::RB;
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[S * STAGE];
+    constexpr int NWA = SPLIT ? NW / 2 : NW, NWB = SPLIT ? NW / 2 : NW;  // waves loading A / B
+    constexpr int AL = BM / G::RPI / NWA, BL = BN / G::RPI / NWB;  // 1 KB loads per loading wave per stage
+    static_assert(AL >= 1 && BL >= 1 && AL * G::RPI * NWA == BM && BL * G::RPI * NWB == BN, "tile / load shape");
+    constexpr int LW = SPLIT ? (AL > BL ? AL : BL) : AL + BL;  // load pointers per wave
+    constexpr int ASTAGE = BM * G::RB, BSTAGE = BN * G::RB;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[SA * ASTAGE + SB * BSTAGE];
+    uint8_t *const ring_a = smem;
+    uint8_t *const ring_b = smem + SA * ASTAGE;
 
     // ---- tile -> (m-tile, n-tile)
     const int NT = GATEUP ? I / (BN / 2) : H / BN;
@@ -134,38 +145,54 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void grouped_kernel(
     if (base == nullptr) return;  // no ready copy of this expert: never dereference
     const size_t IH = (size_t)I * H;
 
-    // ---- per-lane source rows: load instruction q of this wave covers tile
-    // rows RPI(wave + NW q) .. +RPI-1; lane l takes row +l/CPR and the
-    // logical chunk that belongs in slot l % CPR of that row (the swizzle)
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // ---- per-lane source rows: load q of A-wave wa covers A rows
+    // RPI(wa + NWA q) .. +RPI-1 (B likewise with wb, NWB); lane l takes row
+    // +l/CPR and the logical chunk that belongs in slot l % CPR of that row
+    // (the swizzle).  Unified roles: lp[0, AL) are A loads, lp[AL, AL+BL) B.
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool a_role = !SPLIT || wave < NWA;
+    const int wa = wave, wb = SPLIT ? wave - NWA : wave;
     const int rl = lane / G::CPR, slot = lane % G::CPR;
-    const uint16_t *ap[AL];
-    const uint16_t *bp[BL];
-#pragma unroll
-    for (int q = 0; q < AL; ++q) {
-        const int row = (wave + NW * q) * G::RPI + rl;
+    const uint16_t *lp[LW];
+    auto a_ptr = [&](int q) {
+        const int row = (wa + NWA * q) * G::RPI + rl;
         const int cs = slot ^ G::key(row);
         const int gr = min(m0 + row, row_end - 1);
-        ap[q] = GATEUP ? a_src + (size_t)perm_token[gr] * H + cs * 8 : a_src + (size_t)gr * I + cs * 8;
-    }
-#pragma unroll
-    for (int q = 0; q < BL; ++q) {
-        const int rb = (wave + NW * q) * G::RPI + rl;
+        return GATEUP ? a_src + (size_t)perm_token[gr] * H + cs * 8 : a_src + (size_t)gr * I + cs * 8;
+    };
+    auto b_ptr = [&](int q) {
+        const int rb = (wb + NWB * q) * G::RPI + rl;
         const int cs = slot ^ G::key(rb);
         if (GATEUP) {
             const int i = n0 + (rb < BN / 2 ? rb : rb - BN / 2);
-            bp[q] = base + (rb < BN / 2 ? 0 : IH) + (size_t)i * H + cs * 8;
-        } else {
-            bp[q] = base + 2 * IH + (size_t)(n0 + rb) * I + cs * 8;
+            return base + (rb < BN / 2 ? 0 : IH) + (size_t)i * H + cs * 8;
         }
+        return base + 2 * IH + (size_t)(n0 + rb) * I + cs * 8;
+    };
+    if constexpr (SPLIT) {
+        if (a_role) {
+#pragma unroll
+            for (int q = 0; q < AL; ++q) lp[q] = a_ptr(q);
+        } else {
+#pragma unroll
+            for (int q = 0; q < BL; ++q) lp[q] = b_ptr(q);
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < AL; ++q) lp[q] = a_ptr(q);
+#pragma unroll
+        for (int q = 0; q < BL; ++q) lp[AL + q] = b_ptr(q);
     }
-    auto issue = [&](int kt) {
-        uint8_t *st = smem + (kt % S) * STAGE;
-        const int k0 = kt * BK;
+    auto issue_a = [&](int kt, int q0) __attribute__((always_inline)) {  // A stage kt from lp[q0 ..]
+        uint8_t *st = ring_a + (kt % SA) * ASTAGE;
 #pragma unroll
-        for (int q = 0; q < AL; ++q) load_lds16(ap[q] + k0, st + (wave + NW * q) * 1024);
+        for (int q = 0; q < AL; ++q) load_lds16(lp[q0 + q] + kt * BK, st + (wa + NWA * q) * 1024);
+    };
+    auto issue_b = [&](int kt, int q0) __attribute__((always_inline)) {
+        uint8_t *st = ring_b + (kt % SB) * BSTAGE;
 #pragma unroll
-        for (int q = 0; q < BL; ++q) load_lds16(bp[q] + k0, st + BM * G::RB + (wave + NW * q) * 1024);
+        for (int q = 0; q < BL; ++q) load_lds16(lp[q0 + q] + kt * BK, st + (wb + NWB * q) * 1024);
     };
 
     const int wm = wave / WN, wn = wave % WN;
@@ -188,31 +215,31 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void grouped_kernel(
     // every version stays straight-line code.
     const int mb_live = __builtin_amdgcn_readfirstlane(min(MB, max(0, (row_end - m0 - wm * TM + 31) / 32)));
     const int KT = K / BK;
-    // Software-pipelined K loop.  Slot kt % S holds stage kt; stages kt+1 ..
-    // kt+S-1 are in flight while stage kt is consumed.  Each iteration waits
-    // for stage kt+1, synchronises the block (every wave has then also
-    // finished reading stage kt, whose fragments are in registers), refills
-    // slot kt % S with stage kt+S, reads stage kt+1's fragments from LDS and
-    // then runs stage kt's MFMAs, so the LDS reads overlap the MFMAs.
-    auto kloop = [&](auto live) {
+    // Software-pipelined K loop.  Slot kt % SA of the A ring and kt % SB of
+    // the B ring hold stage kt; the stages up to kt+SA-1 / kt+SB-1 are in
+    // flight while stage kt is consumed, and the LDS reads of stage kt+1
+    // overlap stage kt's MFMAs.
+    // ROLE 0: this wave loads both operands (SA == SB); 1: A only; 2: B only
+    auto kloop = [&](auto live, auto role_c) __attribute__((always_inline)) {
         constexpr int L = decltype(live)::value;
+        constexpr int ROLE = decltype(role_c)::value;
         constexpr int KK = BK / 16;
         bf16x8_t af[2][KK][MB], bfr[2][KK][NB];
-        auto read_frags = [&](int kt, int buf) {
-            const uint8_t *st = smem + (kt % S) * STAGE;
+        auto read_frags = [&](int kt, int buf) __attribute__((always_inline)) {
+            const uint8_t *sa = ring_a + (kt % SA) * ASTAGE;
+            const uint8_t *sb = ring_b + (kt % SB) * BSTAGE;
 #pragma unroll
             for (int kk = 0; kk < KK; ++kk) {
                 const int c = kk * 2 + lhalf;
 #pragma unroll
                 for (int i = 0; i < L; ++i)
-                    af[buf][kk][i] = *reinterpret_cast<const bf16x8_t *>(st + G::off(wm * TM + i * 32 + lrow, c));
+                    af[buf][kk][i] = *reinterpret_cast<const bf16x8_t *>(sa + G::off(wm * TM + i * 32 + lrow, c));
 #pragma unroll
                 for (int j = 0; j < NB; ++j)
-                    bfr[buf][kk][j] =
-                        *reinterpret_cast<const bf16x8_t *>(st + BM * G::RB + G::off(brow(j) + lrow, c));
+                    bfr[buf][kk][j] = *reinterpret_cast<const bf16x8_t *>(sb + G::off(brow(j) + lrow, c));
             }
         };
-        auto mfmas = [&](int buf) {
+        auto mfmas = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
             for (int kk = 0; kk < KK; ++kk)
 #pragma unroll
@@ -222,40 +249,103 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void grouped_kernel(
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[buf][kk][i], bfr[buf][kk][j],
                                                                             acc[i][j], 0, 0, 0);
         };
+        // prologue: every ring filled, stage 0 landed
+        if constexpr (ROLE == 1) {
 #pragma unroll
-        for (int s0 = 0; s0 < S; ++s0)
-            if (s0 < KT) issue(s0);
-        wait_stage<S + 1, LPW>(min(S - 1, KT - 1));
+            for (int s0 = 0; s0 < SA; ++s0)
+                if (s0 < KT) issue_a(s0, 0);
+            wait_stage<SA + 1, AL>(min(SA - 1, KT - 1));
+        } else if constexpr (ROLE == 2) {
+#pragma unroll
+            for (int s0 = 0; s0 < SB; ++s0)
+                if (s0 < KT) issue_b(s0, 0);
+            wait_stage<SB + 1, BL>(min(SB - 1, KT - 1));
+        } else {
+#pragma unroll
+            for (int s0 = 0; s0 < SA; ++s0)
+                if (s0 < KT) {
+                    issue_a(s0, 0);
+                    issue_b(s0, AL);
+                }
+            wait_stage<SA + 1, AL + BL>(min(SA - 1, KT - 1));
+        }
         ring_barrier();
         if constexpr (L > 0) read_frags(0, 0);
-        // one pipeline step consuming stage kt from fragment buffer CUR
-        auto step = [&](int kt, auto cur_c) {
+        // one pipeline step consuming stage kt from fragment buffer CUR:
+        // wait for stage kt+1 of this wave's ring(s), synchronise the block
+        // (every wave has then also finished reading stage kt, whose
+        // fragments are in registers), refill stage kt's slots with stages
+        // kt+SA / kt+SB, read stage kt+1's fragments and run stage kt's MFMAs.
+        // STEADY: stages kt+1, kt+SA and kt+SB exist (known at compile time).
+        // The steady-state loop then has no path around the barrier; such a
+        // path joins the loop header, and the compiler's wait analysis would
+        // make this stage's MFMAs wait for the next stage's fragment reads.
+        auto step = [&](int kt, auto cur_c, auto steady_c) __attribute__((always_inline)) {
             constexpr int CUR = decltype(cur_c)::value;
-            if (kt + 1 < KT) {
-                wait_stage<S, LPW>(min(S - 2, KT - 2 - kt));  // stage kt+1 landed
+            constexpr bool STEADY = decltype(steady_c)::value;
+            if (STEADY || kt + 1 < KT) {
+                if constexpr (ROLE == 1) {
+                    if constexpr (STEADY) wait_stage<SA, AL>(SA - 2);
+                    else wait_stage<SA, AL>(min(SA - 2, KT - 2 - kt));
+                } else if constexpr (ROLE == 2) {
+                    if constexpr (STEADY) wait_stage<SB, BL>(SB - 2);
+                    else wait_stage<SB, BL>(min(SB - 2, KT - 2 - kt));
+                } else {
+                    if constexpr (STEADY) wait_stage<SA, AL + BL>(SA - 2);
+                    else wait_stage<SA, AL + BL>(min(SA - 2, KT - 2 - kt));
+                }
                 ring_barrier();
-                if (kt + S < KT) issue(kt + S);  // into slot kt % S, read out before the barrier
+                // into stage kt's slots, read out before the barrier
+                if constexpr (ROLE == 1) {
+                    if (STEADY || kt + SA < KT) issue_a(kt + SA, 0);
+                } else if constexpr (ROLE == 2) {
+                    if (STEADY || kt + SB < KT) issue_b(kt + SB, 0);
+                } else {
+                    if (STEADY || kt + SA < KT) {
+                        issue_a(kt + SA, 0);
+                        issue_b(kt + SA, AL);
+                    }
+                }
                 if constexpr (L > 0) read_frags(kt + 1, CUR ^ 1);
             }
             __builtin_amdgcn_sched_barrier(0);  // keep the next stage's reads ahead of these MFMAs
             if constexpr (L > 0) mfmas(CUR);
         };
+        using C0 = std::integral_constant<int, 0>;
+        using C1 = std::integral_constant<int, 1>;
+        using Steady = std::true_type;
+        using Tail = std::false_type;
         // unrolled by two so the fragment buffers are indexed statically
         int kt = 0;
-        for (; kt + 1 < KT; kt += 2) {
-            step(kt, std::integral_constant<int, 0>{});
-            step(kt + 1, std::integral_constant<int, 1>{});
+        constexpr int SMAX = SA > SB ? SA : SB;
+        for (; kt + 1 + SMAX < KT; kt += 2) {
+            step(kt, C0{}, Steady{});
+            step(kt + 1, C1{}, Steady{});
         }
-        if (kt < KT) step(kt, std::integral_constant<int, 0>{});
+        for (; kt + 1 < KT; kt += 2) {
+            step(kt, C0{}, Tail{});
+            step(kt + 1, C1{}, Tail{});
+        }
+        if (kt < KT) step(kt, C0{}, Tail{});
     };
-    if (mb_live >= MB) kloop(std::integral_constant<int, MB>{});
-    else if (mb_live == 0) kloop(std::integral_constant<int, 0>{});
+    // one straight-line K loop per load role (both roles pass the same
+    // barriers, once per step) and per live row-block count
+    auto run = [&](auto live) __attribute__((always_inline)) {
+        if constexpr (SPLIT) {
+            if (a_role) kloop(live, std::integral_constant<int, 1>{});
+            else kloop(live, std::integral_constant<int, 2>{});
+        } else {
+            kloop(live, std::integral_constant<int, 0>{});
+        }
+    };
+    if (mb_live >= MB) run(std::integral_constant<int, MB>{});
+    else if (mb_live == 0) run(std::integral_constant<int, 0>{});
     else if constexpr (MB >= 2) {
-        if (mb_live == 1) kloop(std::integral_constant<int, 1>{});
+        if (mb_live == 1) run(std::integral_constant<int, 1>{});
         else if constexpr (MB >= 3) {
-            if (mb_live == 2) kloop(std::integral_constant<int, 2>{});
+            if (mb_live == 2) run(std::integral_constant<int, 2>{});
             else if constexpr (MB >= 4) {
-                if (mb_live == 3) kloop(std::integral_constant<int, 3>{});
+                if (mb_live == 3) run(std::integral_constant<int, 3>{});
             }
         }
     }
@@ -288,7 +378,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void grouped_kernel(
 }
 
 // phase: 1 = gate/up only, 2 = down only, 3 = both
-template <int BM, int BN, int BK, int WM, int WN, int S>
+template <int BM, int BN, int BK, int WM, int WN, int SA, int SB>
 int launch_grouped(int phase, const uint16_t *x, const int32_t *perm_token, const int32_t *offsets,
                    const int32_t *sel, int nsel, const int32_t *tile_start, int max_tiles,
                    const uint16_t *const *slots, int H, int I, uint16_t *h_ws, uint16_t *y, hipStream_t s) {
@@ -299,7 +389,7 @@ int launch_grouped(int phase, const uint16_t *x, const int32_t *perm_token, cons
     if (phase & 1) {
         const size_t n1 = (size_t)max_tiles * (size_t)(I / (BN / 2));
         const unsigned g1 = (unsigned)((n1 + 7) / 8 * 8);
-        grouped_kernel<BM, BN, BK, WM, WN, S, true><<<g1, 64 * WM * WN, 0, s>>>(x, perm_token, offsets, sel, nsel, tile_start,
+        grouped_kernel<BM, BN, BK, WM, WN, SA, SB, true><<<g1, 64 * WM * WN, 0, s>>>(x, perm_token, offsets, sel, nsel, tile_start,
                                                                     slots, H, I, h_ws);
         int rc = check_launch("grouped_kernel<gateup>");
         if (rc) return rc;
@@ -307,7 +397,7 @@ int launch_grouped(int phase, const uint16_t *x, const int32_t *perm_token, cons
     if (phase & 2) {
         const size_t n2 = (size_t)max_tiles * (size_t)(H / BN);
         const unsigned g2 = (unsigned)((n2 + 7) / 8 * 8);
-        grouped_kernel<BM, BN, BK, WM, WN, S, false><<<g2, 64 * WM * WN, 0, s>>>(h_ws, nullptr, offsets, sel, nsel, tile_start,
+        grouped_kernel<BM, BN, BK, WM, WN, SA, SB, false><<<g2, 64 * WM * WN, 0, s>>>(h_ws, nullptr, offsets, sel, nsel, tile_start,
                                                                      slots, H, I, y);
         return check_launch("grouped_kernel<down>");
     }
@@ -328,16 +418,16 @@ int grouped_entry(int phase, const void *x, const int32_t *perm_token, const int
     const uint16_t *const *sp = (const uint16_t *const *)slots;
     switch (block_m) {
     case 32:
-        return launch_grouped<32, 256, 64, 1, 4, 4>(phase, xp, perm_token, offsets, sel, nsel, tile_start, max_tiles, sp,
+        return launch_grouped<32, 256, 64, 1, 4, 4, 4>(phase, xp, perm_token, offsets, sel, nsel, tile_start, max_tiles, sp,
                                                 H, I, (uint16_t *)h_ws, (uint16_t *)y, s);
     case 64:
-        return launch_grouped<64, 128, 64, 2, 2, 4>(phase, xp, perm_token, offsets, sel, nsel, tile_start, max_tiles, sp,
+        return launch_grouped<64, 128, 64, 2, 2, 4, 4>(phase, xp, perm_token, offsets, sel, nsel, tile_start, max_tiles, sp,
                                                 H, I, (uint16_t *)h_ws, (uint16_t *)y, s);
     case 128:
-        return launch_grouped<128, 128, 64, 2, 2, 4>(phase, xp, perm_token, offsets, sel, nsel, tile_start, max_tiles,
+        return launch_grouped<128, 128, 64, 2, 2, 4, 4>(phase, xp, perm_token, offsets, sel, nsel, tile_start, max_tiles,
                                                  sp, H, I, (uint16_t *)h_ws, (uint16_t *)y, s);
     case 256:
-        return launch_grouped<256, 256, 32, 2, 4, 4>(phase, xp, perm_token, offsets, sel, nsel, tile_start, max_tiles,
+        return launch_grouped<256, 256, 32, 2, 4, 3, 7>(phase, xp, perm_token, offsets, sel, nsel, tile_start, max_tiles,
                                                  sp, H, I, (uint16_t *)h_ws, (uint16_t *)y, s);
     default:
         return fail(kEInval, "grouped: block_m must be 32, 64, 128 or 256");

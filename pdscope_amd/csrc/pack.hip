@@ -282,6 +282,52 @@ __global__ __launch_bounds__(256) void schedule_kernel(const int32_t *__restrict
     }
 }
 
+// Balanced tile order for the grouped kernel, which cuts its tile list (in
+// sel order) into 8 contiguous equal-count pieces, one per XCD, dispatched in
+// order.  The selected experts are ranked by rows (descending, then by
+// position), rank r is dealt to group (r / 8 even ? r % 8 : 7 - r % 8) and
+// the groups are concatenated: every piece then holds a similar mix of large
+// and small experts (similar work) and starts with its largest ones, so the
+// short tiles run last.  order[i] is the expert at position i of that list,
+// tile_start its m-tile prefix (as schedule_kernel over `order`).  nsel <= 256.
+__global__ __launch_bounds__(256) void schedule_balanced_kernel(const int32_t *__restrict__ counts,
+                                                                const int32_t *__restrict__ sel, int nsel, int bm,
+                                                                int32_t *__restrict__ order,
+                                                                int32_t *__restrict__ tile_start) {
+    __shared__ int s_rows[256];
+    __shared__ int s_at[256];  // list position -> sel position
+    __shared__ int s_wsum[4];
+    const int i = threadIdx.x;
+    s_rows[i] = i < nsel ? counts[sel[i]] : 0;
+    __syncthreads();
+    if (i < nsel) {
+        const int c = s_rows[i];
+        int r = 0;
+        for (int j = 0; j < nsel; ++j) {
+            const int cj = s_rows[j];
+            r += (cj > c) | ((cj == c) & (j < i));
+        }
+        const int full = nsel >> 3, rem = nsel & 7;
+        const int rd = r >> 3, w = r & 7;
+        const int g = (rd & 1) ? 7 - w : w;
+        // groups before g: `full` members each, plus one if the last (partial)
+        // round reaches them (round `full` deals to 0.. upward when even, 7.. downward when odd)
+        int before = g * full;
+        if (rem) before += (full & 1) ? max(0, g - (8 - rem)) : min(g, rem);
+        s_at[before + rd] = i;
+    }
+    __syncthreads();
+    int tiles = 0;
+    if (i < nsel) {
+        const int si = s_at[i];
+        order[i] = sel[si];
+        tiles = (s_rows[si] + bm - 1) / bm;
+    }
+    const int incl = block_scan256(tiles, s_wsum);
+    if (i == 0) tile_start[0] = 0;
+    if (i < nsel) tile_start[i + 1] = incl;
+}
+
 }  // namespace pd
 
 using namespace pd;
@@ -326,4 +372,15 @@ PD_API int pdscope_schedule(const int32_t *counts, const int32_t *sel, int nsel,
         return fail(kEInval, "schedule: block_m must be 32, 64, 128 or 256");
     schedule_kernel<<<1, 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(counts, sel, nsel, block_m, tile_start);
     return check_launch("schedule_kernel");
+}
+
+PD_API int pdscope_schedule_balanced(const int32_t *counts, const int32_t *sel, int nsel, int block_m,
+                                     int32_t *order, int32_t *tile_start, void *stream) {
+    if (!counts || !sel || !order || !tile_start || nsel < 0 || nsel > 256)
+        return fail(kEInval, "schedule_balanced: bad arguments (nsel must be 0..256)");
+    if (block_m != 32 && block_m != 64 && block_m != 128 && block_m != 256)
+        return fail(kEInval, "schedule_balanced: block_m must be 32, 64, 128 or 256");
+    schedule_balanced_kernel<<<1, 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(counts, sel, nsel, block_m, order,
+                                                                                   tile_start);
+    return check_launch("schedule_balanced_kernel");
 }

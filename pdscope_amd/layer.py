@@ -1,7 +1,7 @@
 """One MoE layer on the gfx950 kernels with a preallocated workspace.
 
 ``moe_forward`` is the whole GPU layer for experts addressed through a slot
-table: route (K1) -> decode GEMV (K4) for T == 1, or pack (K2) -> tile
+table: route (K1) -> decode GEMV (K4) for T == 1, or pack (K2) -> balanced tile
 schedule -> grouped SwiGLU (K3) -> merge (K5) for T > 1.  Nothing is
 allocated and nothing is read back to the host, so the call can be captured
 in a hipGraph (torch.cuda.CUDAGraph) and replayed.
@@ -33,6 +33,7 @@ class MoEWorkspace:
         self.perm_pos = torch.empty(n, **i32)
         self.row_of = torch.empty(n, **i32)
         self.tile_start = torch.empty(E + 1, **i32)
+        self.sel_order = torch.empty(E, **i32)  # balanced expert order of the grouped launch
         self.sel_all = torch.arange(E, **i32)
         rows = 1 if route_only else max(n, 1)
         self.h_ws = torch.empty(rows * I, dtype=BF16, device=device)
@@ -108,9 +109,9 @@ def experts_resident(x, ids, weights, slots, ws: MoEWorkspace, out=None, *, bloc
     _, _, _, packed = ws.views(T)
     ops.pack(ids, E, out=packed, workspace=ws.pack_ws)
     bm = block_m or ops.grouped_block_m((T * k) // E)
-    ops.schedule(packed.counts, ws.sel_all, bm, out=ws.tile_start)
+    ops.schedule(packed.counts, ws.sel_all, bm, out=ws.tile_start, order=ws.sel_order)
     max_tiles = (T * k + bm - 1) // bm + E
-    ops.swiglu_grouped(x, packed.perm_token, packed.offsets, ws.sel_all, ws.tile_start, max_tiles, bm, slots, H, I,
+    ops.swiglu_grouped(x, packed.perm_token, packed.offsets, ws.sel_order, ws.tile_start, max_tiles, bm, slots, H, I,
                        ws.h_ws, ws.y)
     ops.merge(ws.y, packed.row_of, weights, out, add_in=add_in)
     return out

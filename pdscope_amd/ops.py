@@ -146,11 +146,22 @@ def grouped_block_m(rows_hint: int) -> int:
     return int(_lib.load().pdscope_grouped_block_m(int(rows_hint)))
 
 
-def schedule(counts, sel, block_m, out=None):
+def schedule(counts, sel, block_m, out=None, order=None):
+    """Tile prefix over `sel` (order=None), or, with an int32 [nsel] `order`
+    buffer, the balanced order of pdscope_schedule_balanced and the prefix
+    over it: the grouped launch must then take `order` as its sel."""
     _need(counts, "counts", torch.int32, 1)
     _need(sel, "sel", torch.int32, 1, counts.device)
     tile_start = out if out is not None else torch.empty(sel.numel() + 1, dtype=torch.int32, device=counts.device)
-    _lib.call("pdscope_schedule", _p(counts), _p(sel), sel.numel(), block_m, _p(tile_start), _stream(counts.device))
+    if order is None:
+        _lib.call("pdscope_schedule", _p(counts), _p(sel), sel.numel(), block_m, _p(tile_start),
+                  _stream(counts.device))
+    else:
+        _need(order, "order", torch.int32, 1, counts.device)
+        if order.numel() < sel.numel():
+            raise ValueError("order buffer smaller than sel")
+        _lib.call("pdscope_schedule_balanced", _p(counts), _p(sel), sel.numel(), block_m, _p(order), _p(tile_start),
+                  _stream(counts.device))
     return tile_start
 
 

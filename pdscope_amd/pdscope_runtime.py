@@ -409,9 +409,10 @@ class PDScopeCudaRuntime:
         bm = ops.grouped_block_m(sum(rows) // len(rows))
         nsel = sel_dev.numel()
         tile_start = ws.tile_start[:nsel + 1]
-        ops.schedule(packed.counts, sel_dev, bm, out=tile_start)
+        order = ws.sel_order[:nsel]
+        ops.schedule(packed.counts, sel_dev, bm, out=tile_start, order=order)
         max_tiles = sum((r + bm - 1) // bm for r in rows)
-        ops.swiglu_grouped(x, packed.perm_token, packed.offsets, sel_dev, tile_start, max_tiles, bm, slots_dev, self.H,
+        ops.swiglu_grouped(x, packed.perm_token, packed.offsets, order, tile_start, max_tiles, bm, slots_dev, self.H,
                            self.I, ws.h_ws, ws.y)
 
     # ------------------------------------------------------------ resident decode graph

@@ -246,6 +246,58 @@ def test_grouped_qwen_multi_tile_experts(orc, pd, qwen, qwen_host, bm):
     assert m["max_rel"] <= MAX_REL and m["mean_abs"] <= MEAN_ABS, m
 
 
+def _snake_order(rows, sel):
+    """Restatement of the balanced order: rank by rows (descending, ties by
+    position), deal rank r to group r%8 (even rounds) or 7-r%8 (odd rounds),
+    concatenate the groups."""
+    ranked = sorted(range(len(sel)), key=lambda i: (-rows[sel[i]], i))
+    groups = [[] for _ in range(8)]
+    for r, i in enumerate(ranked):
+        groups[r % 8 if (r // 8) % 2 == 0 else 7 - r % 8].append(sel[i])
+    return [e for g in groups for e in g]
+
+
+@pytest.mark.parametrize("nsel,bm", [(128, 256), (61, 64), (7, 128), (1, 32), (256, 64)])
+def test_schedule_balanced_order_and_same_outputs(pd, nsel, bm):
+    """The balanced order is the snake deal of the size ranking, tile_start is
+    its m-tile prefix, and the grouped outputs do not depend on the order
+    (bitwise: every row is computed by the same tile arithmetic)."""
+    ops, layer, synthetic = pd
+    g = torch.Generator().manual_seed(nsel * 31 + bm)
+    E = max(nsel, 8)
+    H, I = 256, 128
+    rows = (torch.rand(E, generator=g) ** 3 * 300).to(torch.int32)
+    rows[torch.randperm(E, generator=g)[:E // 5]] = 17  # ties
+    sel_list = sorted(torch.randperm(E, generator=g)[:nsel].tolist())
+    counts = rows.to(DEV)
+    offsets = torch.zeros(E + 1, dtype=torch.int32)
+    offsets[1:] = torch.cumsum(rows, 0)
+    n = int(offsets[-1])
+    sel = torch.tensor(sel_list, dtype=torch.int32, device=DEV)
+    order = torch.empty(nsel, dtype=torch.int32, device=DEV)
+    ts = ops.schedule(counts, sel, bm, order=order)
+    torch.cuda.synchronize()
+    want = _snake_order(rows.tolist(), sel_list)
+    assert order.cpu().tolist() == want
+    tiles = [(int(rows[e]) + bm - 1) // bm for e in want]
+    assert ts.cpu().tolist() == [0] + np.cumsum(tiles).tolist()
+    # same outputs as the identity order
+    lay = synthetic.make_layer(H, I, E, 4, True, seed=nsel + bm, device=DEV)
+    slots = ops.slot_table([lay.experts[e] for e in range(E)], DEV)
+    x = synthetic.make_tokens(max(n, 1), H, seed=bm)
+    perm = torch.randint(0, max(n, 1), (max(n, 1),), generator=g, dtype=torch.int32).to(DEV)
+    off_d = offsets.to(DEV)
+    outs = []
+    for s_, t_ in ((sel, ops.schedule(counts, sel, bm)), (order, ts)):
+        h = torch.zeros(max(n, 1) * I, dtype=torch.bfloat16, device=DEV)
+        y = torch.zeros((max(n, 1), H), dtype=torch.bfloat16, device=DEV)
+        mt = (n + bm - 1) // bm + nsel
+        ops.swiglu_grouped(x, perm, off_d, s_, t_, mt, bm, slots, H, I, h, y)
+        outs.append((h, y))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+
+
 def test_decode_qwen(orc, pd, qwen, qwen_host):
     ops, layer, synthetic = pd
     ws = layer.MoEWorkspace(1, 2048, 768, 128, 8, DEV)
