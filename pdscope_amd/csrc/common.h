@@ -93,6 +93,33 @@ __device__ __forceinline__ float half_sum(float v) {
     return v;
 }
 
+// Sums through DPP lane moves (no LDS round trips, unlike the shuffles
+// above).  Fixed order: neighbours (xor 1), then pairs (xor 2) within quads,
+// then lane i with 7-i of each half-row and with 15-i of each row, after
+// which every lane of a 16-lane row holds the row sum; row_bcast 15 then
+// adds row 0 into row 1 and row 2 into row 3 (rows 1 and 3 hold the sums of
+// lanes 0-31 and 32-63), and row_bcast 31 adds lanes 0-31 into row 3.
+// Lanes a move does not reach add +0.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add(float v) {
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+
+// sum of each 32-lane half: lanes 16-31 hold lanes 0-31's, lanes 48-63 lanes 32-63's
+__device__ __forceinline__ float half_sum_dpp(float v) {
+    v = dpp_add<0xb1, 0xf>(v);   // quad_perm [1,0,3,2]
+    v = dpp_add<0x4e, 0xf>(v);   // quad_perm [2,3,0,1]
+    v = dpp_add<0x141, 0xf>(v);  // row_half_mirror
+    v = dpp_add<0x140, 0xf>(v);  // row_mirror
+    return dpp_add<0x142, 0xa>(v);  // row_bcast:15 into rows 1, 3
+}
+
+// sum over the wave, returned to every lane
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v = dpp_add<0x143, 0xc>(half_sum_dpp(v));  // row_bcast:31 into rows 2, 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));

@@ -63,8 +63,8 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(const uint16_t *__re
                 u = dot8(uv[it][j], xv[j], u);
             }
         }
-        g = wave_sum(g);
-        u = wave_sum(u);
+        g = wave_sum_dpp(g);
+        u = wave_sum_dpp(u);
         const int q = q0 + it;
         if (lane == 0 && q < items) {
             const float a = bf16_round(silu_f32(bf16_round(g)));
@@ -108,10 +108,11 @@ __global__ __launch_bounds__(256) void decode_down_kernel(const uint16_t *__rest
             }
             if (!base) acc = 0.0f;
         }
-        acc = half_sum(acc);
-        const float odd = __shfl(acc, 32, kWave);
+        acc = half_sum_dpp(acc);  // lanes 31 / 63 hold the sums of the two halves
+        const float even = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 31));
+        const float odd = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 63));
         if (lane == 0) {
-            total = __builtin_fmaf(bf2f(w[p]), bf16_round(acc), total);
+            total = __builtin_fmaf(bf2f(w[p]), bf16_round(even), total);
             if (p + 1 < k) total = __builtin_fmaf(bf2f(w[p + 1]), bf16_round(odd), total);
         }
     }

@@ -163,7 +163,7 @@ __global__ __launch_bounds__(256, 2) void decode_layer_kernel(
 #pragma unroll
             for (int j = 0; j < NCH; ++j)
                 if (lane + 64 * j < C) a = dot8(xv[j], wv[j], a);
-            a = wave_sum(a);
+            a = wave_sum_dpp(a);
             b = f2bf(a);
             if (lane == 0) logits[e] = (uint16_t)b;
         }
@@ -242,8 +242,8 @@ __global__ __launch_bounds__(256, 2) void decode_layer_kernel(
                 u = dot8(uv[p][j], xv[j], u);
             }
         }
-        g = wave_sum(g);
-        u = wave_sum(u);
+        g = wave_sum_dpp(g);
+        u = wave_sum_dpp(u);
         const int q = q0 + p;
         if (lane == 0) {
             const float a = bf16_round(silu_f32(bf16_round(g)));
@@ -252,11 +252,11 @@ __global__ __launch_bounds__(256, 2) void decode_layer_kernel(
             s_pub[wave * P + p] = (epoch << 16) | hb;
         }
     }
-    // down rows, issued once the gate/up rows are consumed (fewer loads in
-    // flight per wave streams faster; they land during the h hand-off):
-    // block b owns output columns 4b..4b+3; half-wave (wave w, half h) owns
-    // slot s = 2w + h and reads that expert's 4 rows, so a wave touches two
-    // experts' pages instead of k
+    // down rows, issued once the gate/up rows are consumed (the gate/up rows
+    // feed the h hand-off, the critical path, and stream faster alone; the
+    // down rows land during the hand-off): block b owns output columns
+    // 4b..4b+3; half-wave (wave w, half h) owns slot s = 2w + h and reads
+    // that expert's 4 rows, so a wave touches two experts' pages instead of k
     const int half = lane >> 5, hl = lane & 31;
     const int slot = 2 * wave + half;
     const size_t IH2 = 2 * (size_t)I * H;
@@ -297,8 +297,8 @@ __global__ __launch_bounds__(256, 2) void decode_layer_kernel(
             }
             if (!dhas) acc = 0.0f;
         }
-        acc = half_sum(acc);
-        if (hl == 0 && slot < k) s_y[slot * 4 + c4] = bf16_round(acc);
+        acc = half_sum_dpp(acc);  // lanes 31 / 63 hold the sums of the two halves
+        if (hl == 31 && slot < k) s_y[slot * 4 + c4] = bf16_round(acc);
     }
     __syncthreads();
     // merge in slot order, one lane per column

@@ -61,7 +61,7 @@ __global__ __launch_bounds__(256) void route_gemv_kernel(
 #pragma unroll
             for (int j = 0; j < NCH; ++j)
                 if (lane + 64 * j < C) a = dot8(xv[j], wv[j], a);
-            a = wave_sum(a);
+            a = wave_sum_dpp(a);
             if (lane == 0) logits[(size_t)t * E + e] = (uint16_t)f2bf(a);
         }
     }
