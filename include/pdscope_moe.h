@@ -123,8 +123,8 @@ int pdscope_grouped_block_m(int rows_hint);
  * bf16 MFMA with fp32 accumulation.  max_tiles bounds sum ceil(m_e/block_m)
  * (e.g. ceil(rows/block_m) + nsel); tiles beyond tile_start[nsel] exit.
  * block_m: 32, 64, 128 or 256, the row tile pdscope_schedule used.
- * Limits: H % 64 == 0, I % 64 == 0; with block_m 32 or 256 (256-column
- * tiles) also H % 256 == 0 and I % 128 == 0, with 64 or 128 H % 128 == 0.
+ * Limits: H % 256 == 0 and I % 128 == 0 (every row tile is 256 columns
+ * wide: 128 gate + 128 up columns, or 256 output columns).
  */
 int pdscope_swiglu_grouped(const void *x, const int32_t *perm_token, const int32_t *offsets,
                            const int32_t *sel, int nsel, const int32_t *tile_start,

@@ -421,10 +421,10 @@ int grouped_entry(int phase, const void *x, const int32_t *perm_token, const int
         return launch_grouped<32, 256, 64, 1, 4, 4, 4>(phase, xp, perm_token, offsets, sel, nsel, tile_start, max_tiles, sp,
                                                 H, I, (uint16_t *)h_ws, (uint16_t *)y, s);
     case 64:
-        return launch_grouped<64, 128, 64, 2, 2, 4, 4>(phase, xp, perm_token, offsets, sel, nsel, tile_start, max_tiles, sp,
+        return launch_grouped<64, 256, 64, 2, 4, 3, 4>(phase, xp, perm_token, offsets, sel, nsel, tile_start, max_tiles, sp,
                                                 H, I, (uint16_t *)h_ws, (uint16_t *)y, s);
     case 128:
-        return launch_grouped<128, 128, 64, 2, 2, 4, 4>(phase, xp, perm_token, offsets, sel, nsel, tile_start, max_tiles,
+        return launch_grouped<128, 256, 64, 2, 4, 3, 3>(phase, xp, perm_token, offsets, sel, nsel, tile_start, max_tiles,
                                                  sp, H, I, (uint16_t *)h_ws, (uint16_t *)y, s);
     case 256:
         return launch_grouped<256, 256, 32, 2, 4, 3, 7>(phase, xp, perm_token, offsets, sel, nsel, tile_start, max_tiles,
