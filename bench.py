@@ -303,7 +303,7 @@ def zipf_gemm(lay, x, bias, device, reps=20):
     _, ids, _ = layer.route(x, lay.gate, ws, bias=bias)
     _, _, _, packed = ws.views(T)
     ops.pack(ids, E, out=packed, workspace=ws.pack_ws)
-    bm = ops.grouped_block_m((T * K_TOP) // E)
+    bm = ops.grouped_block_m((T * K_TOP) // E, int(ws.counts.max().item()))
     ops.schedule(packed.counts, ws.sel_all, bm, out=ws.tile_start, order=ws.sel_order)
     max_tiles = (T * K_TOP + bm - 1) // bm + E
     stream = torch.cuda.current_stream(device)

@@ -106,10 +106,19 @@ int pdscope_schedule(const int32_t *counts, const int32_t *sel, int nsel, int bl
 int pdscope_schedule_balanced(const int32_t *counts, const int32_t *sel, int nsel, int block_m,
                               int32_t *order, int32_t *tile_start, void *stream);
 
-/* Row tile (32, 64, 128 or 256) for `rows_hint` average rows per selected
- * expert: the smallest listed tile that covers a typical expert in one
- * m-tile (<= 16, 64, 160 rows; 256 above). */
+/* Row tile (32, 64, 128, 256 or 384) for `rows_hint` average rows per
+ * selected expert: <= 16 rows 32, <= 64 rows 64, <= 96 rows 128, <= 192 rows
+ * 256, <= 320 rows 384 (one tile holds a typical expert, so its weights
+ * stream once), 256 above.  No reference counterpart: the reference launches
+ * one torch GEMM chain per expert (expertbench/adapters/qwen.py:87-90). */
 int pdscope_grouped_block_m(int rows_hint);
+
+/* As pdscope_grouped_block_m(mean_rows), except that a launch whose largest
+ * expert has more than 768 rows keeps the 256-row tile instead of 384: the
+ * 384-row tile is 128 columns wide and reads every activation row twice as
+ * often, which costs more than it saves once a few experts span several
+ * row tiles (skewed routing). */
+int pdscope_grouped_block_m_max(int mean_rows, int max_rows);
 
 /*
  * A4 grouped SwiGLU for prefill: replaces expert_forward

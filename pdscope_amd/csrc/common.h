@@ -39,6 +39,19 @@ __device__ __forceinline__ uint32_t f2bf(float f) {
 
 __device__ __forceinline__ float bf16_round(float f) { return bf2f(f2bf(f)); }
 
+// The same round-to-nearest-even conversion by gfx950's v_cvt_pk_bf16_f32
+// (equal to f2bf for every finite value and infinity): for epilogues that
+// convert many values per lane.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t f2bf_hw(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+__device__ __forceinline__ float bf16_round_hw(float f) { return (float)(__bf16)f; }
+// lo in bits 0-15, hi in bits 16-31
+__device__ __forceinline__ uint32_t f2bf2_hw(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{lo, hi}), bf16x2_t));
+}
+
 // low / high bf16 of a packed 32-bit word, widened to fp32
 __device__ __forceinline__ float lo_bf(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi_bf(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }

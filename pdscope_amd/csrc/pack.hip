@@ -368,8 +368,8 @@ PD_API int pdscope_pack(const int32_t *ids, int T, int k, int E, int32_t *counts
 PD_API int pdscope_schedule(const int32_t *counts, const int32_t *sel, int nsel, int block_m,
                             int32_t *tile_start, void *stream) {
     if (!counts || !sel || !tile_start || nsel < 0) return fail(kEInval, "schedule: bad arguments");
-    if (block_m != 32 && block_m != 64 && block_m != 128 && block_m != 256)
-        return fail(kEInval, "schedule: block_m must be 32, 64, 128 or 256");
+    if (block_m != 32 && block_m != 64 && block_m != 128 && block_m != 256 && block_m != 384)
+        return fail(kEInval, "schedule: block_m must be 32, 64, 128, 256 or 384");
     schedule_kernel<<<1, 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(counts, sel, nsel, block_m, tile_start);
     return check_launch("schedule_kernel");
 }
@@ -378,8 +378,8 @@ PD_API int pdscope_schedule_balanced(const int32_t *counts, const int32_t *sel, 
                                      int32_t *order, int32_t *tile_start, void *stream) {
     if (!counts || !sel || !order || !tile_start || nsel < 0 || nsel > 256)
         return fail(kEInval, "schedule_balanced: bad arguments (nsel must be 0..256)");
-    if (block_m != 32 && block_m != 64 && block_m != 128 && block_m != 256)
-        return fail(kEInval, "schedule_balanced: block_m must be 32, 64, 128 or 256");
+    if (block_m != 32 && block_m != 64 && block_m != 128 && block_m != 256 && block_m != 384)
+        return fail(kEInval, "schedule_balanced: block_m must be 32, 64, 128, 256 or 384");
     schedule_balanced_kernel<<<1, 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(counts, sel, nsel, block_m, order,
                                                                                    tile_start);
     return check_launch("schedule_balanced_kernel");

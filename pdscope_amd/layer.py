@@ -68,7 +68,7 @@ def route(x, gate, ws: MoEWorkspace, *, normalize=True, bias=None):
 
 
 # column width of the gate|up tile for each row-tile height of the grouped kernel
-_GATEUP_COLS = {32: 128, 64: 128, 128: 128, 256: 128}
+_GATEUP_COLS = {32: 128, 64: 128, 128: 128, 256: 128, 384: 64}
 
 
 def shared_block_m(T: int, I: int, min_tiles: int = 512) -> int:

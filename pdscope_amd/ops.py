@@ -142,8 +142,12 @@ def pack(ids, E, out: Packed | None = None, workspace=None) -> Packed:
     return out
 
 
-def grouped_block_m(rows_hint: int) -> int:
-    return int(_lib.load().pdscope_grouped_block_m(int(rows_hint)))
+def grouped_block_m(rows_hint: int, max_rows: int | None = None) -> int:
+    """Row tile of the grouped SwiGLU launch for rows_hint mean rows per expert
+    (and, when the host knows it, the largest expert's rows)."""
+    if max_rows is None:
+        return int(_lib.load().pdscope_grouped_block_m(int(rows_hint)))
+    return int(_lib.load().pdscope_grouped_block_m_max(int(rows_hint), int(max_rows)))
 
 
 def schedule(counts, sel, block_m, out=None, order=None):

@@ -406,7 +406,7 @@ class PDScopeCudaRuntime:
         """One grouped SwiGLU launch over the experts in sel_dev, whose routed
         row counts (known on the host since the demand reveal) are `rows`:
         the row-tile height follows their mean, the grid their exact tile count."""
-        bm = ops.grouped_block_m(sum(rows) // len(rows))
+        bm = ops.grouped_block_m(sum(rows) // len(rows), max(rows))
         nsel = sel_dev.numel()
         tile_start = ws.tile_start[:nsel + 1]
         order = ws.sel_order[:nsel]

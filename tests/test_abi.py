@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
     assert set(_lib.SIGNATURES) == set(declared_symbols())
     assert lib.pdscope_version().decode().startswith("pdscope_moe gfx950")
     assert lib.pdscope_route_workspace_bytes() >= 4
-    assert _lib.load().pdscope_grouped_block_m(8) == 32 and _lib.load().pdscope_grouped_block_m(32) == 64
+    assert [lib.pdscope_grouped_block_m(r) for r in (8, 32, 80, 128, 256, 600)] == [32, 64, 128, 256, 384, 256]
 
 
 def test_invalid_arguments_raise_before_any_launch():

@@ -201,7 +201,7 @@ def test_layer_prefill_qwen(orc, pd, qwen, qwen_host, T):
     assert m["max_rel"] <= MAX_REL and m["mean_abs"] <= MEAN_ABS, m
 
 
-@pytest.mark.parametrize("bm", [32, 64, 128, 256])
+@pytest.mark.parametrize("bm", [32, 64, 128, 256, 384])
 def test_grouped_block_m_variants(orc, pd, bm):
     """Every row tile on a small layer with ragged expert sizes (0..many rows)."""
     ops, layer, synthetic = pd
@@ -223,7 +223,7 @@ def test_grouped_block_m_variants(orc, pd, bm):
     assert m["max_rel"] <= MAX_REL and m["mean_abs"] <= MEAN_ABS, m
 
 
-@pytest.mark.parametrize("bm", [128, 256])
+@pytest.mark.parametrize("bm", [128, 256, 384])
 def test_grouped_qwen_multi_tile_experts(orc, pd, qwen, qwen_host, bm):
     """Qwen shape with a skewed router: hot experts span several row tiles
     (and the weight tiles they share), cold ones a partial tile or none."""
