@@ -78,16 +78,20 @@ __device__ __forceinline__ uint4 ld_g(const void *p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-// dot of 8 bf16 pairs packed in two uint4, accumulated in order into acc
+// dot of 8 bf16 pairs packed in two uint4, accumulated in word order into
+// acc by four v_dot2_f32_bf16 (each adds the two bf16 products of one 32-bit
+// word pair to acc).  One instruction per two pairs instead of six (unpack
+// and fma); measured on gfx950 it matches the exactly rounded two-product
+// sum more often than an fma chain does and keeps denormals.
+__device__ __forceinline__ float dot2w(uint32_t a, uint32_t b, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), acc,
+                                           false);
+}
 __device__ __forceinline__ float dot8(const uint4 a, const uint4 b, float acc) {
-    acc = __builtin_fmaf(lo_bf(a.x), lo_bf(b.x), acc);
-    acc = __builtin_fmaf(hi_bf(a.x), hi_bf(b.x), acc);
-    acc = __builtin_fmaf(lo_bf(a.y), lo_bf(b.y), acc);
-    acc = __builtin_fmaf(hi_bf(a.y), hi_bf(b.y), acc);
-    acc = __builtin_fmaf(lo_bf(a.z), lo_bf(b.z), acc);
-    acc = __builtin_fmaf(hi_bf(a.z), hi_bf(b.z), acc);
-    acc = __builtin_fmaf(lo_bf(a.w), lo_bf(b.w), acc);
-    acc = __builtin_fmaf(hi_bf(a.w), hi_bf(b.w), acc);
+    acc = dot2w(a.x, b.x, acc);
+    acc = dot2w(a.y, b.y, acc);
+    acc = dot2w(a.z, b.z, acc);
+    acc = dot2w(a.w, b.w, acc);
     return acc;
 }
 

@@ -28,8 +28,9 @@
 // device-scope relaxed stores (write-through) and read with device-scope
 // relaxed loads until its epoch is the current one.  A value and its
 // validity travel in one word, so no ordering between locations is needed.
-// Each block publishes its words with one thread, in 8-byte stores
-// (logits: 4 per block in a line of their own; h: 4P consecutive words).
+// Each block publishes its words from its last wave, in 8-byte stores
+// (logits: 4 per block in a line of their own, one thread; h: 4P
+// consecutive words, 2P threads), and polls with the other waves.
 // The epoch is a per-block counter kept in the workspace (all blocks of a
 // launch see the same value because every launch runs every block once);
 // it cycles through 1..65535, never 0, so a zero-filled workspace holds no
@@ -52,6 +53,14 @@ namespace pd {
 // Polls one thread may spend over the whole launch (a normal launch needs a
 // few hundred at most); once spent, the thread stops waiting.
 constexpr uint32_t kSpinBudget = 1u << 16;
+
+// First thread of the last wave of a block: it publishes the block's words
+// and that wave takes no part in polling.  On gfx9 the vector-memory counter
+// covers stores as well as loads, so a wave that has just stored would see
+// each of its polls wait for its stores to be acknowledged (write-through to
+// memory, slow while the weight stream saturates HBM); for the same reason
+// the logits and h_ws outputs are stored at the end of the launch.
+constexpr int kPublisher = 192;
 
 constexpr int kDecodeMaxK = 8;
 constexpr int kDecodeMaxE = 256;
@@ -165,11 +174,10 @@ __global__ __launch_bounds__(256, 2) void decode_layer_kernel(
                 if (lane + 64 * j < C) a = dot8(xv[j], wv[j], a);
             a = wave_sum_dpp(a);
             b = f2bf(a);
-            if (lane == 0) logits[e] = (uint16_t)b;
         }
         if (lane == 0) s_pub[wave] = (epoch << 16) | b;
         __syncthreads();
-        if (tid == 0) {
+        if (tid == kPublisher) {
             uint64_t *line = reinterpret_cast<uint64_t *>(ws + kWsLogit + blockIdx.x * 32);
             __hip_atomic_store(line, (uint64_t)s_pub[0] | ((uint64_t)s_pub[1] << 32), __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
@@ -231,30 +239,51 @@ __global__ __launch_bounds__(256, 2) void decode_layer_kernel(
             uv[p][j] = ld_nt(urow + 8 * min(lane + 64 * j, C - 1));
         }
     }
-    // ---- 4. gate/up -> h
+    // ---- 4. gate/up -> h.  The 2P dot products are independent chains
+    // (each keeps its chunk order); interleaved, their latencies overlap.
+    float g[P], u[P];
 #pragma unroll
-    for (int p = 0; p < P; ++p) {
-        float g = 0.0f, u = 0.0f;
+    for (int p = 0; p < P; ++p) g[p] = u[p] = 0.0f;
 #pragma unroll
-        for (int j = 0; j < NCH; ++j) {
-            if (lane + 64 * j < C) {
-                g = dot8(gv[p][j], xv[j], g);
-                u = dot8(uv[p][j], xv[j], u);
+    for (int j = 0; j < NCH; ++j) {
+        if (lane + 64 * j < C) {
+#pragma unroll
+            for (int p = 0; p < P; ++p) {
+                g[p] = dot8(gv[p][j], xv[j], g[p]);
+                u[p] = dot8(uv[p][j], xv[j], u[p]);
             }
         }
-        g = wave_sum_dpp(g);
-        u = wave_sum_dpp(u);
-        const int q = q0 + p;
-        if (lane == 0) {
-            const float a = bf16_round(silu_f32(bf16_round(g)));
-            const uint32_t hb = has[p] ? f2bf(a * bf16_round(u)) : 0u;
-            if (q < KI) h_ws[q] = (uint16_t)hb;
+    }
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        g[p] = wave_sum_dpp(g[p]);
+        u[p] = wave_sum_dpp(u[p]);
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            const float a = bf16_round(silu_f32(bf16_round(g[p])));
+            const uint32_t hb = has[p] ? f2bf(a * bf16_round(u[p])) : 0u;
             s_pub[wave * P + p] = (epoch << 16) | hb;
         }
     }
-    // down rows, issued once the gate/up rows are consumed (the gate/up rows
-    // feed the h hand-off, the critical path, and stream faster alone; the
-    // down rows land during the hand-off): block b owns output columns
+    // the block's 4P words go out as 8-byte writes by the last wave's first
+    // 2P threads
+    __syncthreads();
+    if (tid >= kPublisher && tid < kPublisher + 2 * P) {
+        const int t2 = tid - kPublisher;
+        const int qb = blockIdx.x * 4 * P + 2 * t2;
+        if (qb < KI)
+            __hip_atomic_store(reinterpret_cast<uint64_t *>(ws + kWsH + qb),
+                               (uint64_t)s_pub[2 * t2] | ((uint64_t)s_pub[2 * t2 + 1] << 32), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
+
+    // down rows, issued once every wave of the block has consumed its
+    // gate/up rows (the gate/up rows feed the h hand-off, the critical path;
+    // a wave that issued its down rows as soon as its own gate/up rows were
+    // in would slow its sibling waves' gate/up rows down; the down rows land
+    // during the hand-off): block b owns output columns
     // 4b..4b+3; half-wave (wave w, half h) owns slot s = 2w + h and reads
     // that expert's 4 rows, so a wave touches two experts' pages instead of k
     const int half = lane >> 5, hl = lane & 31;
@@ -272,33 +301,32 @@ __global__ __launch_bounds__(256, 2) void decode_layer_kernel(
         for (int c = 0; c < DC; ++c) dv[c4][c] = ld_nt(row + 8 * min(hl + 32 * c, CI - 1));
     }
 
-    // the block's 4P words go out as 8-byte writes by one thread
-    __syncthreads();
-    if (tid < 2 * P) {
-        const int qb = blockIdx.x * 4 * P + 2 * tid;
-        if (qb < KI)
-            __hip_atomic_store(reinterpret_cast<uint64_t *>(ws + kWsH + qb),
-                               (uint64_t)s_pub[2 * tid] | ((uint64_t)s_pub[2 * tid + 1] << 32), __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-    }
 
-    // ---- 5. collect h, then down + merge
-    collect<6>(ws + kWsH, KI, tid, blockDim.x, epoch, err, budget, reinterpret_cast<uint16_t *>(s_h));
+    // ---- 5. collect h (the other waves), then down + merge
+    if (tid < kPublisher)
+        collect<8>(ws + kWsH, KI, tid, kPublisher, epoch, err, budget, reinterpret_cast<uint16_t *>(s_h));
     __syncthreads();
-    // y[s][c] = bf16(h_s . down_s[col c]), each half-wave its own slot
+    // y[s][c] = bf16(h_s . down_s[col c]), each half-wave its own slot: the
+    // slot's h chunks are read once, and the four column chains (each in
+    // chunk order) are interleaved so their latencies overlap
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (slot < k) {
+        uint4 hv[DC];
+#pragma unroll
+        for (int c = 0; c < DC; ++c) hv[c] = s_h[slot * CI + min(hl + 32 * c, CI - 1)];
+#pragma unroll
+        for (int c = 0; c < DC; ++c) {
+            if (hl + 32 * c < CI) {
+#pragma unroll
+                for (int c4 = 0; c4 < 4; ++c4) acc[c4] = dot8(dv[c4][c], hv[c], acc[c4]);
+            }
+        }
+        if (!dhas) acc[0] = acc[1] = acc[2] = acc[3] = 0.0f;
+    }
 #pragma unroll
     for (int c4 = 0; c4 < 4; ++c4) {
-        float acc = 0.0f;
-        if (slot < k) {
-#pragma unroll
-            for (int c = 0; c < DC; ++c) {
-                const int ch = hl + 32 * c;
-                if (ch < CI) acc = dot8(dv[c4][c], s_h[slot * CI + ch], acc);
-            }
-            if (!dhas) acc = 0.0f;
-        }
-        acc = half_sum_dpp(acc);  // lanes 31 / 63 hold the sums of the two halves
-        if (hl == 31 && slot < k) s_y[slot * 4 + c4] = bf16_round(acc);
+        acc[c4] = half_sum_dpp(acc[c4]);  // lanes 31 / 63 hold the sums of the two halves
+        if (hl == 31 && slot < k) s_y[slot * 4 + c4] = bf16_round(acc[c4]);
     }
     __syncthreads();
     // merge in slot order, one lane per column
@@ -307,6 +335,14 @@ __global__ __launch_bounds__(256, 2) void decode_layer_kernel(
         float total = 0.0f;
         for (int s2 = 0; s2 < k; ++s2) total = __builtin_fmaf(bf2f(s_tk.selw[s2]), s_y[s2 * 4 + tid], total);
         if (col < H) out[col] = (uint16_t)f2bf(total);
+    }
+    // outputs off the critical path: the logits (block 0, from the collected
+    // words) and this block's h values
+    if (blockIdx.x == 0)
+        for (int e = tid; e < E; e += blockDim.x) logits[e] = (uint16_t)(__float_as_uint(s_logit[e]) >> 16);
+    if (tid < 4 * P) {
+        const int q = blockIdx.x * 4 * P + tid;
+        if (q < KI) h_ws[q] = (uint16_t)s_pub[tid];
     }
     if (tid == 0) __hip_atomic_store(ws + kWsEpoch + blockIdx.x, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

@@ -51,24 +51,18 @@ __device__ __forceinline__ float dpp_max_f32(float f) {
     return __int_as_float(__builtin_amdgcn_readlane(v, 63));
 }
 
-// lrow: E logits of the token (bf16 values held as fp32, in LDS).
-// Lane l owns experts l, l+64, ...; the softmax denominator is summed per
-// lane in that order and then by an xor butterfly over offsets 32..1, an
-// order that is fixed and reproduced by the host-side checker.
-// Selection: k rounds of a wave-wide max over the probabilities' bit
-// patterns (p >= 0, so integer order is float order; taken candidates drop
-// to -1); among equal maxima the lowest expert id wins (ballot, first set
-// lane of the lowest j).  This is the total order "higher probability
-// first, lower expert id on ties", so the k rounds give the sorted top-k.
-// ids / weights / probs (global, row t) are written when non-null.
+// Softmax of one token's logits by one wave.  lrow: E logits of the token
+// (bf16 values held as fp32, in LDS).  Lane l owns experts l, l+64, ...;
+// the softmax denominator is summed per lane in that order and then by an
+// xor butterfly over offsets 32..1, an order that is fixed and reproduced by
+// the host-side checker.  p[j] is the probability of expert lane + 64 j (0
+// where that is >= E); probs row t is written when non-null.
 template <int J>
-__device__ __forceinline__ void topk_token(const float *lrow, const float *__restrict__ bias, int E, int k,
-                                           int normalize, int t, int32_t *__restrict__ ids,
-                                           uint16_t *__restrict__ weights, float *__restrict__ probs,
-                                           TopkScratch *sc) {
+__device__ __forceinline__ void softmax_wave(const float *lrow, const float *__restrict__ bias, int E, int t,
+                                             float *__restrict__ probs, float (&p)[J]) {
 #pragma clang fp contract(off)
     const int lane = lane_id();
-    float v[J], p[J];
+    float v[J];
     float m = -__builtin_inff();
 #pragma unroll
     for (int j = 0; j < J; ++j) {
@@ -94,14 +88,33 @@ __device__ __forceinline__ void topk_token(const float *lrow, const float *__res
         p[j] = ex;
     }
     const float S = wave_sum(acc);
-    int hi[J];
 #pragma unroll
     for (int j = 0; j < J; ++j) {
         p[j] = p[j] / S;
         const int e = lane + 64 * j;
-        hi[j] = e < E ? (int)__float_as_uint(p[j]) : -1;
         if (e < E && probs) probs[(size_t)t * E + e] = p[j];
     }
+}
+
+// Softmax + selection of one token by one wave.  Selection: k rounds of a
+// wave-wide max over the probabilities' bit patterns (p >= 0, so integer
+// order is float order; taken candidates drop to -1); among equal maxima the
+// lowest expert id wins (ballot, first set lane of the lowest j).  This is
+// the total order "higher probability first, lower expert id on ties", so
+// the k rounds give the sorted top-k.  ids / weights / probs (global, row t)
+// are written when non-null.
+template <int J>
+__device__ __forceinline__ void topk_token(const float *lrow, const float *__restrict__ bias, int E, int k,
+                                           int normalize, int t, int32_t *__restrict__ ids,
+                                           uint16_t *__restrict__ weights, float *__restrict__ probs,
+                                           TopkScratch *sc) {
+#pragma clang fp contract(off)
+    const int lane = lane_id();
+    float p[J];
+    softmax_wave<J>(lrow, bias, E, t, probs, p);
+    int hi[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) hi[j] = lane + 64 * j < E ? (int)__float_as_uint(p[j]) : -1;
     float myp = 0.0f, denom = 0.0f;
     int myid = 0;
     for (int r = 0; r < k; ++r) {
