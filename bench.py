@@ -245,7 +245,8 @@ def run_zipf_staged(steps, warmup, n_layers, device, seed0):
         del lay
     torch.cuda.empty_cache()
     xs = [synthetic.make_tokens(T, H, seed=seed0 + 9007 + 1000 * i, device=device) for i in range(n_layers)]
-    rt = PDScopeCudaRuntime(masters, hot_keys=hot, speculative_slots=0, demand_slots=8, device=device)
+    rt = PDScopeCudaRuntime(masters, hot_keys=hot, speculative_slots=0, demand_slots=8, device=device,
+                            diagnostics=False)
     try:
         def step(i):
             # one request per pass over the rotated layers (the ledger orders events per request)
@@ -368,7 +369,7 @@ def run_stack(n_layers, device, seed0, T_prefill=2048, n_decode=64, cap_gib=24, 
     if speculative < 0:
         raise ValueError("hot set and staging slots exceed the HBM cap")
     rt = PDScopeCudaRuntime(masters, hot_keys=hot, speculative_slots=speculative, demand_slots=demand_slots,
-                            resident_graphs=True, device=device)
+                            resident_graphs=True, device=device, diagnostics=False)
     setup_s = time.perf_counter() - t_setup
     try:
         def pass_(x, step):

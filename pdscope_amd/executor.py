@@ -77,6 +77,14 @@ def masters_from_block(layer, block, E, H, I, *, pin=True, chunk_bytes=1 << 28):
 
 
 @dataclass
+class PendingCpu:
+    """A CPU-backend expert call in flight (key, future, input rows)."""
+    key: ExpertKey
+    future: object
+    input_ref: object
+
+
+@dataclass
 class PendingCompute:
     handles: tuple
     output: object
@@ -177,6 +185,8 @@ class ExpertExecutor:
         self._dev_tables = {}   # layer -> device int64 [E]
         self._ring = _PinnedRing(8 * 256)
         self._group_stream_ctx = None
+        self._cpu_pool = None
+        self._cpu_tasks = {}  # key -> PendingCpu
 
     # ------------------------------------------------------------ sources
 
@@ -403,7 +413,56 @@ class ExpertExecutor:
 
         return self.gpu_group([key], launch, input_ref=inputs)
 
+    # ------------------------------------------------------------ CPU experts
+
+    def submit_cpu(self, key, inputs):
+        """Run one expert on the caller's CPU backend (executor.py:528-560):
+        ``cpu_backend.submit(key, inputs)`` when the backend has it, else the
+        callable ``cpu_backend(key, inputs)`` on one worker thread, so the CPU
+        work overlaps the GPU launches.  inputs: CPU bf16 [rows, H].  There is
+        no built-in CPU expert: without a backend this raises."""
+        self._open()
+        backend = self.cpu_backend
+        if backend is None:
+            raise ValueError("CPU placement needs an explicit CPU backend")
+        if (key in self._cpu_tasks or key not in self.cache.unfinished_demand_keys or inputs.device.type != "cpu"
+                or inputs.dtype != torch.bfloat16 or inputs.ndim != 2
+                or inputs.shape[1] != self.masters[key].tensors["gate_proj"].shape[1]):
+            raise ValueError("CPU submission requires unique active demand and CPU BF16 input")
+        if callable(getattr(backend, "submit", None)):
+            future = backend.submit(key, inputs)
+        else:
+            if self._cpu_pool is None:
+                from concurrent.futures import ThreadPoolExecutor
+                self._cpu_pool = ThreadPoolExecutor(max_workers=1, thread_name_prefix="pdscope-cpu")
+            future = self._cpu_pool.submit(backend, key, inputs)
+        pending = PendingCpu(key, future, inputs)
+        self._cpu_tasks[key] = pending
+        return pending
+
+    def finish_cpu(self, pending, *, wait=False):
+        """The expert's unweighted CPU bf16 output [rows, H] (None while it runs
+        and wait is False); completes its demand in the ledger."""
+        self._open()
+        if self._cpu_tasks.get(pending.key) is not pending:
+            raise ValueError("CPU completion does not own an active task")
+        if not wait and not pending.future.done():
+            return None
+        out = pending.future.result()
+        if isinstance(out, tuple):  # (output, timing) as the reference's pool returns
+            out = out[0]
+        if (not isinstance(out, torch.Tensor) or out.device.type != "cpu" or out.dtype != torch.bfloat16
+                or tuple(out.shape) != tuple(pending.input_ref.shape)):
+            raise ValueError("CPU backend must return completed unweighted CPU BF16 input-shaped output")
+        self.cache.finish_cpu(pending.key)
+        del self._cpu_tasks[pending.key]
+        pending.input_ref = None
+        return out
+
     def shutdown(self):
+        if self._cpu_pool is not None:
+            self._cpu_pool.shutdown(wait=True)
+            self._cpu_pool = None
         if not self.closed:
             self.load_stream.synchronize()
             self.compute_stream.synchronize()

@@ -26,13 +26,19 @@ With ``resident_graphs=True`` a decode layer whose experts are all resident
 replays a captured hipGraph of route + decode (K1 + K4); its ledger accounting
 follows the replay (nothing can evict while the control thread waits).
 
-This runtime places every expert on the GPU: the CPU/GPU split of
-``plan_pdscope`` (expertbench/pdscope_policy.py:72-223) is not part of this
-path, so ``costs`` and ``cpu_backend`` are accepted and recorded but unused.
+Placement.  Given a cost table (``costs``, e.g. costs.FileCosts) AND a
+``cpu_backend``, each call plans with ``plan_pdscope``
+(expertbench/pdscope_policy.py:72-223, restated in policy.py): the CPU queue
+runs on the backend (``cpu_backend(key, rows) -> rows`` or its ``submit``),
+overlapped with the GPU launches, and its outputs fill their rows of the
+grouped output before the merge; resident, demand and prefetch queues follow
+the plan, and the decode graph replay is not used.  Without either, every
+expert runs on the GPU.  There is no built-in CPU expert path.
 """
 from __future__ import annotations
 
 import hashlib
+import time
 from pathlib import Path
 
 import torch
@@ -42,6 +48,7 @@ from . import ops
 from .adapters.qwen import Routing
 from .cache import DemandID, ExpertCache, ExpertKey
 from .executor import ExpertExecutor
+from .policy import plan_pdscope
 
 
 def load_hot_profile(path, masters, slots):
@@ -96,6 +103,8 @@ class PDScopeCudaRuntime:
         self.costs, self.cpu_backend, self.native_dispatch = costs, cpu_backend, native_dispatch
         self.demand_slots, self.diagnostics = demand_slots, diagnostics
         self.merge, self.dispatch = merge, dispatch
+        self.input_pregather, self.graph_output_pool = input_pregather, graph_output_pool
+        self.balance_profile, self.decode_cpu_target = balance_profile, decode_cpu_target
         self.resident_graphs = resident_graphs
         self.cache = ExpertCache(sizes, (len(hot_keys) + speculative_slots) * self.size, [self.size] * demand_slots,
                                  policy="LRU", initial_hotset=hot_keys)
@@ -178,6 +187,7 @@ class PDScopeCudaRuntime:
         if inputs.device != self.device or inputs.dtype != torch.bfloat16:
             raise ValueError("inputs must be bf16 on the runtime device")
         phase = "prefill" if step == 0 else "decode"
+        started = time.perf_counter()
         T, H = inputs.shape
         E, k = self.E, top_k
         x = inputs.contiguous()
@@ -192,7 +202,8 @@ class PDScopeCudaRuntime:
         # misses, at most k <= demand_slots of them, are staged in one batch
         # and the same graph is replayed once more over the completed table
         # (with fewer slots than k only a fully resident layer replays)
-        graph_path = (self.resident_graphs and phase == "decode" and bias is None
+        planned = self.costs is not None and self.cpu_backend is not None
+        graph_path = (self.resident_graphs and phase == "decode" and bias is None and not planned
                       and ops.decode_layer_supported(H, self.I, E, k, self.device)
                       and (k <= self.demand_slots or self._layer_fully_resident(layer)))
 
@@ -242,10 +253,31 @@ class PDScopeCudaRuntime:
             self.prediction_counts[phase]["total"] += len(prior)
         observed = dict(self.prediction_counts[phase])
 
-        # ---- plan: every expert on the GPU; resident first, misses through staging
+        # ---- plan: with a cost table and a CPU backend, plan_pdscope splits the
+        # experts between the CPU backend, resident copies and demand staging
+        # and picks the prefetch (pdscope_runtime.py:268-279); else every
+        # expert runs on the GPU, resident first, misses through staging
         views = {e: self.cache.lookup(key(e)) for e in counts}
-        resident = sorted((e for e in counts if views[e] is not None), key=lambda e: (-counts[e], e))
-        demand = sorted((e for e in counts if views[e] is None), key=lambda e: (-counts[e], e))
+        has_next = predict and (layer + 1) in self.layers
+        if planned:
+            hit_rate = observed["hits"] / observed["total"] if observed["total"] else 0.0
+            next_resident = [e for e in next_counts if self.cache.lookup(nkey(e)) is not None] if has_next else []
+            decision = plan_pdscope(counts, next_counts if has_next else {}, current_layer=layer, phase=phase,
+                                    current_gpu_ids=[e for e in counts if views[e] is not None],
+                                    next_gpu_ids=next_resident, costs=self.costs, attention_ms=attention_ms,
+                                    hit_rate=hit_rate, prefetch_slots=self.speculative_slots, top_k=k,
+                                    cpu_balance_target_override=self.decode_cpu_target if phase == "decode" else None,
+                                    record_checks=False, trusted=True,
+                                    compute_formula_target=self.decode_cpu_target is None,
+                                    num_experts=E, num_layers=max(self.layers) + 1)
+            cpu_list = list(decision["cpu_queue"])
+            resident = list(decision["gpu_resident_queue"])
+            demand = list(decision["on_demand_queue"])
+        else:
+            decision = None
+            cpu_list = []
+            resident = sorted((e for e in counts if views[e] is not None), key=lambda e: (-counts[e], e))
+            demand = sorted((e for e in counts if views[e] is None), key=lambda e: (-counts[e], e))
         for e in resident:
             if views[e].state == "loading":
                 self.executor.finish_load(views[e].ticket, wait=True)
@@ -267,9 +299,21 @@ class PDScopeCudaRuntime:
             missing = [e for e in experts if ex.table_entry(layer, e) == 0]
             if missing:
                 raise AssertionError(f"experts {missing} of layer {layer} have no ready device copy")
-        decode_fast = (T == 1 and not demand and not graph_path)
-        if T == 1 and demand and not graph_path:
+        decode_fast = (T == 1 and not demand and not cpu_list and not graph_path)
+        if T == 1 and (demand or cpu_list) and not graph_path:
             ops.pack(ids, E, out=packed, workspace=ws.pack_ws)  # decode misses take the grouped path
+        # ---- CPU experts start before the GPU launches (pdscope_runtime.py:300-336):
+        # each gets its routed rows in grouped order, and its output later fills
+        # the same rows of the grouped output, so the merge is unchanged
+        cpu_tasks = {}
+        if cpu_list:
+            x_host = x.cpu()
+            if T > 1:
+                offs = packed.offsets.cpu().tolist()
+                perm = packed.perm_token.cpu()
+            for e in cpu_list:
+                rows = x_host if T == 1 else x_host.index_select(0, perm[offs[e]:offs[e + 1]].long())
+                cpu_tasks[e] = ex.submit_cpu(key(e), rows.contiguous())
         if graph_path:
             if not demand:  # with misses the demand batch below replays over the completed table
                 if any(replay_table[e] == 0 for e in counts):
@@ -326,8 +370,9 @@ class PDScopeCudaRuntime:
         # ---- retire this layer's speculation, prefetch the next layer's forecast
         self._retire_current(layer, wait=True)
         issued, skipped = [], []
-        if predict and (layer + 1) in self.layers:
-            forecast = sorted(next_counts, key=lambda e: (-next_counts[e], e))
+        if has_next:
+            forecast = (list(decision["prefetch_queue"]) if planned
+                        else sorted(next_counts, key=lambda e: (-next_counts[e], e)))
             for e in forecast:
                 target = nkey(e)
                 if self.cache.lookup(target) is not None:
@@ -348,9 +393,15 @@ class PDScopeCudaRuntime:
             if issued:
                 self.forecasts[(request, step, layer + 1)] = tuple(issued)
 
-        # ---- finish GPU work, merge in token order
+        # ---- finish GPU work, place the CPU experts' rows, merge in token order
         for task in tasks:
             ex.finish_gpu(task, wait=True)
+        if cpu_tasks:
+            offs = packed.offsets.cpu().tolist() if T == 1 else offs
+            with torch.cuda.stream(ex.compute_stream):
+                for e, pending in cpu_tasks.items():
+                    rows = ex.finish_cpu(pending, wait=True)
+                    ws.y[offs[e] * H:offs[e + 1] * H].view(-1, H).copy_(rows)
         if not (decode_fast or graph_path):
             with torch.cuda.stream(ex.compute_stream):
                 ops.merge(ws.y, packed.row_of, weights, out)
@@ -369,15 +420,35 @@ class PDScopeCudaRuntime:
         if delta.get("cpu_completed_experts", 0) + delta.get("gpu_completed_experts", 0) != len(counts):
             raise AssertionError("lost or duplicated routed expert")
         routing = Routing(logits.clone(), ids.long(), weights.clone())
-        placements = {e: "gpu" for e in sorted(counts)}
-        decision = dict(phase=phase, mode="gpu_all", cpu_queue=[], gpu_resident_queue=resident,
-                        on_demand_queue=demand, prefetch_queue=issued, unload_queue=[], placements=placements)
-        row = dict(phase=phase, step=step, layer=layer, token_counts=counts, decision=decision,
-                   prefetch_issued=issued, prefetch_capacity_skipped=skipped, next_prediction_counts=next_counts,
-                   causal_hit_counts=observed, predictor="next_layer_gate_on_current_activation",
+        if decision is None:
+            decision = dict(phase=phase, mode="gpu_all", cpu_queue=[], gpu_resident_queue=resident,
+                            on_demand_queue=demand, prefetch_queue=issued, unload_queue=[],
+                            placements={e: "gpu" for e in sorted(counts)})
+        cpu_tokens = sum(counts[e] for e in cpu_list)
+        balance = (dict(cpu_experts=len(cpu_list), gpu_experts=len(counts) - len(cpu_list),
+                        cpu_token_assignments=cpu_tokens, gpu_token_assignments=sum(counts.values()) - cpu_tokens,
+                        host_ms=dict(layer_host_ms=(time.perf_counter() - started) * 1e3),
+                        timing_scope="host wall time of the layer call, completion waits included")
+                   if self.balance_profile else None)
+        digest = lambda t: hashlib.sha256(t.detach().cpu().contiguous().numpy().tobytes()).hexdigest()  # noqa: E731
+        row = dict(phase=phase, step=step, layer=layer, token_counts=counts, balance=balance,
+                   cpu_packing=False, cpu_batched_io=False, dispatch=self.dispatch,
+                   decode_submission="single_launch" if phase == "decode" and (decode_fast or graph_path)
+                   else "grouped_launch",
+                   decision=decision, prefetch_issued=issued, prefetch_capacity_skipped=skipped,
+                   next_prediction_counts=next_counts, causal_hit_counts=observed,
+                   predictor="next_layer_gate_on_current_activation",
+                   scheduler="cross_layer" if planned else "gpu_all", predictor_prior_hit_rate=0.0,
+                   selected_sha256=digest(routing.selected) if self.diagnostics else None,
+                   next_selected_sha256=digest(nids.long()) if self.diagnostics and predict else None,
                    ready_at_reveal=sum(o.ready_hit for o in observations),
                    loading_at_reveal=sum(o.state_at_reveal == "loading" for o in observations),
-                   counters=delta, ping_pong_slots=ping_pong, demand_slots=self.demand_slots,
+                   counters=delta, ping_pong_slots=ping_pong,
+                   static_retention="CPU placement keeps the charged device copy of a static hot expert",
+                   merge_mode=self.merge, input_pregather=self.input_pregather, demand_slots=self.demand_slots,
+                   graph_output_pool=self.graph_output_pool,
+                   pipeline="CPU queue on the backend beside the GPU launches; demand copies in staging-slot "
+                            "batches before next-layer speculation",
                    decode_path=("graph" if graph_path else "fused_gemv" if decode_fast else "grouped")
                    if phase == "decode" else "grouped",
                    measured_performance=False)
