@@ -54,6 +54,8 @@ def parse():
     ap.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, cpus) - 1")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 5 device copies of 1 GiB (calibrates the FETCH_SIZE / WRITE_SIZE counters)")
+    ap.add_argument("--calibrate-costs", metavar="PATH",
+                    help="only measure the per-expert cost table of the placement planner and write it to PATH")
     return ap.parse_args()
 
 
@@ -68,6 +70,100 @@ def calibrate_copy():
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"calibration": "device copy", "bytes_read": n, "bytes_written": n, "dispatches": 5}))
+
+
+def calibrate_costs(path, device, threads, reps=15, group=32, copies=40):
+    """Per-expert completion times by routed token count on this host, in the
+    FileCosts format (benchmarks/pdscope_compare.py:55-85; the loads of the
+    reference's costs/cost_table.json):
+      cpu_ms  one expert's n rows on the host's AVX2 stand-in CPU kernel
+              (oracle/cpu_moe_avx2.c, `threads` threads), its weights rotated
+              through `copies` host copies so DRAM serves them, median;
+      gpu_ms  one expert's share of a resident grouped launch: the gate/up and
+              down launches over `group` experts of n rows each, HIP events,
+              divided by `group` (the runtime launches its GPU experts together),
+              median;
+      h2d_ms  its 9 MiB gate|up|down block copied from pinned host memory into
+              an HBM slot (median) plus gpu_ms.
+    """
+    import numpy as np
+    import torch
+    from oracle import oracle as orc
+    from pdscope_amd import ops, synthetic
+    loads = (1, 4, 16, 64, 128, 256, 1024, 4096)
+    T = 4096
+    lay = synthetic.make_layer(H, I, E, K_TOP, True, seed=20261013, device=device)
+    x = synthetic.make_tokens(T, H, seed=20261014, device=device)
+    slots = ops.slot_table([lay.experts[e] for e in range(E)], device)
+    host = torch.empty((4, EXPERT_BYTES), dtype=torch.uint8, pin_memory=True)
+    host.copy_(lay.experts[:4].view(torch.uint8).reshape(4, -1).cpu())
+    slot = torch.empty(EXPERT_BYTES, dtype=torch.uint8, device=device)
+    rows_max = group * loads[-1]
+    h_ws = torch.empty(rows_max * I, dtype=torch.bfloat16, device=device)
+    y = torch.empty(rows_max * H, dtype=torch.bfloat16, device=device)
+    i32 = dict(dtype=torch.int32, device=device)
+    sel_all = torch.arange(E, **i32)
+    tile_start = torch.empty(E + 1, **i32)
+    order = torch.empty(E, **i32)
+    stream = torch.cuda.current_stream(device)
+    copy_ms = []
+    for r in range(reps + 2):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        slot.copy_(host[r % 4], non_blocking=True)
+        b.record(stream)
+        torch.cuda.synchronize(device)
+        if r >= 2:
+            copy_ms.append(a.elapsed_time(b))
+    copy_med = statistics.median(copy_ms)
+    experts_host = u16(lay.experts[:4])
+    pool = [np.ascontiguousarray(experts_host[i % 4]) for i in range(copies)]
+    x_host = u16(x)
+    points = {}
+    for n in loads:
+        counts = torch.zeros(E, **i32)
+        counts[:group] = n
+        offsets = torch.zeros(E + 1, **i32)
+        offsets[1:] = torch.cumsum(counts, 0)
+        perm = torch.arange(group * n, **i32) % T
+        bm = ops.grouped_block_m(n, n)
+        ops.schedule(counts, sel_all, bm, out=tile_start, order=order)
+        max_tiles = group * ((n + bm - 1) // bm)
+        gpu = []
+        for r in range(reps + 2):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            ops.swiglu_grouped(x, perm, offsets, order, tile_start, max_tiles, bm, slots, H, I, h_ws, y)
+            b.record(stream)
+            torch.cuda.synchronize(device)
+            if r >= 2:
+                gpu.append(a.elapsed_time(b) / group)
+        rows = np.ascontiguousarray(x_host[np.arange(n) % T])
+        sel = np.zeros(n, np.int64)
+        coeff = np.ones(n, np.float32)
+        cpu = []
+        for r in range(2 + (5 if n >= 1024 else 9)):
+            ptrs = [pool[r % copies].ctypes.data] * 4
+            t0 = time.perf_counter()
+            orc.cpu_moe_rows(rows, sel, coeff, ptrs, H, I, threads)
+            if r >= 2:
+                cpu.append((time.perf_counter() - t0) * 1e3)
+        g = statistics.median(gpu)
+        points[str(n)] = dict(cpu_ms=statistics.median(cpu), gpu_ms=g, h2d_ms=copy_med + g)
+        log(f"[costs] n={n}: {points[str(n)]}")
+    table = dict(schema_version=1, kind="pdscope_cost_table",
+                 model="Qwen3-30B-A3B-shaped expert (H 2048, I 768), bf16",
+                 platform=f"AMD Instinct MI355X + {cpu_model()}",
+                 native_operator="AVX2 bf16 SwiGLU stand-in kernel (oracle/cpu_moe_avx2.c)", workers=threads,
+                 loads=list(loads), points=points,
+                 scope=f"per-expert completion time by routed token count: CPU stand-in path (weights from DRAM), "
+                       f"one expert's share of a grouped launch over {group} resident experts, and pinned H2D copy "
+                       f"({copy_med:.3f} ms per 9 MiB) plus that share; measured by bench.py --calibrate-costs. "
+                       f"Recalibrate per machine.")
+    with open(path, "w") as f:
+        json.dump(table, f, indent=2)
+        f.write("\n")
+    print(json.dumps(dict(calibration="costs", path=path, loads=list(loads))))
 
 
 def traffic_from_profiles(name):
@@ -637,6 +733,9 @@ def main():
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
     threads = cpu_threads(args.cpu_threads)
+    if args.calibrate_costs:
+        calibrate_costs(args.calibrate_costs, device, threads)
+        return
 
     plan = {"prefill512": ("prefill", 512, 4), "decode": ("decode", 1, 16), "prefill4096": ("prefill", 4096, 2),
             "prefill4096_zipf": ("zipf", 4096, 2), "dsv2_mixed": ("dsv2", 1304, 4), "stack48": ("stack", 2048, 48)}

@@ -232,3 +232,16 @@ def test_file_costs_rejects_bad_tables(tmp_path):
         FileCosts(_table(tmp_path, pts, kind="other"))
     with pytest.raises(ValueError):
         FileCosts(_table(tmp_path, {n: p for n, p in pts.items() if n != 4096}))
+
+
+def test_shipped_mi355x_cost_table():
+    """The table measured on MI355X loads, covers the measured domain and
+    interpolates linearly between its points."""
+    from pdscope_amd.costs import mi355x_costs
+    c = mi355x_costs()
+    assert c.loads == [1, 4, 16, 64, 128, 256, 1024, 4096]
+    lo, hi = c.for_load(64), c.for_load(128)
+    mid = c.for_load(96)
+    for k in ("cpu_ms", "gpu_ms", "h2d_ms"):
+        assert lo[k] > 0 and abs(mid[k] - (lo[k] + hi[k]) / 2) <= 1e-12 * max(1.0, hi[k])
+    assert c.for_load(4096)["cpu_ms"] > c.for_load(1)["cpu_ms"]
