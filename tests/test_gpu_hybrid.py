@@ -36,6 +36,16 @@ class OracleCpuBackend:
         return torch.from_numpy(y.view(np.int16)).view(torch.bfloat16)
 
 
+# the keys of the reference's per-layer trace row (expertbench/pdscope_runtime.py:492-512)
+REFERENCE_ROW_KEYS = {
+    "phase", "step", "layer", "token_counts", "balance", "cpu_packing", "cpu_batched_io", "dispatch",
+    "decode_submission", "decision", "prefetch_issued", "prefetch_capacity_skipped", "next_prediction_counts",
+    "causal_hit_counts", "predictor", "scheduler", "predictor_prior_hit_rate", "selected_sha256",
+    "next_selected_sha256", "ready_at_reveal", "loading_at_reveal", "counters", "ping_pong_slots",
+    "static_retention", "merge_mode", "input_pregather", "demand_slots", "graph_output_pool", "pipeline",
+    "measured_performance"}
+
+
 def cost_table(tmp_path, cpu_ms_per_row, gpu_ms=0.2, h2d_ms=0.5):
     points = {str(n): dict(cpu_ms=cpu_ms_per_row * n, gpu_ms=gpu_ms, h2d_ms=h2d_ms)
               for n in (1, 4, 16, 64, 128, 256, 1024, 4096)}
@@ -75,6 +85,8 @@ def test_runtime_places_experts_on_the_cpu_backend(orc, tmp_path):
                 assert row["counters"]["cpu_completed_experts"] + row["counters"]["gpu_completed_experts"] == \
                     len(row["token_counts"])
                 cpu_total += len(d["cpu_queue"])
+                assert REFERENCE_ROW_KEYS <= set(row), REFERENCE_ROW_KEYS - set(row)
+                assert row["selected_sha256"] is not None and row["balance"] is None
         assert cpu_total > 0 and backend.calls == cpu_total
         closure(rt)
     finally:
