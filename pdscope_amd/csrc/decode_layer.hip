@@ -82,6 +82,42 @@ __device__ __forceinline__ bool pair_ready(uint64_t v, uint32_t epoch) {
     return ((uint32_t)v >> 16) == epoch && (uint32_t)(v >> 48) == epoch;
 }
 
+// Poll the word pair at w until both words carry `epoch`, keeping four
+// polls in flight: the oldest is checked when it returns and re-issued at
+// once, so the pair is seen about a quarter of a round trip after it became
+// visible instead of up to a whole one.  The four loads live in fixed
+// registers and the loop is uniform over the active lanes (a lane latches
+// its value when ready; the loop ends when every active lane has one), so
+// the compiler's wait analysis keeps three newer polls in flight at each
+// check.  Loads left in flight on return are harmless (later waits cover
+// them).  Every round spends one unit of budget; when it runs out the
+// sticky error word is set (a lane without a current value then returns 0).
+__device__ __forceinline__ uint64_t poll_pair(const uint32_t *w, uint32_t epoch, uint32_t *err, uint32_t &budget) {
+    uint64_t p0 = load_pair(w), p1 = load_pair(w), p2 = load_pair(w), p3 = load_pair(w);
+    uint64_t got = 0;
+    bool have = false;
+    for (;;) {
+#define PD_POLL_STEP(P)                              \
+        {                                            \
+            const bool r = !have && pair_ready(P, epoch); \
+            got = r ? P : got;                       \
+            have = have || r;                        \
+        }                                            \
+        if (__ballot(!have) == 0) return got;        \
+        P = load_pair(w);
+        PD_POLL_STEP(p0)
+        PD_POLL_STEP(p1)
+        PD_POLL_STEP(p2)
+        PD_POLL_STEP(p3)
+#undef PD_POLL_STEP
+        if (budget == 0) {
+            __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return got;
+        }
+        --budget;
+    }
+}
+
 // Collect `count` published words starting at w (count even, w 8-byte
 // aligned) into dst (LDS, 16-bit values), cooperatively: thread t takes the
 // word pairs t, t + nthreads, ...  B pair loads are issued together, then
@@ -102,15 +138,7 @@ __device__ __forceinline__ void collect(const uint32_t *w, int count, int t, int
         for (int b = 0; b < B; ++b) {
             const int j = j0 + b * nthreads;
             if (j >= pairs) continue;
-            while (!pair_ready(v[b], epoch)) {
-                if (budget == 0) {
-                    __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    break;
-                }
-                --budget;
-                __builtin_amdgcn_s_sleep(1);
-                v[b] = load_pair(w + 2 * j);
-            }
+            if (!pair_ready(v[b], epoch)) v[b] = poll_pair(w + 2 * j, epoch, err, budget);
             dst[2 * j] = (uint16_t)v[b];
             dst[2 * j + 1] = (uint16_t)(v[b] >> 32);
         }
@@ -192,16 +220,7 @@ __global__ __launch_bounds__(256, 2) void decode_layer_kernel(
     if (wave == 0) {
         for (int j = lane; j < 2 * RB; j += 64) {
             const uint32_t *w = ws + kWsLogit + (j >> 1) * 32 + (j & 1) * 2;
-            uint64_t v = load_pair(w);
-            while (!pair_ready(v, epoch)) {
-                if (budget == 0) {
-                    __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    break;
-                }
-                --budget;
-                __builtin_amdgcn_s_sleep(1);
-                v = load_pair(w);
-            }
+            const uint64_t v = poll_pair(w, epoch, err, budget);
             if (2 * j < E) s_logit[2 * j] = bf2f((uint32_t)v & 0xffffu);
             if (2 * j + 1 < E) s_logit[2 * j + 1] = bf2f((uint32_t)(v >> 32) & 0xffffu);
         }

@@ -187,6 +187,7 @@ class ExpertExecutor:
         self._group_stream_ctx = None
         self._cpu_pool = None
         self._cpu_tasks = {}  # key -> PendingCpu
+        self._landed = {}     # ticket -> completed load event not yet waited on by a consumer
 
     # ------------------------------------------------------------ sources
 
@@ -294,6 +295,9 @@ class ExpertExecutor:
             if ticket in self.loads:
                 raise RuntimeError("the ledger retired a copy with a transfer in flight")
             flat = self.copies.pop(ticket, None)
+            ev = self._landed.pop(ticket, None)
+            if ev is not None:
+                self._free_events.append(ev)
             slot = self._cache_slot_of.pop(ticket, None)
             if slot is not None:
                 self._free_cache_slots.append(slot)
@@ -335,7 +339,9 @@ class ExpertExecutor:
             return False
         self.cache.complete_load(ticket)
         del self.loads[ticket]
-        self._free_events.append(ev)
+        # kept until the copy's first consumer is launched, which waits on it
+        # on the compute stream (gpu_group)
+        self._landed[ticket] = ev
         self._set_entry(ticket.key, self.copies[ticket].data_ptr())
         self._log(event="load_completed", generation=ticket.generation)
         return True
@@ -367,6 +373,15 @@ class ExpertExecutor:
             if not span:
                 self.compute_stream.wait_stream(torch.cuda.current_stream(self.device)
                                                 if wait_for is None else wait_for)
+            # order each copy's transfer (load stream) before its first consumer
+            # on the device as well: the host already saw the transfer complete,
+            # so the wait costs nothing, and the dependency is explicit to the
+            # runtime, which applies its cache visibility rules to it
+            for h in handles:
+                ev = self._landed.pop(h.ticket, None)
+                if ev is not None:
+                    self.compute_stream.wait_event(ev)
+                    self._free_events.append(ev)
             output = launch()
             ev = self._event()
             ev.record(self.compute_stream)
@@ -468,6 +483,7 @@ class ExpertExecutor:
             self.compute_stream.synchronize()
             self.copies.clear()
             self.loads.clear()
+            self._landed.clear()
             self.computes.clear()
             self.staging.clear()
             self.pinned.clear()

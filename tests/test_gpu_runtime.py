@@ -27,12 +27,28 @@ def build(n_layers, H, I, E, k, seed=77):
     return layers, masters
 
 
-def check_output(orc, out, routing, x, layer_obj, H, I, k, normalize=True):
+def check_output(orc, out, routing, x, layer_obj, H, I, k, normalize=True, row=None):
     ids = routing.selected.cpu().numpy()
     oi, ow = orc.route_from_logits(u16(routing.logits), k, normalize)
     assert np.array_equal(ids, oi) and np.array_equal(u16(routing.weights), ow)
     ref, _, _ = oracle_layer_given_routing(orc, u16(x), ids, u16(routing.weights), u16(layer_obj.experts), H, I)
-    assert_layer_close(orc, out, ref)
+    try:
+        assert_layer_close(orc, out, ref)
+    except AssertionError as err:
+        # name the experts behind the mismatch: those routed by every badly
+        # matching token, with where the runtime placed them
+        d = np.abs(orc.bf16_to_f32(u16(out)).astype(np.float64) - orc.bf16_to_f32(ref))
+        bad = np.nonzero(d.max(axis=1) > 0.1 * np.abs(orc.bf16_to_f32(ref)).max())[0]
+        common = set(ids[bad[0]]) if len(bad) else set()
+        for t in bad[1:]:
+            common &= set(ids[t])
+        where = {}
+        if row is not None:
+            dec = row["decision"]
+            where = {e: ("resident" if e in dec["gpu_resident_queue"] else "staged" if e in dec["on_demand_queue"]
+                         else "cpu") for e in common}
+        raise AssertionError(f"{err}; {len(bad)} tokens off, experts common to all of them: {sorted(common)} "
+                             f"{where}") from None
 
 
 def closure(rt):
@@ -83,7 +99,7 @@ def test_runtime_qwen_demand_staging_eight_slots(orc):
         x = synthetic.make_tokens(64, q["H"], seed=92)
         out, routing, row = rt.forward(x, layers[0].gate, layer=0, step=0, top_k=8)
         torch.cuda.synchronize()
-        check_output(orc, out, routing, x, layers[0], q["H"], q["I"], 8)
+        check_output(orc, out, routing, x, layers[0], q["H"], q["I"], 8, row=row)
         assert len(row["decision"]["on_demand_queue"]) > 50
         assert {p["slot"] for p in row["ping_pong_slots"]} <= set(range(8))
         closure(rt)
