@@ -107,6 +107,30 @@ def test_runtime_qwen_demand_staging_eight_slots(orc):
         rt.close()
 
 
+def test_runtime_staging_slots_reused_across_calls(orc):
+    """Successive prefill calls stage different experts through the same eight
+    slots (each slot's previous contents were other weights, read by earlier
+    launches): every call matches the oracle."""
+    from pdscope_amd import synthetic
+    from pdscope_amd.cache import ExpertKey
+    from pdscope_amd.pdscope_runtime import PDScopeCudaRuntime
+    q = synthetic.QWEN
+    layers, masters = build(2, q["H"], q["I"], q["E"], q["k"], seed=95)
+    hot = [ExpertKey(l, e, "bf16") for l in range(2) for e in range(16)]
+    rt = PDScopeCudaRuntime(masters, hot_keys=hot, speculative_slots=0, demand_slots=8)
+    try:
+        for call in range(4):
+            l = call % 2
+            x = synthetic.make_tokens(48 + 16 * call, q["H"], seed=96 + call)
+            out, routing, row = rt.forward(x, layers[l].gate, layer=l, step=0, top_k=8, request=f"r{call}")
+            torch.cuda.synchronize()
+            check_output(orc, out, routing, x, layers[l], q["H"], q["I"], 8, row=row)
+            assert len(row["decision"]["on_demand_queue"]) > 40
+        closure(rt)
+    finally:
+        rt.close()
+
+
 def test_runtime_decode_graph_matches_eager(orc):
     from pdscope_amd import layer, ops, synthetic
     from pdscope_amd.cache import ExpertKey
