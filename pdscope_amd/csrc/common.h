@@ -97,16 +97,25 @@ __device__ __forceinline__ float dot8(const uint4 a, const uint4 b, float acc) {
 
 // ---------------------------------------------------------------- wave ops
 
+// Sum over the wave by an xor butterfly, offsets 32, 16, 8, 4, 2, 1: each
+// step adds lane a's value and lane a^d's, so after it the lanes that differ
+// only in the bits already reduced hold identical values, and every lane
+// ends with the same total.  The steps run without LDS: v_permlane32_swap /
+// v_permlane16_swap hand each lane the value of lane a^32 / a^16 (in the
+// one or the other output register, whose per-lane sum is then v_a +
+// v_(a^d) in some operand order; fp32 addition commutes), and row_ror 8, 4,
+// 2, 1 read a lane of the same 16-lane row that differs from a^d only in
+// bits whose lanes already agree.  The result is bit-identical to the
+// shuffle butterfly v += shfl_xor(v, d).
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
-    return v;
-}
-
-// sum inside each 32-lane half (offsets 16..1)
-__device__ __forceinline__ float half_sum(float v) {
-#pragma unroll
-    for (int off = 16; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+    auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+    v = v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xf, 0xf, true));  // row_ror:8
+    v = v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x124, 0xf, 0xf, true));  // row_ror:4
+    v = v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x122, 0xf, 0xf, true));  // row_ror:2
+    v = v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x121, 0xf, 0xf, true));  // row_ror:1
     return v;
 }
 
@@ -135,23 +144,6 @@ __device__ __forceinline__ float half_sum_dpp(float v) {
 __device__ __forceinline__ float wave_sum_dpp(float v) {
     v = dpp_add<0x143, 0xc>(half_sum_dpp(v));  // row_bcast:31 into rows 2, 3
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
-    return v;
-}
-
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        uint32_t lo = __shfl_xor((uint32_t)v, off, kWave);
-        uint32_t hi = __shfl_xor((uint32_t)(v >> 32), off, kWave);
-        uint64_t o = ((uint64_t)hi << 32) | lo;
-        v = o > v ? o : v;
-    }
-    return v;
 }
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }

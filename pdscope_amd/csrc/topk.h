@@ -24,31 +24,26 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 // Wave-wide max through DPP (no LDS round trips): row_shr 1/2/4/8 leave
 // each row's max in its lane 15, row_bcast 15/31 carry it to lane 63, which
-// is read back as a uniform value.  Lanes without a DPP source keep their
-// own value (bound_ctrl off), so max is taken over real values only.
+// is read back as a uniform value.  Lanes without a DPP source read the
+// identity of max (INT_MIN), so each step is one v_max_i32 with a DPP operand.
 __device__ __forceinline__ int dpp_max_i32(int v) {
-    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x111, 0xf, 0xf, false));  // row_shr:1
-    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x112, 0xf, 0xf, false));  // row_shr:2
-    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x114, 0xf, 0xf, false));  // row_shr:4
-    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x118, 0xf, 0xf, false));  // row_shr:8
-    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x142, 0xa, 0xf, false));  // row_bcast:15
-    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x143, 0xc, 0xf, false));  // row_bcast:31
+    constexpr int kId = (int)0x80000000;
+    v = max(v, __builtin_amdgcn_update_dpp(kId, v, 0x111, 0xf, 0xf, false));  // row_shr:1
+    v = max(v, __builtin_amdgcn_update_dpp(kId, v, 0x112, 0xf, 0xf, false));  // row_shr:2
+    v = max(v, __builtin_amdgcn_update_dpp(kId, v, 0x114, 0xf, 0xf, false));  // row_shr:4
+    v = max(v, __builtin_amdgcn_update_dpp(kId, v, 0x118, 0xf, 0xf, false));  // row_shr:8
+    v = max(v, __builtin_amdgcn_update_dpp(kId, v, 0x142, 0xa, 0xf, false));  // row_bcast:15
+    v = max(v, __builtin_amdgcn_update_dpp(kId, v, 0x143, 0xc, 0xf, false));  // row_bcast:31
     return __builtin_amdgcn_readlane(v, 63);
 }
 
+// Wave-wide max of fp32 values that are not NaN, through dpp_max_i32 on an
+// order-preserving integer image of the bits (negative values have their
+// magnitude bits flipped).  Among equal maxima +0 beats -0.
 __device__ __forceinline__ float dpp_max_f32(float f) {
-    int v = __float_as_int(f);
-#define PD_FMAX_STEP(ctrl, rmask)                                                                          \
-    v = __float_as_int(                                                                                    \
-        fmaxf(__int_as_float(v), __int_as_float(__builtin_amdgcn_update_dpp(v, v, ctrl, rmask, 0xf, false))))
-    PD_FMAX_STEP(0x111, 0xf);
-    PD_FMAX_STEP(0x112, 0xf);
-    PD_FMAX_STEP(0x114, 0xf);
-    PD_FMAX_STEP(0x118, 0xf);
-    PD_FMAX_STEP(0x142, 0xa);
-    PD_FMAX_STEP(0x143, 0xc);
-#undef PD_FMAX_STEP
-    return __int_as_float(__builtin_amdgcn_readlane(v, 63));
+    const int b = __float_as_int(f);
+    const int m = dpp_max_i32(b ^ ((b >> 31) & 0x7fffffff));
+    return __int_as_float(m ^ ((m >> 31) & 0x7fffffff));
 }
 
 // Softmax of one token's logits by one wave.  lrow: E logits of the token

@@ -111,6 +111,23 @@ def test_route_tie_heavy(orc, pd, T):
     assert (srt[:, 7] == srt[:, 8]).any()
 
 
+@pytest.mark.parametrize("T", [1, 64])
+def test_route_probability_collisions(orc, pd, T):
+    """Distinct logits whose probabilities underflow to the same value (0):
+    three experts carry the mass, the other five of the top 8 are chosen
+    among equal probabilities by lower id, while the logits rank those
+    experts the other way (higher ids have the larger logits)."""
+    ops, _, _ = pd
+    gen = torch.Generator(device=DEV).manual_seed(13)
+    E, H = 128, 256
+    scale = -1.0 - (E - 1 - torch.arange(E, device=DEV, dtype=torch.float32)) * 0.01
+    scale[[100, 50, 7]] = torch.tensor([0.01, 0.005, 0.0], device=DEV)
+    gate = scale[:, None].expand(E, H).to(torch.bfloat16).contiguous()
+    x = (torch.rand((T, H), generator=gen, device=DEV) + 0.5).to(torch.bfloat16)
+    _, ik, _ = _route_check(orc, ops, x, gate, 8, True)
+    assert (ik[:, :3] == [100, 50, 7]).all() and (ik[:, 3:] == [0, 1, 2, 3, 4]).all()
+
+
 def test_route_hist(orc, pd):
     ops, _, _ = pd
     ids = torch.randint(0, 128, (4096, 8), device=DEV, dtype=torch.int32)
