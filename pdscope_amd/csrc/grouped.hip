@@ -121,6 +121,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void grouped_kernel(
     constexpr int TM = BM / WM, TN = BN / WN;  // wave tile
     constexpr int MB = TM / 32, NB = TN / 32;  // 32x32 MFMA blocks per wave
     static_assert(MB >= 1 && NB >= 1 && (!GATEUP || NB % 2 == 0), "wave tiling");
+    static_assert(MB <= 4, "the live row-block dispatch below covers up to 4 row blocks per wave");
     typedef Geo<BK> G;
     constexpr int NWA = SPLIT ? NW / 2 : NW, NWB = SPLIT ? NW / 2 : NW;  // waves loading A / B
     constexpr int AL = BM / G::RPI / NWA, BL = BN / G::RPI / NWB;  // 1 KB loads per loading wave per stage
