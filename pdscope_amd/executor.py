@@ -188,6 +188,9 @@ class ExpertExecutor:
         self._cpu_pool = None
         self._cpu_tasks = {}  # key -> PendingCpu
         self._landed = {}     # ticket -> completed load event not yet waited on by a consumer
+        # optional check hook: consume_hook(key, flat) runs on the compute
+        # stream right before each grouped launch, once per device copy it reads
+        self.consume_hook = None
 
     # ------------------------------------------------------------ sources
 
@@ -244,7 +247,11 @@ class ExpertExecutor:
         host = self._host_table(layer, E)
         dev = self._dev_tables.get(layer)
         if dev is None:
+            # the zero fill runs on the current stream while uploads and
+            # launches use other streams: let it finish before any of them
+            # can write or read the table
             dev = torch.zeros(E, dtype=torch.int64, device=self.device)
+            torch.cuda.current_stream(self.device).synchronize()
             self._dev_tables[layer] = dev
         return dev, host
 
@@ -276,8 +283,10 @@ class ExpertExecutor:
         i, buf = self._ring.take()
         view = buf[:4 * n].view(torch.int32)
         view.copy_(torch.tensor(values, dtype=torch.int32))
-        dev = torch.empty(n, dtype=torch.int32, device=self.device)
         with torch.cuda.stream(stream):
+            # allocated on the stream that writes and reads it, so the caching
+            # allocator reuses its block only in that stream's order
+            dev = torch.empty(n, dtype=torch.int32, device=self.device)
             dev.copy_(view, non_blocking=True)
         self._ring.mark(i, stream)
         return dev
@@ -382,6 +391,9 @@ class ExpertExecutor:
                 if ev is not None:
                     self.compute_stream.wait_event(ev)
                     self._free_events.append(ev)
+            if self.consume_hook is not None:
+                for h in handles:
+                    self.consume_hook(h.ticket.key, self.copies[h.ticket])
             output = launch()
             ev = self._event()
             ev.record(self.compute_stream)

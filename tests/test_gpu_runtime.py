@@ -42,13 +42,72 @@ def check_output(orc, out, routing, x, layer_obj, H, I, k, normalize=True, row=N
         common = set(ids[bad[0]]) if len(bad) else set()
         for t in bad[1:]:
             common &= set(ids[t])
+        # experts every one of whose tokens is off (the likely culprits)
+        badset = set(bad.tolist())
+        suspects = sorted(e for e in set(ids.reshape(-1).tolist())
+                          if all(t in badset for t in np.nonzero((ids == e).any(axis=1))[0]))
         where = {}
         if row is not None:
             dec = row["decision"]
-            where = {e: ("resident" if e in dec["gpu_resident_queue"] else "staged" if e in dec["on_demand_queue"]
-                         else "cpu") for e in common}
-        raise AssertionError(f"{err}; {len(bad)} tokens off, experts common to all of them: {sorted(common)} "
-                             f"{where}") from None
+            demand = list(dec["on_demand_queue"])
+
+            def place(e):
+                if e in dec["gpu_resident_queue"]:
+                    return "resident"
+                return f"staged#{demand.index(e)}" if e in demand else "cpu"
+            where = {e: place(e) for e in sorted(common | set(suspects))}
+        raise AssertionError(f"{err}; {len(bad)} of {ids.shape[0]} tokens off, experts common to all of them: "
+                             f"{sorted(common)}, experts with all their tokens off: {suspects}; placement {where}"
+                             ) from None
+
+
+def watch_copies(rt, layers):
+    """Compare every device copy with its layer's weights on the compute
+    stream right before the launch that reads it (no host sync); returns the
+    list of (key, mismatch flag tensor) to check after synchronising."""
+    records = []
+
+    def hook(key, flat):
+        w = layers[key.layer].experts[key.expert]
+        got = flat[:w.numel() * 2].view(torch.int16)
+        records.append((key, (got != w.view(torch.int16)).any()))
+    rt.executor.consume_hook = hook
+    return records
+
+
+def assert_copies_intact(records):
+    bad = [(k.layer, k.expert) for k, m in records if bool(m)]
+    records.clear()
+    assert not bad, f"device copies differ from their masters when consumed: {bad}"
+
+
+def explain_rows(orc, rt, x, layer_obj, layer, ids, H, I, k):
+    """After a mismatch: which experts' grouped output rows (ws.y) differ
+    from the oracle's expert outputs, whether the device grouping equals the
+    oracle's, and the device/host slot-table entries of those experts."""
+    ws = rt._ws[k]
+    T = x.shape[0]
+    p = orc.pack(np.ascontiguousarray(ids, dtype=np.int32), layer_obj.E)
+    offs = ws.offsets.cpu().numpy()
+    perm = ws.perm_token[:T * k].cpu().numpy()
+    same_pack = bool(np.array_equal(offs, p["offsets"]) and np.array_equal(perm, p["perm_token"]))
+    y = u16(ws.y[:T * k * H].view(T * k, H))
+    xg = u16(x)[p["perm_token"]]
+    experts = u16(layer_obj.experts)
+    IH = I * H
+    wrong = []
+    for e in np.nonzero(p["counts"])[0]:
+        a, b = p["offsets"][e], p["offsets"][e + 1]
+        blk = experts[e]
+        ref = orc.expert_forward(xg[a:b], blk[:IH].reshape(I, H), blk[IH:2 * IH].reshape(I, H),
+                                 blk[2 * IH:].reshape(H, I))
+        d = np.abs(orc.bf16_to_f32(y[a:b]).astype(np.float64) - orc.bf16_to_f32(ref))
+        if d.max() > 0.1 * np.abs(orc.bf16_to_f32(ref)).max():
+            wrong.append(int(e))
+    dev_tab, host_tab = rt.executor.table(layer, layer_obj.E)
+    dev_tab = dev_tab.cpu().tolist()
+    tabs = {e: (hex(dev_tab[e]), hex(host_tab[e])) for e in wrong[:6]}
+    return f"grouping equals the oracle's: {same_pack}; experts with wrong y rows: {wrong}; tables {tabs}"
 
 
 def closure(rt):
@@ -95,10 +154,12 @@ def test_runtime_qwen_demand_staging_eight_slots(orc):
     layers, masters = build(1, q["H"], q["I"], q["E"], q["k"], seed=91)
     hot = [ExpertKey(0, e, "bf16") for e in range(32)]
     rt = PDScopeCudaRuntime(masters, hot_keys=hot, speculative_slots=0, demand_slots=8)
+    copies = watch_copies(rt, layers)
     try:
         x = synthetic.make_tokens(64, q["H"], seed=92)
         out, routing, row = rt.forward(x, layers[0].gate, layer=0, step=0, top_k=8)
         torch.cuda.synchronize()
+        assert_copies_intact(copies)
         check_output(orc, out, routing, x, layers[0], q["H"], q["I"], 8, row=row)
         assert len(row["decision"]["on_demand_queue"]) > 50
         assert {p["slot"] for p in row["ping_pong_slots"]} <= set(range(8))
@@ -118,13 +179,19 @@ def test_runtime_staging_slots_reused_across_calls(orc):
     layers, masters = build(2, q["H"], q["I"], q["E"], q["k"], seed=95)
     hot = [ExpertKey(l, e, "bf16") for l in range(2) for e in range(16)]
     rt = PDScopeCudaRuntime(masters, hot_keys=hot, speculative_slots=0, demand_slots=8)
+    copies = watch_copies(rt, layers)
     try:
         for call in range(4):
             l = call % 2
             x = synthetic.make_tokens(48 + 16 * call, q["H"], seed=96 + call)
             out, routing, row = rt.forward(x, layers[l].gate, layer=l, step=0, top_k=8, request=f"r{call}")
             torch.cuda.synchronize()
-            check_output(orc, out, routing, x, layers[l], q["H"], q["I"], 8, row=row)
+            assert_copies_intact(copies)
+            try:
+                check_output(orc, out, routing, x, layers[l], q["H"], q["I"], 8, row=row)
+            except AssertionError as err:
+                why = explain_rows(orc, rt, x, layers[l], l, routing.selected.cpu().numpy(), q["H"], q["I"], 8)
+                raise AssertionError(f"call {call}: {err}; {why}") from None
             assert len(row["decision"]["on_demand_queue"]) > 40
         closure(rt)
     finally:
