@@ -198,6 +198,31 @@ def test_runtime_staging_slots_reused_across_calls(orc):
         rt.close()
 
 
+def test_slot_table_fill_is_ordered_before_uploads_on_other_streams():
+    """The device slot table is created by a zero fill on the caller's
+    stream; its first upload runs on the compute stream.  With the caller's
+    stream busy (a timed spin kernel ahead of the fill), the upload must
+    still be what the table holds afterwards."""
+    from pdscope_amd.cache import ExpertKey
+    from pdscope_amd.pdscope_runtime import PDScopeCudaRuntime
+    H, I, E, k = 256, 128, 32, 4
+    layers, masters = build(2, H, I, E, k, seed=81)
+    rt = PDScopeCudaRuntime(masters, hot_keys=[ExpertKey(1, e, "bf16") for e in range(4)], speculative_slots=0)
+    try:
+        ex = rt.executor
+        torch.cuda.synchronize()
+        assert 1 not in ex._dev_tables
+        torch.cuda._sleep(20_000_000)  # about 10 ms on the caller's stream
+        dev = ex.upload_table(1, E, ex.compute_stream)
+        ex.compute_stream.synchronize()
+        torch.cuda.synchronize()
+        host = ex.table(1, E)[1]
+        assert all(host[e] != 0 for e in range(4))
+        assert dev.cpu().tolist() == list(host)
+    finally:
+        rt.close()
+
+
 def test_runtime_decode_graph_matches_eager(orc):
     from pdscope_amd import layer, ops, synthetic
     from pdscope_amd.cache import ExpertKey
