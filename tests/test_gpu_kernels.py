@@ -218,6 +218,49 @@ def test_layer_prefill_qwen(orc, pd, qwen, qwen_host, T):
     assert m["max_rel"] <= MAX_REL and m["mean_abs"] <= MEAN_ABS, m
 
 
+def test_layer_prefill_qwen_t4096_sampled_tokens(orc, pd, qwen, qwen_host):
+    """The full T=4096 layer (the 384-row tile the workload uses, all 128
+    experts, every tile boundary) checked on a seeded sample of tokens: for
+    each sampled token its k grouped rows (ws.y, located through the device
+    row map) against the oracle's expert outputs for that token, and its
+    merged output against the oracle merge of those rows.  The grouping
+    itself is checked bit-exact in full."""
+    ops, layer, synthetic = pd
+    T, H, I, k = 4096, 2048, 768, 8
+    x = synthetic.make_tokens(T, H, seed=4096)
+    ws = layer.MoEWorkspace(T, H, I, 128, k, DEV)
+    slots = ops.slot_table([qwen.experts[e] for e in range(128)], DEV)
+    out, logits, ids, w = layer.moe_forward(x, qwen.gate, slots, ws)
+    torch.cuda.synchronize()
+    assert ops.grouped_block_m(T * k // 128, int(ws.counts.max())) == 384
+    ik, wk, xu = ids.cpu().numpy(), u16(w), u16(x)
+    oi, ow = orc.route_from_logits(u16(logits), k, True)
+    assert np.array_equal(ik, oi) and np.array_equal(wk, ow)
+    p = orc.pack(np.ascontiguousarray(ik, dtype=np.int32), 128)
+    assert np.array_equal(ws.row_of[:T * k].cpu().numpy(), p["row_of"])
+    rng = np.random.default_rng(4096)
+    tokens = np.sort(rng.choice(T, 40, replace=False))
+    tokens[0], tokens[-1] = 0, T - 1
+    IH = I * H
+    y_all = u16(ws.y[:T * k * H]).reshape(T * k, H)
+    row_of = p["row_of"].reshape(T, k)
+    got_y, ref_y = [], []
+    for t in tokens:
+        for s in range(k):
+            blk = qwen_host["experts"][ik[t, s]]
+            ref_y.append(orc.expert_forward(xu[t:t + 1], blk[:IH].reshape(I, H), blk[IH:2 * IH].reshape(I, H),
+                                            blk[2 * IH:].reshape(H, I))[0])
+            got_y.append(y_all[row_of[t, s]])
+    got_y, ref_y = np.stack(got_y), np.stack(ref_y)
+    m_y = err_metrics(orc.bf16_to_f32(got_y), orc.bf16_to_f32(ref_y))
+    assert m_y["max_rel"] <= MAX_REL and m_y["mean_abs"] <= MEAN_ABS, m_y
+    # merge of the sampled tokens' device rows, in slot order
+    local_row_of = np.arange(len(tokens) * k, dtype=np.int32).reshape(len(tokens), k)
+    ref_out = orc.merge(got_y, local_row_of, wk[tokens])
+    d = ulp_diff_bf16(u16(out)[tokens], ref_out)
+    assert (d <= 1).all() and (d > 0).mean() < 1e-3, "merge of the sampled tokens differs from the oracle merge"
+
+
 @pytest.mark.parametrize("bm", [32, 64, 128, 256, 384])
 def test_grouped_block_m_variants(orc, pd, bm):
     """Every row tile on a small layer with ragged expert sizes (0..many rows)."""
