@@ -198,6 +198,59 @@ def test_runtime_staging_slots_reused_across_calls(orc):
         rt.close()
 
 
+def test_runtime_zipf_t4096_sampled_tokens(orc):
+    """The Zipf(1.1) T=4096 prefill layer through the runtime at full size:
+    32 hottest experts resident, every other touched expert staged through 8
+    demand slots in batches, hot experts spanning many row tiles.  Routing is
+    checked bit-exact for every token; for a seeded sample of tokens each of
+    their grouped rows is checked against the oracle's expert output and
+    their merged outputs against the oracle merge of those rows."""
+    from pdscope_amd import synthetic
+    from pdscope_amd.cache import ExpertKey
+    from pdscope_amd.pdscope_runtime import PDScopeCudaRuntime
+    from tests.gpu_helpers import MAX_REL, MEAN_ABS, err_metrics, ulp_diff_bf16
+    q = synthetic.QWEN
+    H, I, E, k, T = q["H"], q["I"], q["E"], q["k"], 4096
+    layers, masters = build(1, H, I, E, k, seed=97)
+    bias, perm = synthetic.zipf_bias(E, 1.1, seed=98, device=DEV)
+    hottest = sorted(range(E), key=lambda e: int(perm[e]))[:32]
+    rt = PDScopeCudaRuntime(masters, hot_keys=[ExpertKey(0, e, "bf16") for e in hottest], speculative_slots=0,
+                            demand_slots=8)
+    copies = watch_copies(rt, layers)
+    try:
+        x = synthetic.make_tokens(T, H, seed=99)
+        out, routing, row = rt.forward(x, layers[0].gate, layer=0, step=0, top_k=k, bias=bias)
+        torch.cuda.synchronize()
+        assert_copies_intact(copies)
+        ids, wk = routing.selected.cpu().numpy(), u16(routing.weights)
+        oi, ow = orc.route_from_logits(u16(routing.logits), k, True, bias.cpu().numpy())
+        assert np.array_equal(ids, oi) and np.array_equal(wk, ow)
+        counts = np.bincount(ids.reshape(-1), minlength=E)
+        assert counts.max() > 2000 and len(row["decision"]["on_demand_queue"]) > 50
+        ws = rt._ws[k]
+        row_of = ws.row_of[:T * k].cpu().numpy().reshape(T, k)
+        y_all = u16(ws.y[:T * k * H].view(T * k, H))
+        rng = np.random.default_rng(4097)
+        tokens = np.sort(rng.choice(T, 32, replace=False))
+        experts, xu, IH = u16(layers[0].experts), u16(x), I * H
+        got_y, ref_y = [], []
+        for t in tokens:
+            for s in range(k):
+                blk = experts[ids[t, s]]
+                ref_y.append(orc.expert_forward(xu[t:t + 1], blk[:IH].reshape(I, H), blk[IH:2 * IH].reshape(I, H),
+                                                blk[2 * IH:].reshape(H, I))[0])
+                got_y.append(y_all[row_of[t, s]])
+        got_y, ref_y = np.stack(got_y), np.stack(ref_y)
+        m_y = err_metrics(orc.bf16_to_f32(got_y), orc.bf16_to_f32(ref_y))
+        assert m_y["max_rel"] <= MAX_REL and m_y["mean_abs"] <= MEAN_ABS, m_y
+        local = np.arange(len(tokens) * k, dtype=np.int32).reshape(len(tokens), k)
+        d = ulp_diff_bf16(u16(out)[tokens], orc.merge(got_y, local, wk[tokens]))
+        assert (d <= 1).all() and (d > 0).mean() < 1e-3
+        closure(rt)
+    finally:
+        rt.close()
+
+
 def test_slot_table_fill_is_ordered_before_uploads_on_other_streams():
     """The device slot table is created by a zero fill on the caller's
     stream; its first upload runs on the compute stream.  With the caller's
