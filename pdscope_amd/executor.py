@@ -184,6 +184,12 @@ class ExpertExecutor:
         self._host_tables = {}  # layer -> host list of base addresses (0 = no ready copy)
         self._dev_tables = {}   # layer -> device int64 [E]
         self._ring = _PinnedRing(8 * 256)
+        # the slot storage was allocated on the current stream, whose queued
+        # work may still touch the blocks' previous owners: order both
+        # executor streams after it before they write or read a slot
+        cur = torch.cuda.current_stream(self.device)
+        self.load_stream.wait_stream(cur)
+        self.compute_stream.wait_stream(cur)
         self._group_stream_ctx = None
         self._cpu_pool = None
         self._cpu_tasks = {}  # key -> PendingCpu
