@@ -107,7 +107,7 @@ int pdscope_schedule_balanced(const int32_t *counts, const int32_t *sel, int nse
                               int32_t *order, int32_t *tile_start, void *stream);
 
 /* Row tile (32, 64, 128, 256 or 384) for `rows_hint` average rows per
- * selected expert: <= 16 rows 32, <= 64 rows 64, <= 96 rows 128, <= 192 rows
+ * selected expert: <= 16 rows 32, <= 64 rows 64, <= 124 rows 128, <= 192 rows
  * 256, <= 320 rows 384 (one tile holds a typical expert, so its weights
  * stream once), 256 above.  No reference counterpart: the reference launches
  * one torch GEMM chain per expert (expertbench/adapters/qwen.py:87-90). */

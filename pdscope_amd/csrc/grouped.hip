@@ -472,7 +472,10 @@ using namespace pd;
 PD_API int pdscope_grouped_block_m(int rows_hint) {
     if (rows_hint <= 16) return 32;
     if (rows_hint <= 64) return 64;
-    if (rows_hint <= 96) return 128;
+    // up to ~124 rows a 128-row tile holds most experts whole (measured:
+    // 122 mean rows of 17 MB experts 3.6% faster than 256-row tiles, 128 mean
+    // rows of 9 MB experts 2.7% slower)
+    if (rows_hint <= 124) return 128;
     if (rows_hint <= 192) return 256;
     // one 384-row tile holds an expert of the typical 200..320 rows (no
     // tail tile re-reading its weights); beyond that 256x256 tiles read the
