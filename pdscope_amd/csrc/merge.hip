@@ -11,6 +11,11 @@
 
 namespace pd {
 
+// KM > 0: k <= KM, and the k row indices, weights and rows of a thread are
+// loaded before the first is used (two memory latencies per output chunk
+// instead of 2k); KM == 0: any k, one slot at a time.  The fp32
+// accumulation is the same in both: slot order, one rounding.
+template <int KM>
 __global__ __launch_bounds__(256) void merge_kernel(const uint16_t *__restrict__ y,
                                                     const int32_t *__restrict__ row_of,
                                                     const uint16_t *__restrict__ w, int T, int k, int H,
@@ -30,10 +35,7 @@ __global__ __launch_bounds__(256) void merge_kernel(const uint16_t *__restrict__
 #pragma unroll
             for (int q = 0; q < 8; ++q) acc[q] = 0.0f;
         }
-        for (int s = 0; s < k; ++s) {
-            const int r = row_of[(size_t)t * k + s];
-            const float ws = bf2f(w[(size_t)t * k + s]);
-            const uint4 v = reinterpret_cast<const uint4 *>(y + (size_t)r * H)[c];
+        auto add = [&](float ws, uint4 v) __attribute__((always_inline)) {
             acc[0] = __builtin_fmaf(ws, lo_bf(v.x), acc[0]);
             acc[1] = __builtin_fmaf(ws, hi_bf(v.x), acc[1]);
             acc[2] = __builtin_fmaf(ws, lo_bf(v.y), acc[2]);
@@ -42,6 +44,27 @@ __global__ __launch_bounds__(256) void merge_kernel(const uint16_t *__restrict__
             acc[5] = __builtin_fmaf(ws, hi_bf(v.z), acc[5]);
             acc[6] = __builtin_fmaf(ws, lo_bf(v.w), acc[6]);
             acc[7] = __builtin_fmaf(ws, hi_bf(v.w), acc[7]);
+        };
+        if constexpr (KM > 0) {
+            int r[KM];
+            float ws[KM];
+#pragma unroll
+            for (int s = 0; s < KM; ++s) {
+                r[s] = s < k ? row_of[(size_t)t * k + s] : 0;
+                ws[s] = s < k ? bf2f(w[(size_t)t * k + s]) : 0.0f;
+            }
+            uint4 v[KM];
+#pragma unroll
+            for (int s = 0; s < KM; ++s)
+                if (s < k) v[s] = reinterpret_cast<const uint4 *>(y + (size_t)r[s] * H)[c];
+#pragma unroll
+            for (int s = 0; s < KM; ++s)
+                if (s < k) add(ws[s], v[s]);
+        } else {
+            for (int s = 0; s < k; ++s) {
+                const int r = row_of[(size_t)t * k + s];
+                add(bf2f(w[(size_t)t * k + s]), reinterpret_cast<const uint4 *>(y + (size_t)r * H)[c]);
+            }
         }
         uint4 o;
         o.x = f2bf(acc[0]) | (f2bf(acc[1]) << 16);
@@ -75,8 +98,14 @@ PD_API int pdscope_merge(const void *y, const int32_t *row_of, const void *w, in
     if (T < 1 || k < 1 || H < 8 || H % 8) return fail(kEInval, "merge: need T,k >= 1 and H % 8 == 0");
     const int64_t total = (int64_t)T * (H / 8);
     const int blocks = (int)std::min<int64_t>((total + 255) / 256, 65536);
-    merge_kernel<<<blocks, 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
-        (const uint16_t *)y, row_of, (const uint16_t *)w, T, k, H, (const uint16_t *)add_in, (uint16_t *)out);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const uint16_t *yy = (const uint16_t *)y, *ww = (const uint16_t *)w, *aa = (const uint16_t *)add_in;
+    if (k <= 8)
+        merge_kernel<8><<<blocks, 256, 0, s>>>(yy, row_of, ww, T, k, H, aa, (uint16_t *)out);
+    else if (k <= 16)
+        merge_kernel<16><<<blocks, 256, 0, s>>>(yy, row_of, ww, T, k, H, aa, (uint16_t *)out);
+    else
+        merge_kernel<0><<<blocks, 256, 0, s>>>(yy, row_of, ww, T, k, H, aa, (uint16_t *)out);
     return check_launch("merge_kernel");
 }
 

@@ -294,18 +294,22 @@ __global__ __launch_bounds__(256) void schedule_balanced_kernel(const int32_t *_
                                                                 const int32_t *__restrict__ sel, int nsel, int bm,
                                                                 int32_t *__restrict__ order,
                                                                 int32_t *__restrict__ tile_start) {
-    __shared__ int s_rows[256];
+    __shared__ __align__(16) int s_rows[256];  // -1 past nsel: never ranks above a real expert
     __shared__ int s_at[256];  // list position -> sel position
     __shared__ int s_wsum[4];
     const int i = threadIdx.x;
-    s_rows[i] = i < nsel ? counts[sel[i]] : 0;
+    s_rows[i] = i < nsel ? counts[sel[i]] : -1;
     __syncthreads();
     if (i < nsel) {
         const int c = s_rows[i];
         int r = 0;
-        for (int j = 0; j < nsel; ++j) {
-            const int cj = s_rows[j];
-            r += (cj > c) | ((cj == c) & (j < i));
+        // four rows per LDS read (broadcast)
+        for (int j = 0; j < nsel; j += 4) {
+            const int4 q = *reinterpret_cast<const int4 *>(s_rows + j);
+            r += (q.x > c) | ((q.x == c) & (j < i));
+            r += (q.y > c) | ((q.y == c) & (j + 1 < i));
+            r += (q.z > c) | ((q.z == c) & (j + 2 < i));
+            r += (q.w > c) | ((q.w == c) & (j + 3 < i));
         }
         const int full = nsel >> 3, rem = nsel & 7;
         const int rd = r >> 3, w = r & 7;

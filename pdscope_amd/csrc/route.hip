@@ -117,6 +117,8 @@ __global__ __launch_bounds__(512) void route_partial_kernel(const uint16_t *__re
 
 // route_finish_kernel: one wave per token sums the KS partials in chunk
 // order, rounds to the bf16 logit and runs the softmax / top-k / renorm.
+// The partials are loaded eight chunks at a time before they are added (one
+// memory latency per eight chunks, not per chunk).
 template <int J>
 __global__ __launch_bounds__(256) void route_finish_kernel(const float *__restrict__ part, int KS, int T, int E,
                                                            const float *__restrict__ bias, int k, int normalize,
@@ -130,12 +132,22 @@ __global__ __launch_bounds__(256) void route_finish_kernel(const float *__restri
     float v[J];
 #pragma unroll
     for (int j = 0; j < J; ++j) v[j] = 0.0f;
-    for (int ks = 0; ks < KS; ++ks) {
-        const float *row = part + ((size_t)ks * T + t) * E;
+    for (int ks0 = 0; ks0 < KS; ks0 += 8) {
+        float pv[8][J];
 #pragma unroll
-        for (int j = 0; j < J; ++j) {
-            const int e = lane + 64 * j;
-            if (e < E) v[j] = v[j] + row[e];
+        for (int u = 0; u < 8; ++u) {
+            const float *row = part + ((size_t)(ks0 + u) * T + t) * E;
+#pragma unroll
+            for (int j = 0; j < J; ++j) {
+                const int e = lane + 64 * j;
+                pv[u][j] = (ks0 + u < KS && e < E) ? row[e] : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+#pragma unroll
+            for (int j = 0; j < J; ++j)
+                if (ks0 + u < KS && lane + 64 * j < E) v[j] = v[j] + pv[u][j];
         }
     }
 #pragma unroll
