@@ -100,9 +100,13 @@ PD_API int pdscope_merge(const void *y, const int32_t *row_of, const void *w, in
     const int blocks = (int)std::min<int64_t>((total + 255) / 256, 65536);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const uint16_t *yy = (const uint16_t *)y, *ww = (const uint16_t *)w, *aa = (const uint16_t *)add_in;
-    if (k <= 8)
+    // few tokens: latency-bound, all of a thread's rows in flight at once
+    // (T=512: 7.7 us against 9.5 us); many tokens: bandwidth-bound, where the
+    // slot-at-a-time loop keeps more threads resident (T=4096: 29.5 us
+    // against 33.3 us)
+    if (k <= 8 && T <= 1024)
         merge_kernel<8><<<blocks, 256, 0, s>>>(yy, row_of, ww, T, k, H, aa, (uint16_t *)out);
-    else if (k <= 16)
+    else if (k <= 16 && T <= 1024)
         merge_kernel<16><<<blocks, 256, 0, s>>>(yy, row_of, ww, T, k, H, aa, (uint16_t *)out);
     else
         merge_kernel<0><<<blocks, 256, 0, s>>>(yy, row_of, ww, T, k, H, aa, (uint16_t *)out);
