@@ -1,7 +1,7 @@
 /*
  * oracle.c -- CPU restatement of PDScope's GPU MoE-layer arithmetic.
  *
- * TEST INFRASTRUCTURE ONLY (the checker): never linked into the product
+ * TEST INFRASTRUCTURE ONLY (results are checked against it): never linked into the product
  * library.  Built by oracle/Makefile into oracle/liboracle.so and called from
  * tests/ through oracle/oracle.py.
  *

@@ -3,7 +3,7 @@
  *
  * TEST INFRASTRUCTURE ONLY.  Nothing in the product library links, loads or
  * calls this code; only tests/, __graft_entry__.smoke() and bench.py's
- * cpu_baseline leg use it, and only as the checker.
+ * cpu_baseline leg use it, and only to check results against.
  *
  * Every function cites the reference line it restates.  All bf16 values are
  * raw uint16_t bit patterns (the upper half of an IEEE binary32).

@@ -1,7 +1,7 @@
 """numpy front end of the C oracle (oracle/liboracle.so).
 
-TEST INFRASTRUCTURE ONLY: the checker that tests/, ``__graft_entry__.smoke()``
-and bench.py's ``cpu_baseline`` leg call.  The product package never imports
+TEST INFRASTRUCTURE ONLY: the reference restatement that tests/,
+``__graft_entry__.smoke()`` and bench.py's ``cpu_baseline`` leg check against.  The product package never imports
 this module.
 
 bf16 tensors are numpy ``uint16`` arrays of raw bit patterns.

@@ -152,7 +152,7 @@ __device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
 // reduction x = n*ln2 + r with ln2 split into a 13-bit head and a tail, the
 // degree-7 Taylor polynomial of exp(r) in Horner form, and scaling by 2^n
 // built in the exponent field.  Results below 2^-125 flush to 0, so the value
-// never depends on the denormal mode.  The host-side checker evaluates the
+// never depends on the denormal mode.  The host-side oracle evaluates the
 // same sequence, which makes routing probabilities reproducible bit for bit.
 __device__ __forceinline__ float route_expf(float x) {
 #pragma clang fp contract(off)

@@ -50,7 +50,7 @@ __device__ __forceinline__ float dpp_max_f32(float f) {
 // (bf16 values held as fp32, in LDS).  Lane l owns experts l, l+64, ...;
 // the softmax denominator is summed per lane in that order and then by an
 // xor butterfly over offsets 32..1, an order that is fixed and reproduced by
-// the host-side checker.  p[j] is the probability of expert lane + 64 j (0
+// the host-side oracle.  p[j] is the probability of expert lane + 64 j (0
 // where that is >= E); probs row t is written when non-null.
 template <int J>
 __device__ __forceinline__ void softmax_wave(const float *lrow, const float *__restrict__ bias, int E, int t,
