@@ -67,6 +67,7 @@ SHAPES = [
     dict(H=1024, I=512, E=64, k=4, normalize=True),
     dict(H=2048, I=1408, E=64, k=2, normalize=False),  # DeepSeek-V2-Lite widths, k within the fused limits
     dict(H=4096, I=256, E=32, k=3, normalize=True),
+    dict(H=2048, I=512, E=256, k=8, normalize=True),   # 256 experts: four candidates per lane in the top-k
 ]
 
 
