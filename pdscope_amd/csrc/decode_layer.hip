@@ -10,8 +10,8 @@
 // every block is resident at once (checked against the occupancy of this
 // kernel on the current device).  Phases:
 //   1. blocks 0 .. E/4-1: one wave per router row -> bf16 logit;
-//   2. every block collects the E logits and runs softmax / top-k itself
-//      (block-wide ranking), so no further hop publishes the routing;
+//   2. wave 0 of every block collects the E logits and runs softmax / top-k
+//      itself, so no further hop publishes the routing;
 //   3. every wave issues the loads of its P (gate, up) row pairs of the
 //      routed experts (16-byte non-temporal loads);
 //   4. gate/up dot products -> h; then the wave issues its down-projection
