@@ -478,13 +478,9 @@ class PDScopeCudaRuntime:
         row counts (known on the host since the demand reveal) are `rows`:
         the row-tile height follows their mean, the grid their exact tile count."""
         bm = ops.grouped_block_m(sum(rows) // len(rows), max(rows))
-        nsel = sel_dev.numel()
-        tile_start = ws.tile_start[:nsel + 1]
-        order = ws.sel_order[:nsel]
-        ops.schedule(packed.counts, sel_dev, bm, out=tile_start, order=order)
-        max_tiles = sum((r + bm - 1) // bm for r in rows)
-        ops.swiglu_grouped(x, packed.perm_token, packed.offsets, order, tile_start, max_tiles, bm, slots_dev, self.H,
-                           self.I, ws.h_ws, ws.y)
+        bmd = L.down_block_m(bm, self.H, self.I)
+        L.grouped_ffn(x, packed, sel_dev, bm, sum((r + bm - 1) // bm for r in rows), slots_dev, ws,
+                      max_tiles_down=sum((r + bmd - 1) // bmd for r in rows))
 
     # ------------------------------------------------------------ resident decode graph
 
