@@ -198,13 +198,17 @@ def test_runtime_staging_slots_reused_across_calls(orc):
         rt.close()
 
 
-def test_runtime_zipf_t4096_sampled_tokens(orc):
-    """The Zipf(1.1) T=4096 prefill layer through the runtime at full size:
-    32 hottest experts resident, every other touched expert staged through 8
-    demand slots in batches, hot experts spanning many row tiles.  Routing is
-    checked bit-exact for every token; for a seeded sample of tokens each of
-    their grouped rows is checked against the oracle's expert output and
-    their merged outputs against the oracle merge of those rows."""
+@pytest.mark.parametrize("case", ["zipf_staged", "uniform_resident"])
+def test_runtime_t4096_sampled_tokens(orc, case):
+    """T=4096 prefill layers through the runtime at full size.  zipf_staged:
+    a Zipf(1.1) router bias, the 32 hottest experts resident, every other
+    touched expert staged through 8 demand slots in batches, hot experts
+    spanning many row tiles.  uniform_resident: uniform routing with all 128
+    experts resident, one grouped launch on 384-row gate/up tiles and
+    256-row down tiles.  Routing is checked bit-exact for every token; for a
+    seeded sample of tokens each of their grouped rows is checked against the
+    oracle's expert output and their merged outputs against the oracle merge
+    of those rows."""
     from pdscope_amd import synthetic
     from pdscope_amd.cache import ExpertKey
     from pdscope_amd.pdscope_runtime import PDScopeCudaRuntime
@@ -212,8 +216,11 @@ def test_runtime_zipf_t4096_sampled_tokens(orc):
     q = synthetic.QWEN
     H, I, E, k, T = q["H"], q["I"], q["E"], q["k"], 4096
     layers, masters = build(1, H, I, E, k, seed=97)
+    zipf = case == "zipf_staged"
     bias, perm = synthetic.zipf_bias(E, 1.1, seed=98, device=DEV)
-    hottest = sorted(range(E), key=lambda e: int(perm[e]))[:32]
+    hottest = sorted(range(E), key=lambda e: int(perm[e]))[:32] if zipf else list(range(E))
+    if not zipf:
+        bias = None
     rt = PDScopeCudaRuntime(masters, hot_keys=[ExpertKey(0, e, "bf16") for e in hottest], speculative_slots=0,
                             demand_slots=8)
     copies = watch_copies(rt, layers)
@@ -223,10 +230,16 @@ def test_runtime_zipf_t4096_sampled_tokens(orc):
         torch.cuda.synchronize()
         assert_copies_intact(copies)
         ids, wk = routing.selected.cpu().numpy(), u16(routing.weights)
-        oi, ow = orc.route_from_logits(u16(routing.logits), k, True, bias.cpu().numpy())
+        oi, ow = orc.route_from_logits(u16(routing.logits), k, True, None if bias is None else bias.cpu().numpy())
         assert np.array_equal(ids, oi) and np.array_equal(wk, ow)
         counts = np.bincount(ids.reshape(-1), minlength=E)
-        assert counts.max() > 2000 and len(row["decision"]["on_demand_queue"]) > 50
+        if zipf:
+            assert counts.max() > 2000 and len(row["decision"]["on_demand_queue"]) > 50
+        else:
+            from pdscope_amd import layer as L, ops
+            assert not row["decision"]["on_demand_queue"]
+            bm = ops.grouped_block_m(T * k // E, int(counts.max()))
+            assert bm == 384 and L.down_block_m(bm, H, I) == 256
         ws = rt._ws[k]
         row_of = ws.row_of[:T * k].cpu().numpy().reshape(T, k)
         y_all = u16(ws.y[:T * k * H].view(T * k, H))
