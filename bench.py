@@ -12,14 +12,16 @@ prefill, route (K1) -> decode GEMV gate/up + down/merge (K4) for T = 1
 independently seeded layer copies so the 256 MB Infinity Cache cannot hold
 the streamed weights between steps.
 
-The default workload is the T = 512 prefill (128 experts, top-8, all resident).
-The same JSON line also carries the T = 1 decode, the T = 4096 prefill (all
-resident, and Zipf-skewed with 32 resident experts and 8 demand staging slots
-through the runtime) and the DeepSeek-V2-Lite mixed-batch results
-("workloads"), each with its own roofline figure, and a CPU baseline: the
+The default workload is the T = 1 decode layer (128 experts, top-8, all
+resident), the configuration the metric is quoted on.  The same JSON line
+also carries the T = 512 and T = 4096 prefills (all resident, and the
+T = 4096 Zipf-skewed layer with 32 resident experts and 8 demand staging
+slots through the runtime) and the DeepSeek-V2-Lite mixed-batch results
+("workloads"), each with its own roofline figure, and CPU baselines: the
 AVX2 bf16 SwiGLU expert kernel under oracle/ (a stand-in for ktransformers'
 AVX2BF16_MOE, which is not available offline) timed on this host's cores on
-the same layer and routing.
+the same layers and routings, each over a sample of about CPU_SAMPLE_S
+seconds of CPU work.
 
 Roofline: ``achieved`` is algorithmic bytes (or useful flops) of the dominant
 kernel per launch divided by its mean duration, measured with HIP events on
@@ -40,18 +42,21 @@ BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
 H, I, E, K_TOP = 2048, 768, 128, 8
 EXPERT_BYTES = 3 * I * H * 2   # 9 437 184
 ROUTER_BYTES = E * H * 2
+CPU_SAMPLE_S = 10.0            # seconds of CPU work per CPU-baseline sample
 
 
 def parse():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="prefill512",
+    ap.add_argument("--steps", type=int, default=4000)
+    ap.add_argument("--warmup", type=int, default=400)
+    ap.add_argument("--workload", default="decode",
                     choices=["prefill512", "decode", "prefill4096", "prefill4096_zipf", "dsv2_mixed", "stack48"])
     ap.add_argument("--no-extra", action="store_true", help="only the main workload")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, cpus) - 1")
+    ap.add_argument("--cpu-seconds", type=float, default=CPU_SAMPLE_S,
+                    help="CPU work per CPU-baseline sample (after two warm-up runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 5 device copies of 1 GiB (calibrates the FETCH_SIZE / WRITE_SIZE counters)")
     ap.add_argument("--calibrate-costs", metavar="PATH",
@@ -378,7 +383,6 @@ def run_zipf_staged(steps, warmup, n_layers, device, seed0):
     finally:
         rt.close()
     gemm = zipf_gemm(lay0, xs[0], bias, device)
-    del lay0
     t = statistics.mean(times)
     h2d_mean = statistics.mean(h2d)
     pcie = dict(bound="pcie_h2d", achieved=h2d_mean / t / 1e9, peak=copy_gbs, unit="GB/s",
@@ -390,7 +394,8 @@ def run_zipf_staged(steps, warmup, n_layers, device, seed0):
                 resident_experts=len(hottest), demand_slots=8, experts_touched=statistics.mean(n_touched),
                 demand_experts=statistics.mean(n_demand), h2d_bytes_per_layer=h2d_mean,
                 max_rows_per_expert=max_rows, pcie=pcie, layer_tflops=flops / t / 1e12,
-                layers_rotated=n_layers, copy_only_ms=nc * EXPERT_BYTES / copy_gbs / 1e6, grouped_gemm=gemm)
+                layers_rotated=n_layers, copy_only_ms=nc * EXPERT_BYTES / copy_gbs / 1e6, grouped_gemm=gemm,
+                first_layer=(lay0, None), first_x=xs[0], bias=bias)
 
 
 def zipf_gemm(lay, x, bias, device, reps=20):
@@ -630,66 +635,88 @@ def u16(t):
     return t.detach().contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
 
 
-def cpu_baseline_prefill(res, threads, reps=7, warm=2):
-    """Full expert work of the first layer's routing (all T*k rows) on the host cores."""
+def timed_sample(run, budget_s, warm=2, min_runs=3):
+    """run(r) repeated after `warm` untimed calls until `budget_s` seconds of
+    timed work (and at least min_runs runs) have passed; the per-run times."""
+    for r in range(warm):
+        run(r)
+    times = []
+    r = warm
+    while len(times) < min_runs or sum(times) < budget_s:
+        t0 = time.perf_counter()
+        run(r)
+        times.append(time.perf_counter() - t0)
+        r += 1
+    return times
+
+
+def cpu_baseline_prefill(lay, x, threads, budget_s, *, bias=None, what="", warm=2):
+    """The full expert work of one layer's routing (all T*k rows, each through
+    its expert, scaled by its routing weight) on the host cores, repeated for
+    about budget_s seconds; tokens per second of CPU time."""
     import numpy as np
     from oracle import oracle as orc
-    lay, _ = res["first_layer"]
-    ws = res["ws"]
-    T = res["T"]
     from pdscope_amd import layer
-    layer.route(res["first_x"], lay.gate, ws)
+    T = x.shape[0]
+    ws = layer.MoEWorkspace(T, H, I, E, K_TOP, x.device, route_only=True)
+    layer.route(x, lay.gate, ws, bias=bias)
     ids = ws.ids[:T].cpu().numpy()
     w = ws.weights[:T].float().cpu().numpy()
-    x = u16(res["first_x"])
+    x_host = u16(x)
     experts = np.ascontiguousarray(u16(lay.experts))
     ptrs = [experts[e].ctypes.data for e in range(E)]
-    rows = np.ascontiguousarray(np.repeat(x, K_TOP, axis=0))
+    rows = np.ascontiguousarray(np.repeat(x_host, K_TOP, axis=0))
     sel = ids.reshape(-1).astype(np.int64)
     coeff = w.reshape(-1).astype(np.float32)
-    times = []
-    for r in range(warm + reps):
-        t0 = time.perf_counter()
-        orc.cpu_moe_rows(rows, sel, coeff, ptrs, H, I, threads)
-        if r >= warm:
-            times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
-    return dict(value=T / med, unit="tok/s", cores=threads, kind="port",
-                sample=f"full T={T} layer expert work ({T * K_TOP} rows, routing of layer 0), median of {reps} "
-                       f"runs after {warm} warm-ups, {threads} threads, {cpu_model()}",
-                median_s=med)
+    times = timed_sample(lambda r: orc.cpu_moe_rows(rows, sel, coeff, ptrs, H, I, threads), budget_s, warm=warm)
+    total = sum(times)
+    return dict(value=T * len(times) / total, unit="tok/s", cores=threads, kind="port",
+                sample=f"{what}T={T} layer, full expert work of its routing ({T * K_TOP} rows through "
+                       f"{int((np.bincount(sel, minlength=E) > 0).sum())} experts), {len(times)} runs "
+                       f"({total:.1f} s of CPU work) after {warm} warm-ups, {threads} threads, {cpu_model()}",
+                median_s=statistics.median(times))
 
 
-def cpu_baseline_decode(res, threads, reps=7, warm=2):
+def cpu_baseline_decode(lay, x, threads, budget_s, copies=8, warm=2):
+    """One T=1 token through its 8 routed experts on the host cores, repeated
+    for about budget_s seconds; the 8 experts' weights rotate through
+    `copies` distinct host copies (copies x 75 MB, more than a last-level
+    cache holds) so DRAM serves them, as it serves a CPU decode step."""
+    import ctypes
     import numpy as np
     from oracle import oracle as orc
     from pdscope_amd import layer
-    lay, _ = res["first_layer"]
-    ws = res["ws"]
-    layer.route(res["first_x"], lay.gate, ws)
-    ids = ws.ids[:1].cpu().numpy()
-    w = u16(ws.weights[:1])
-    x = u16(res["first_x"])
-    experts = np.ascontiguousarray(u16(lay.experts))
-    ptrs = [experts[e].ctypes.data for e in range(E)]
-    # rotate the 8 selected experts through distinct host copies so DRAM, not the
-    # CPU caches, serves the weights (8 x 9 MiB per token)
-    copies = [np.ascontiguousarray(experts[ids[0]].copy()) for _ in range(4)]
-    times = []
-    for r in range(warm + reps):
-        c = copies[r % len(copies)]
-        local_ptrs = list(ptrs)
-        for s, e in enumerate(ids[0]):
-            local_ptrs[e] = c[s].ctypes.data
-        t0 = time.perf_counter()
-        orc.cpu_moe_decode(x, ids, w, local_ptrs, H, I, threads)
-        if r >= warm:
-            times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
-    return dict(value=1.0 / med, unit="tok/s", cores=threads, kind="port",
-                sample=f"one T=1 token through its 8 routed experts, median of {reps} runs after {warm} warm-ups, "
-                       f"{threads} threads, {cpu_model()}",
-                dram_gbs=K_TOP * EXPERT_BYTES / med / 1e9)
+    ws = layer.MoEWorkspace(1, H, I, E, K_TOP, x.device, route_only=True)
+    layer.route(x, lay.gate, ws)
+    ids = np.ascontiguousarray(ws.ids[:1].cpu().numpy().reshape(-1), dtype=np.int32)
+    w = np.ascontiguousarray(u16(ws.weights[:1]).reshape(-1))
+    x_host = np.ascontiguousarray(u16(x).reshape(-1))
+    experts = u16(lay.experts)
+    u16p = ctypes.POINTER(ctypes.c_uint16)
+    bufs, tables = [], []
+    for _ in range(copies):
+        c = np.ascontiguousarray(experts[ids].copy())
+        bufs.append(c)
+        ptrs = [ctypes.cast(experts[0].ctypes.data, u16p)] * E
+        for s, e in enumerate(ids):
+            ptrs[e] = ctypes.cast(c[s].ctypes.data, u16p)
+        tables.append((u16p * E)(*ptrs))
+    out = np.empty(H, np.uint16)
+    L = orc.lib()
+
+    def run(r):
+        rc = L.cpu_moe_decode(x_host.ctypes.data_as(u16p), ids.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
+                              w.ctypes.data_as(u16p), K_TOP, tables[r % copies], H, I, out.ctypes.data_as(u16p),
+                              threads)
+        if rc:
+            raise RuntimeError("cpu_moe_decode unavailable (needs AVX2+FMA)")
+    times = timed_sample(run, budget_s, warm=warm)
+    total = sum(times)
+    return dict(value=len(times) / total, unit="tok/s", cores=threads, kind="port",
+                sample=f"T=1 tokens through their 8 routed experts of one layer, {len(times)} tokens "
+                       f"({total:.1f} s of CPU work) after {warm} warm-ups, weights rotated over {copies} host "
+                       f"copies, {threads} threads, {cpu_model()}",
+                median_s=statistics.median(times), dram_gbs=K_TOP * EXPERT_BYTES * len(times) / total / 1e9)
 
 
 # ----------------------------------------------------------------------------- reporting
@@ -782,13 +809,21 @@ def main():
             f"{rec['kernel_ms_mean']:.4f} ms, {bw['achieved']:.0f} GB/s ({bw['bound']})")
         records[wl] = rec
         raw[wl] = res
-        if not args.no_cpu_baseline and wl in ("prefill512", "decode"):
-            log(f"[bench] {wl}: CPU baseline on {threads} threads")
-            cb = cpu_baseline_prefill(res, threads) if kind == "prefill" else cpu_baseline_decode(res, threads)
+        if not args.no_cpu_baseline and wl in ("prefill512", "decode", "prefill4096", "prefill4096_zipf"):
+            log(f"[bench] {wl}: CPU baseline on {threads} threads, ~{args.cpu_seconds:.0f} s")
+            lay0 = res["first_layer"][0]
+            if kind == "decode":
+                cb = cpu_baseline_decode(lay0, res["first_x"], threads, args.cpu_seconds)
+            elif kind == "zipf":
+                cb = cpu_baseline_prefill(lay0, res["first_x"], threads, args.cpu_seconds, bias=res["bias"],
+                                          what="Zipf(1.1)-biased ")
+            else:
+                cb = cpu_baseline_prefill(lay0, res["first_x"], threads, args.cpu_seconds)
             rec["cpu_baseline"] = cb
             log(f"[bench] {wl}: CPU baseline {cb['value']:.2f} tok/s")
-        for k in ("first_layer", "first_x", "ws"):
+        for k in ("first_layer", "first_x", "ws", "bias"):
             res.pop(k, None)
+            rec.pop(k, None)
         torch.cuda.empty_cache()
 
     main = records[args.workload]

@@ -133,6 +133,10 @@ class ExpertExecutor:
             raise ValueError("equal-size bf16 experts required")
         self.expert_bytes = next(iter(sizes))
         self.device = torch.device("cuda", device) if isinstance(device, int) else torch.device(device)
+        if self.device.type != "cuda":
+            raise ValueError("the executor runs on a GPU device")
+        if self.device.index is None:  # "cuda" names the current device; keep its index so placement checks compare
+            self.device = torch.device("cuda", torch.cuda.current_device())
         self.cpu_backend = cpu_backend
         self.gpu_backend = None
         self.capture_events = capture_events

@@ -213,6 +213,7 @@ class PDScopeCudaRuntime:
             # entries the first replay saw (a copy still in flight reads as null)
             replay_table = list(self.executor.table(layer, E)[1])
             logits, ids, weights = self._replay_decode_graph(layer, x, gate, normalize, k, out)
+            fused_replays = 1
         else:
             logits, ids, weights = L.route(x, gate, ws, normalize=normalize, bias=bias)
         predict = prefetch and next_gate is not None
@@ -232,8 +233,14 @@ class PDScopeCudaRuntime:
         host[:n0].copy_(counts_dev, non_blocking=True)
         if predict:
             host[n0:n0 + E].copy_(nws.hist, non_blocking=True)
+        err_at = 2 * E + 8
+        if graph_path:
+            # the fused decode kernel's sticky error word rides along with the counts
+            host[err_at:err_at + 1].copy_(self._decode_error_word(), non_blocking=True)
         self._copy_done.record(cur)
         self._copy_done.synchronize()
+        if graph_path:
+            self._raise_if_decode_gave_up(int(host[err_at]))
         if T > 1:
             counts = {e: int(c) for e, c in enumerate(host[:E].tolist()) if c}
         else:
@@ -318,6 +325,8 @@ class PDScopeCudaRuntime:
             if not demand:  # with misses the demand batch below replays over the completed table
                 if any(replay_table[e] == 0 for e in counts):
                     # a routed copy landed after the first replay: replay over the completed table
+                    fused_replays += 1
+
                     def launch():
                         self._replay_decode_graph(layer, x, gate, normalize, k, out)
                 else:
@@ -348,6 +357,8 @@ class PDScopeCudaRuntime:
                 ex.table(layer, E)
                 require_copies(batch)
                 if graph_path:
+                    fused_replays += 1
+
                     def launch():
                         self._replay_decode_graph(layer, x, gate, normalize, k, out)
                     comp = ex.gpu_group([key(e) for e in resident + batch], launch, input_ref=x, wait_for=cur)
@@ -408,6 +419,12 @@ class PDScopeCudaRuntime:
         done = torch.cuda.Event()
         done.record(ex.compute_stream)
         cur.wait_event(done)
+        if graph_path and fused_replays > 1:
+            # replays after the demand reveal: their error word, read once they completed
+            host[err_at:err_at + 1].copy_(self._decode_error_word(), non_blocking=True)
+            self._copy_done.record(cur)
+            self._copy_done.synchronize()
+            self._raise_if_decode_gave_up(int(host[err_at]))
         self.cache.end_demand(identity)
         self._retire_current(layer, wait=True)
         self.poll()
@@ -453,6 +470,20 @@ class PDScopeCudaRuntime:
                    if phase == "decode" else "grouped",
                    measured_performance=False)
         return out, routing, row
+
+    def _decode_error_word(self):
+        """The fused decode kernel's sticky error word (int32 [1] device view)."""
+        w = ops.DECODE_WS_ERROR_WORD
+        return ops.decode_workspace(self.device, self.H)[w:w + 1]
+
+    def _raise_if_decode_gave_up(self, flag):
+        """A bounded wait of the fused decode kernel gave up (its grid was not
+        co-resident, e.g. while other work held CUs): the layer output is
+        invalid.  The word is cleared so later calls report only their own."""
+        if flag:
+            self._decode_error_word().zero_()
+            raise RuntimeError("fused decode layer: a bounded internal wait gave up, so this layer's output is "
+                               "invalid (its blocks were not all resident at once)")
 
     def _demand_pipeline(self, phase):
         """(experts per grouped launch, batches whose staging slots are held at once).
@@ -504,9 +535,17 @@ class PDScopeCudaRuntime:
             with torch.cuda.stream(side):
                 L.moe_forward(xin, gate, slots_dev, gws, normalize=normalize)
             torch.cuda.current_stream(self.device).wait_stream(side)
+            eager = [t.clone() for t in (gout, gws.logits[:1], gws.ids[:1], gws.weights[:1])]
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
                 L.moe_forward(xin, gate, slots_dev, gws, normalize=normalize)
+            # a captured graph must reproduce the eager launch bit for bit
+            # before it serves (the reference checks the same at capture,
+            # expertbench/executor.py:95-96)
+            graph.replay()
+            replayed = (gout, gws.logits[:1], gws.ids[:1], gws.weights[:1])
+            if not all(torch.equal(a, b) for a, b in zip(eager, replayed)):
+                raise AssertionError(f"captured decode graph of layer {layer} differs from its eager launch")
             g = (graph, xin, gout, gws, slots_dev)
             self._graphs[gkey] = g
         graph, xin, gout, gws, _ = g

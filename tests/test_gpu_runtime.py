@@ -316,6 +316,41 @@ def test_runtime_decode_graph_matches_eager(orc):
         rt.close()
 
 
+def test_runtime_raises_when_the_fused_decode_error_word_is_set():
+    """The fused decode kernel sets a sticky error word when a bounded wait
+    gives up.  Forced from the host here (the word is pre-set; the kernel only
+    ever sets it), the runtime must raise on that layer call, clear the word,
+    and serve the next call normally."""
+    from pdscope_amd import ops, synthetic
+    from pdscope_amd.cache import ExpertKey
+    from pdscope_amd.pdscope_runtime import PDScopeCudaRuntime
+    q = synthetic.QWEN
+    layers, masters = build(1, q["H"], q["I"], q["E"], q["k"], seed=97)
+    hot = [ExpertKey(0, e, "bf16") for e in range(q["E"])]
+    rt = PDScopeCudaRuntime(masters, hot_keys=hot, speculative_slots=0, resident_graphs=True)
+    try:
+        rt.forward(synthetic.make_tokens(4, q["H"], seed=98), layers[0].gate, layer=0, step=0)
+        x = synthetic.make_tokens(1, q["H"], seed=99)
+        out, _, row = rt.forward(x, layers[0].gate, layer=0, step=1)
+        assert row["decode_path"] == "graph"
+        word = ops.decode_workspace(DEV, q["H"])
+        word[ops.DECODE_WS_ERROR_WORD] = 1
+        with pytest.raises(RuntimeError, match="bounded internal wait gave up"):
+            rt.forward(x, layers[0].gate, layer=0, step=2)
+        assert int(word[ops.DECODE_WS_ERROR_WORD].item()) == 0
+    finally:
+        rt.close()
+    # a fresh runtime on the same device serves normally after the cleared word
+    rt = PDScopeCudaRuntime(masters, hot_keys=hot, speculative_slots=0, resident_graphs=True)
+    try:
+        rt.forward(synthetic.make_tokens(4, q["H"], seed=98), layers[0].gate, layer=0, step=0)
+        out2, _, _ = rt.forward(x, layers[0].gate, layer=0, step=1)
+        torch.cuda.synchronize()
+        assert torch.equal(out, out2)
+    finally:
+        rt.close()
+
+
 def test_runtime_partial_resident_decode_graph(orc):
     """Decode graph over a partly resident layer: experts without a copy read as
     null on the first replay; misses are staged in one batch and the graph is
