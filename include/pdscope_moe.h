@@ -84,6 +84,22 @@ int pdscope_pack(const int32_t *ids, int T, int k, int E, int32_t *counts, int32
                  int32_t *perm_token, int32_t *perm_pos, int32_t *row_of, void *workspace, void *stream);
 
 /*
+ * pdscope_pack without a workspace argument and without any allocation.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under hipGraph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Same arguments and outputs as pdscope_pack (bit
+ * for bit); the multi-block path's per-chunk counts live in a library-owned
+ * static device array of 512 KiB per GPU, looked up once per device on the
+ * first call.  Limit: T*k <= pdscope_pack_static_max_ids() (1048576 ids);
+ * larger inputs return 1 (EINVAL).  Every call on one GPU shares that GPU's
+ * array, so calls that overlap in time on one GPU (several streams or
+ * threads) race; nothing in the array has to be cleared between calls.
+ */
+size_t pdscope_pack_static_max_ids(void);
+int pdscope_pack_static(const int32_t *ids, int T, int k, int E, int32_t *counts, int32_t *offsets,
+                        int32_t *perm_token, int32_t *perm_pos, int32_t *row_of, void *stream);
+
+/*
  * Tile schedule for pdscope_swiglu_grouped over a subset of experts:
  * tile_start[i] = sum_{j<i} ceil(counts[sel[j]] / block_m), i = 0..nsel.
  * block_m is the row tile the grouped call will use (see

@@ -25,6 +25,8 @@ SIGNATURES = {
     "pdscope_route_hist": ([_vp, _i32, _i32, _vp, _vp], _i32),
     "pdscope_pack": ([_vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp], _i32),
     "pdscope_pack_workspace_size": ([_i32, _i32, _i32], _sz),
+    "pdscope_pack_static": ([_vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp], _i32),
+    "pdscope_pack_static_max_ids": ([], _sz),
     "pdscope_schedule": ([_vp, _vp, _i32, _i32, _vp, _vp], _i32),
     "pdscope_schedule_balanced": ([_vp, _vp, _i32, _i32, _vp, _vp, _vp], _i32),
     "pdscope_grouped_block_m": ([_i32], _i32),

@@ -12,6 +12,8 @@
 // Pass 2 repeats the ballots; a lane's grouped row is its wave base plus the
 // number of equal ids in lower lanes, so the order inside an expert stays
 // (slot, token) ascending.
+#include <mutex>
+
 #include "common.h"
 
 namespace pd {
@@ -367,6 +369,63 @@ PD_API int pdscope_pack(const int32_t *ids, int T, int k, int E, int32_t *counts
     pack_scatter_kernel<<<nchunk, 1024, 0, s>>>(ids, T, k, E, hist, nchunk, counts, offsets, perm_token, perm_pos,
                                                 row_of);
     return check_launch("pack_scatter_kernel");
+}
+
+// ---------------------------------------------------------------- no-allocation variant
+//
+// pdscope_pack_static: pdscope_pack whose multi-block path keeps its
+// per-chunk counts in a library-owned device array instead of a caller
+// workspace.  The count launch writes hist[c][e] for every chunk c < nchunk
+// and expert e < E before the scatter launch reads them, so nothing in the
+// array has to start at zero and a call never depends on what an earlier
+// call left there.  Every call on one GPU shares that GPU's array: calls that
+// overlap in time on one GPU race.
+constexpr int kPackStaticMaxIds = 1 << 20;
+constexpr int kPackStaticWords = (kPackStaticMaxIds / kChunkIds) * kPackMaxE;  // 512 KiB
+
+static __device__ __align__(256) int32_t scratch[kPackStaticWords];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static int32_t *g_scratch_ptr[kMaxDevices];
+
+// Device address of `scratch` on the current device, looked up once per
+// device with that device current (the array's host-side name is not a
+// device address and must never be passed to a kernel).
+static int pack_scratch(int32_t **out) {
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return fail(kEHip, std::string("pack_static: hipGetDevice: ") + hipGetErrorString(err));
+    if (dev < 0 || dev >= kMaxDevices) return fail(kEInval, "pack_static: device index out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (err != hipSuccess || !p)
+            return fail(kEHip, std::string("pack_static: hipGetSymbolAddress: ") + hipGetErrorString(err));
+        g_scratch_ptr[dev] = static_cast<int32_t *>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return kOk;
+}
+
+PD_API size_t pdscope_pack_static_max_ids(void) { return (size_t)kPackStaticMaxIds; }
+
+PD_API int pdscope_pack_static(const int32_t *ids, int T, int k, int E, int32_t *counts, int32_t *offsets,
+                               int32_t *perm_token, int32_t *perm_pos, int32_t *row_of, void *stream) {
+    if (!ids || !counts || !offsets || !perm_token || !perm_pos || !row_of)
+        return fail(kEInval, "pack_static: null pointer");
+    if (T < 1 || k < 1 || E < 1 || E > kPackMaxE)
+        return fail(kEInval, "pack_static: need T,k >= 1 and 1 <= E <= 256");
+    if ((int64_t)T * k > kPackStaticMaxIds)
+        return fail(kEInval, "pack_static: T*k exceeds the static scratch limit of 1048576 ids");
+    const int n = T * k;
+    if (n <= kPackMultiMin) return pdscope_pack(ids, T, k, E, counts, offsets, perm_token, perm_pos, row_of, nullptr,
+                                                stream);
+    int32_t *hist = nullptr;
+    const int rc = pack_scratch(&hist);
+    if (rc) return rc;
+    return pdscope_pack(ids, T, k, E, counts, offsets, perm_token, perm_pos, row_of, hist, stream);
 }
 
 PD_API int pdscope_schedule(const int32_t *counts, const int32_t *sel, int nsel, int block_m,

@@ -142,6 +142,27 @@ def pack(ids, E, out: Packed | None = None, workspace=None) -> Packed:
     return out
 
 
+def pack_static_max_ids() -> int:
+    return int(_lib.load().pdscope_pack_static_max_ids())
+
+
+def pack_static(ids, E, out: Packed) -> Packed:
+    """pack() through the entry point that allocates nothing (its multi-block
+    scratch is a library-owned device array; calls overlapping in time on
+    one GPU race).  All outputs are caller-provided."""
+    _need(ids, "ids", torch.int32, 2)
+    T, k = ids.shape
+    dev = ids.device
+    for t, n, size in ((out.counts, "counts", E), (out.offsets, "offsets", E + 1), (out.perm_token, "perm_token", T * k),
+                       (out.perm_pos, "perm_pos", T * k), (out.row_of, "row_of", T * k)):
+        _need(t, n, torch.int32, None, dev)
+        if t.numel() < size:
+            raise ValueError(f"{n} holds {t.numel()} entries, needs {size}")
+    _lib.call("pdscope_pack_static", _p(ids), T, k, E, _p(out.counts), _p(out.offsets), _p(out.perm_token),
+              _p(out.perm_pos), _p(out.row_of), _stream(dev))
+    return out
+
+
 def grouped_block_m(rows_hint: int, max_rows: int | None = None) -> int:
     """Row tile of the grouped SwiGLU launch for rows_hint mean rows per expert
     (and, when the host knows it, the largest expert's rows)."""
