@@ -178,17 +178,34 @@ int pdscope_merge(const void *y, const int32_t *row_of, const void *w, int T, in
                   const void *add_in, void *out, void *stream);
 
 /*
+ * A8 in the arithmetic of the reference's default merge (merge='reference',
+ * expertbench/pdscope_runtime.py:454-468: a zero output and one bf16
+ * index_add_ of parts[e] * coeff per expert, experts in ascending id).  A
+ * token meets an expert at most once, so per token its k rows are added in
+ * ascending expert id (= ascending grouped row):
+ *   acc = 0;  acc = bf16(acc + bf16(w[t,s] * y[row,:]))  for each row;
+ *   out[t,:] = add_in ? bf16(acc + add_in[t,:]) : acc    (add_in added last).
+ * Same arguments as pdscope_merge; deterministic, bit-exact with that
+ * sequence of index_add_ calls.
+ */
+int pdscope_merge_ordered(const void *y, const int32_t *row_of, const void *w, int T, int k, int H,
+                          const void *add_in, void *out, void *stream);
+
+/*
  * A4+A8 for one decode token (T == 1): replaces the per-expert decode
  * submissions (expertbench/pdscope_runtime.py:326-350, executor.py:454-488,
  * including the resident-graph replay of executor.py:113-138) and the merge.
  *   h_s  = bf16(bf16(silu(bf16(x.gate_s^T))) * bf16(x.up_s^T))  (h_ws [k,I])
- *   out  = bf16( sum_s w[s] * bf16(h_s . down_s^T) )            (out [H])
+ *   y_s  = bf16(h_s . down_s^T)
+ *   merge_mode 0: out = bf16( sum_s w[s] * y_s ), fp32 in slot order, one rounding
+ *   merge_mode 1: the y_s added in ascending expert id in bf16 arithmetic, as
+ *                 pdscope_merge_ordered (the reference's default merge)
  * for the k experts ids[0..k). Streaming GEMV, weights read once.
  * Limits: H % 8 == 0, H <= 4096, I % 8 == 0, k <= 16, k*I*2 <= 64 KiB.
  */
 int pdscope_swiglu_decode(const void *x, const int32_t *ids, const void *w, int k,
                           const void *const *slots, int H, int I, void *h_ws, void *out,
-                          void *stream);
+                          int merge_mode, void *stream);
 
 /*
  * A1+A4+A8 for one decode token in ONE launch: replaces route
@@ -196,7 +213,8 @@ int pdscope_swiglu_decode(const void *x, const int32_t *ids, const void *w, int 
  * (expertbench/pdscope_runtime.py:326-350, executor.py:454-488, including the
  * resident-graph replay of executor.py:113-138) and the merge
  * (pdscope_runtime.py:450-469).  Results are bitwise those of
- * pdscope_route_topk followed by pdscope_swiglu_decode (same arguments).
+ * pdscope_route_topk followed by pdscope_swiglu_decode (same arguments,
+ * merge_mode as there).
  * x [H], gate [E,H], bias [E] fp32 or NULL, logits [E] bf16, ids [k] int32,
  * weights [k] bf16, probs [E] fp32 or NULL, h_ws [k*I] bf16, out [H] bf16.
  * workspace: pdscope_decode_workspace_bytes() bytes, zero-filled once by the
@@ -213,8 +231,9 @@ int pdscope_swiglu_decode(const void *x, const int32_t *ids, const void *w, int 
 size_t pdscope_decode_workspace_bytes(void);
 int pdscope_decode_layer_supported(int H, int I, int E, int k);
 int pdscope_decode_layer(const void *x, const void *gate, const float *bias, int H, int E, int k,
-                         int normalize, const void *const *slots, int I, void *logits, int32_t *ids,
-                         void *weights, float *probs, void *h_ws, void *out, void *workspace, void *stream);
+                         int normalize, int merge_mode, const void *const *slots, int I, void *logits,
+                         int32_t *ids, void *weights, float *probs, void *h_ws, void *out, void *workspace,
+                         void *stream);
 
 /*
  * A7 demand staging: replaces the three per-projection non_blocking copies

@@ -278,6 +278,64 @@ void orc_merge(const uint16_t *y, const int32_t *row_of, const uint16_t *w, int 
         }
 }
 
+/* A8 reference merge and A9 GPU half: torch's bf16 index_add_, row by row.
+ * out[tokens[r], j] = bf16(out[tokens[r], j] + bf16(rows[r, j] * w[r]))
+ * for r = 0..n-1 in order, in bf16 arithmetic (each sum and product of two
+ * bf16 values formed in fp32 and rounded to nearest even, as
+ * c10::BFloat16's operators do).  Restates the per-expert merge
+ * output.index_add_(0, tokens, (parts[e] * coeff[:, None]).to(bf16)) of
+ * pdscope_runtime.py:466-468 applied expert by expert, and the
+ * out.index_add_(0, tokens, scratch * weights[:, None]) of
+ * native_layer_dispatch.cpp:88,129. */
+void orc_index_add_bf16(uint16_t *out, int H, const int64_t *tokens, const uint16_t *rows,
+                        const uint16_t *w, int64_t n) {
+    for (int64_t r = 0; r < n; ++r) {
+        uint16_t *o = out + (size_t)tokens[r] * H;
+        const uint16_t *y = rows + (size_t)r * H;
+        const float wr = orc_bf16_to_f32(w[r]);
+        for (int j = 0; j < H; ++j) {
+            const float prod = orc_bf16_to_f32(orc_f32_to_bf16(orc_bf16_to_f32(y[j]) * wr));
+            o[j] = orc_f32_to_bf16(orc_bf16_to_f32(o[j]) + prod);
+        }
+    }
+}
+
+/* The reference's default merge (merge='reference', pdscope_runtime.py:466-468)
+ * for one layer: out starts at zero and each expert's rows are index-added in
+ * ascending expert id.  A token meets each expert at most once, so per token
+ * this is its k weighted rows added one at a time in ascending expert id,
+ * i.e. in ascending grouped row (rows are grouped by expert ascending).
+ * add_in (nullable, shared experts) is added last, as a dense block adds its
+ * shared-expert output after the routed sum. */
+void orc_merge_ordered(const uint16_t *y, const int32_t *row_of, const uint16_t *w, int T, int k,
+                       int H, const uint16_t *add_in, uint16_t *out) {
+#pragma omp parallel for schedule(static)
+    for (int t = 0; t < T; ++t) {
+        int r[64], s_of[64];
+        for (int s = 0; s < k; ++s) {
+            r[s] = row_of[(size_t)t * k + s];
+            s_of[s] = s;
+        }
+        for (int a = 1; a < k; ++a) /* insertion sort by grouped row */
+            for (int b = a; b > 0 && r[b - 1] > r[b]; --b) {
+                int tr = r[b], ts = s_of[b];
+                r[b] = r[b - 1]; s_of[b] = s_of[b - 1];
+                r[b - 1] = tr; s_of[b - 1] = ts;
+            }
+        for (int j = 0; j < H; ++j) {
+            float acc = 0.0f;
+            for (int q = 0; q < k; ++q) {
+                const float wr = orc_bf16_to_f32(w[(size_t)t * k + s_of[q]]);
+                const float prod =
+                    orc_bf16_to_f32(orc_f32_to_bf16(orc_bf16_to_f32(y[(size_t)r[q] * H + j]) * wr));
+                acc = orc_bf16_to_f32(orc_f32_to_bf16(acc + prod));
+            }
+            if (add_in) acc = orc_bf16_to_f32(orc_f32_to_bf16(acc + orc_bf16_to_f32(add_in[(size_t)t * H + j])));
+            out[(size_t)t * H + j] = orc_f32_to_bf16(acc);
+        }
+    }
+}
+
 /* ---------------------------------------------------------------- layer */
 
 int orc_moe_layer(const uint16_t *x, int T, int H, int I, int E, int k, int normalize,

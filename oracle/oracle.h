@@ -71,6 +71,16 @@ void orc_expert_forward_fp(const uint16_t *x, int m, const uint16_t *wg, const u
 void orc_merge(const uint16_t *y, const int32_t *row_of, const uint16_t *w, int T, int k,
                int H, const uint16_t *add_in, uint16_t *out);
 
+/* torch bf16 index_add_ row by row: out[tokens[r]] = bf16(out + bf16(rows[r] * w[r])),
+ * r = 0..n-1 in order (pdscope_runtime.py:466-468, native_layer_dispatch.cpp:88,129). */
+void orc_index_add_bf16(uint16_t *out, int H, const int64_t *tokens, const uint16_t *rows,
+                        const uint16_t *w, int64_t n);
+
+/* The reference's default merge: per token its k weighted rows added in bf16, one
+ * at a time, in ascending expert id (= ascending grouped row); add_in added last. */
+void orc_merge_ordered(const uint16_t *y, const int32_t *row_of, const uint16_t *w, int T, int k,
+                       int H, const uint16_t *add_in, uint16_t *out);
+
 /* Whole layer: route -> pack -> experts -> merge.  slots[e] points at expert
  * e's gate|up|down block (row-major [I,H],[I,H],[H,I]).  Outputs are optional
  * (nullable) except out.  Returns 0/-1. */

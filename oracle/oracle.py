@@ -67,6 +67,11 @@ def lib():
         L.orc_merge.restype = None
         L.orc_merge.argtypes = [_u16p, _i32p, _u16p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                 _u16p, _u16p]
+        L.orc_index_add_bf16.restype = None
+        L.orc_index_add_bf16.argtypes = [_u16p, ctypes.c_int, _i64p, _u16p, _u16p, ctypes.c_int64]
+        L.orc_merge_ordered.restype = None
+        L.orc_merge_ordered.argtypes = [_u16p, _i32p, _u16p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                        _u16p, _u16p]
         L.orc_moe_layer.restype = ctypes.c_int
         L.orc_moe_layer.argtypes = [_u16p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                     ctypes.c_int, ctypes.c_int, _u16p, _f32p,
@@ -208,6 +213,36 @@ def merge(y, row_of, w, add_in=None):
     a = None if add_in is None else _u16(add_in)
     lib().orc_merge(_p(y, _u16p), _p(row_of, _i32p), _p(w, _u16p), T, k, H, _p(a, _u16p),
                     _p(out, _u16p))
+    return out
+
+
+def merge_ordered(y, row_of, w, add_in=None):
+    """The reference's default merge (pdscope_runtime.py:466-468): per token,
+    its k weighted rows added in bf16 in ascending expert id; add_in last."""
+    y, w = _u16(y), _u16(w)
+    row_of = np.ascontiguousarray(row_of, dtype=np.int32)
+    T, k = w.shape
+    H = y.shape[1]
+    if k > 64:
+        raise ValueError("merge_ordered: k <= 64")
+    out = np.empty((T, H), np.uint16)
+    a = None if add_in is None else _u16(add_in)
+    lib().orc_merge_ordered(_p(y, _u16p), _p(row_of, _i32p), _p(w, _u16p), T, k, H, _p(a, _u16p),
+                            _p(out, _u16p))
+    return out
+
+
+def index_add_bf16(out, tokens, rows, w):
+    """torch's bf16 index_add_ of rows * w into out, row by row (returns a new array)."""
+    out = np.array(_u16(out), copy=True)
+    rows, w = _u16(rows), _u16(w).reshape(-1)
+    tokens = np.ascontiguousarray(tokens, dtype=np.int64).reshape(-1)
+    n, H = rows.shape
+    if out.ndim != 2 or out.shape[1] != H or tokens.size != n or w.size != n:
+        raise ValueError("index_add_bf16: shapes")
+    if n and (tokens.min() < 0 or tokens.max() >= out.shape[0]):
+        raise ValueError("index_add_bf16: token index out of range")
+    lib().orc_index_add_bf16(_p(out, _u16p), H, _p(tokens, _i64p), _p(rows, _u16p), _p(w, _u16p), n)
     return out
 
 

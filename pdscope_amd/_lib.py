@@ -35,11 +35,12 @@ SIGNATURES = {
     "pdscope_swiglu_grouped_gateup": ([_vp, _vp, _vp, _vp, _i32, _vp, _i32, _i32, _vp, _i32, _i32, _vp, _vp], _i32),
     "pdscope_swiglu_grouped_down": ([_vp, _vp, _vp, _i32, _vp, _i32, _i32, _vp, _i32, _i32, _vp, _vp], _i32),
     "pdscope_merge": ([_vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp], _i32),
-    "pdscope_swiglu_decode": ([_vp, _vp, _vp, _i32, _vp, _i32, _i32, _vp, _vp, _vp], _i32),
+    "pdscope_merge_ordered": ([_vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp], _i32),
+    "pdscope_swiglu_decode": ([_vp, _vp, _vp, _i32, _vp, _i32, _i32, _vp, _vp, _i32, _vp], _i32),
     "pdscope_decode_workspace_bytes": ([], _sz),
     "pdscope_decode_layer_supported": ([_i32, _i32, _i32, _i32], _i32),
-    "pdscope_decode_layer": ([_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
-                              _vp], _i32),
+    "pdscope_decode_layer": ([_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
+                              _vp, _vp], _i32),
     "pdscope_stage_expert": ([_vp, _vp, _sz, _vp, _vp], _i32),
     "pdscope_stage_merge": ([_vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp], _i32),
     "pdscope_dispatch_pack": ([_vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp], _i32),

@@ -1,29 +1,42 @@
-"""Expert residency ledger: one byte-budgeted cache pool plus demand staging slots.
+"""Expert residency ledger: which expert copies live in HBM, and where.
 
-Host-side bookkeeping only (no tensors, no clocks), owned by one control
-thread.  It keeps the contract of expertbench/cache.py:136-662
-(``ExpertCache``) that the executor and runtime depend on:
+Host-side bookkeeping for one control thread (no tensors, clocks or device
+calls).  It honours the ExpertCache contract of expertbench/cache.py:136-662,
+on which the executor and runtime rely:
 
-* a load is reserved (``begin_load``), then its transfer is ``submit``-ted, then
-  ``complete_load`` is reported only after the copy's event has completed;
-* a copy that is computing is held by ``acquire`` until ``release`` (again only
-  after the compute event completed), so it can be neither evicted nor reused;
-* demand misses that cannot be admitted into the cache fall back to the
-  smallest free staging slot that fits (cache.py:531-537) and leave the ledger
-  when their single use is released (cache.py:621-624);
-* the true demand of one (request, step, layer) is declared first
-  (``on_demand``) and closed by ``end_demand`` once every expert completed on
-  the GPU (``release``) or the CPU (``finish_cpu``);
-* illegal transitions raise ``CacheError`` (``CapacityBlocked`` when a caller
-  must wait for work in flight or decline speculation).
+* one byte-budgeted cache pool plus a few demand-only staging slots, disjoint;
+* a copy is reserved (``begin_load``), its transfer submitted (``submit``),
+  and made usable by ``complete_load`` -- reported only after the copy's
+  event completed;
+* a copy feeding a computation is held (``acquire``) until ``release``, again
+  reported only once that computation completed; held copies are never
+  evicted or reused;
+* a demand miss that the cache cannot admit takes the smallest free staging
+  slot that fits (``min((capacity, index))``, cache.py:531-537) and leaves the
+  ledger when its single use is released;
+* the true demand of one (request, step, layer) is revealed first
+  (``on_demand``) and closed (``end_demand``) once each of its experts has
+  completed on the GPU (``release``) or the CPU (``finish_cpu``);
+* illegal transitions raise ``CacheError``; ``CapacityBlocked`` means the
+  caller must wait for work in flight or decline speculation, and a blocked
+  reservation changes nothing.
 
-Eviction order: LRU over demand ticks (ties by ExpertKey), or LFU
-(frequency, then tick, then key); copies protected by a retention hint
-sort after unprotected ones; ``static`` never evicts.
+Victim order when the cache pool must make room: LRU evicts the copy whose
+expert was demanded least recently (demand ticks; ties by ExpertKey), LFU
+the least frequently demanded (then least recently, then by key); copies
+under protection (an explicit set, or a next-layer retention hint) go only
+after every unprotected one; ``static`` never evicts.
+
+Design: every copy carries an explicit lifecycle phase; the evictable copies
+are kept in rankings -- buckets keyed by their rank (tick, or frequency and
+tick), each holding its keys sorted, plus the sorted list of live ranks --
+that are updated whenever a copy's eligibility or rank changes, so choosing
+victims walks the cheapest copies in order without scanning the pool.
 """
 from __future__ import annotations
 
-import heapq
+import bisect
+import itertools
 from collections import Counter
 from collections.abc import Mapping
 from dataclasses import dataclass, field
@@ -32,17 +45,19 @@ from uuid import uuid4
 
 
 class CacheError(ValueError):
-    """Illegal configuration, identity or lifecycle transition."""
+    """An illegal configuration, identity or lifecycle transition."""
 
 
 class CapacityBlocked(CacheError):
-    """Wait for transfers/uses in flight, or decline speculative work."""
+    """No room now: wait for transfers or uses in flight, or decline speculation."""
 
 
-def _nonneg_int(value, name, minimum=0):
-    if type(value) is not int or value < minimum:
-        raise CacheError(f"{name} must be an integer >= {minimum}")
+def _require_int(value, what, low=0):
+    if type(value) is not int or value < low:
+        raise CacheError(f"{what} must be an int >= {low}, got {value!r}")
 
+
+# ---------------------------------------------------------------- public records
 
 @dataclass(frozen=True, order=True)
 class ExpertKey:
@@ -51,23 +66,24 @@ class ExpertKey:
     representation: str
 
     def __post_init__(self):
-        _nonneg_int(self.layer, "layer")
-        _nonneg_int(self.expert, "expert")
+        _require_int(self.layer, "layer")
+        _require_int(self.expert, "expert")
         if not isinstance(self.representation, str) or not self.representation:
-            raise CacheError("representation must be explicit")
+            raise CacheError("an expert key names its representation")
 
 
 @dataclass(frozen=True)
 class DemandID:
+    """One revealed layer demand: (step, layer) increases within a request."""
     request: str
     step: int
     layer: int
 
     def __post_init__(self):
         if not isinstance(self.request, str) or not self.request:
-            raise CacheError("request must be a nonempty string")
-        _nonneg_int(self.step, "step")
-        _nonneg_int(self.layer, "layer")
+            raise CacheError("a demand names its request")
+        _require_int(self.step, "step")
+        _require_int(self.layer, "layer")
 
 
 @dataclass(frozen=True)
@@ -75,8 +91,8 @@ class LoadTicket:
     owner: str
     generation: int
     key: ExpertKey
-    pool: str          # "cache" or "demand_staging"
-    slot: int | None   # staging slot index, None for the cache pool
+    pool: str            # "cache" or "demand_staging"
+    slot: int | None     # staging slot index
 
 
 @dataclass(frozen=True)
@@ -90,7 +106,7 @@ class EntryView:
     key: ExpertKey
     nbytes: int
     pool: str
-    state: str
+    state: str           # "loading", "ready" or "in_use"
     ticket: LoadTicket
     submitted: bool
     users: int
@@ -107,411 +123,588 @@ class DemandObservation:
     nbytes: int
     state_at_reveal: str
     pool_at_reveal: str | None
-    hit_source: str | None
+    hit_source: str | None   # "history", "fresh_prefetch", "fresh_refresh" or None
 
     @property
     def ready_hit(self):
         return self.hit_source is not None
 
 
+@dataclass(frozen=True)
+class RetentionHint:
+    source: DemandID
+    target: DemandID
+    keys: frozenset
+
+
+# ---------------------------------------------------------------- internals
+
+RESERVED, IN_FLIGHT, READY = "reserved", "in_flight", "ready"
+
+
 @dataclass
-class _Copy:
+class _Residency:
+    """One device copy: its ticket, lifecycle phase and current holders."""
     ticket: LoadTicket
     nbytes: int
     origin: str
-    submitted: bool = False
-    ready: bool = False
+    phase: str = RESERVED
+    holders: set = field(default_factory=set)
     used: bool = False
     expired: bool = False
-    users: set = field(default_factory=set)
-    rev: int = 0
 
     @property
     def state(self):
-        if self.users:
+        if self.holders:
             return "in_use"
-        return "ready" if self.ready else "loading"
+        return "ready" if self.phase == READY else "loading"
 
 
 @dataclass
-class _Demand:
+class _Reveal:
     identity: DemandID
     counts: tuple
     valid: dict
     observations: tuple
-    remaining: set
+    open_keys: set
+
+
+class _Ranking:
+    """Keys ordered by (rank, key): one sorted bucket of keys per rank value
+    and the sorted list of ranks that have a non-empty bucket."""
+
+    def __init__(self):
+        self._rank_of = {}
+        self._buckets = {}
+        self._ranks = []
+
+    def __contains__(self, key):
+        return key in self._rank_of
+
+    def __len__(self):
+        return len(self._rank_of)
+
+    def put(self, key, rank):
+        if self._rank_of.get(key) == rank:
+            return
+        self.discard(key)
+        bucket = self._buckets.get(rank)
+        if bucket is None:
+            bucket = self._buckets[rank] = []
+            bisect.insort(self._ranks, rank)
+        bisect.insort(bucket, key)
+        self._rank_of[key] = rank
+
+    def discard(self, key):
+        rank = self._rank_of.pop(key, None)
+        if rank is None:
+            return
+        bucket = self._buckets[rank]
+        del bucket[bisect.bisect_left(bucket, key)]
+        if not bucket:
+            del self._buckets[rank]
+            del self._ranks[bisect.bisect_left(self._ranks, rank)]
+
+    def ascending(self):
+        for rank in list(self._ranks):
+            yield from list(self._buckets.get(rank, ()))
+
+    def clear(self):
+        self._rank_of.clear()
+        self._buckets.clear()
+        self._ranks.clear()
 
 
 class ExpertCache:
-    EVICTING = ("LRU", "LFU")
+    """Residency ledger with LRU, LFU or static replacement and staging fallback."""
+
+    POLICIES = ("static", "LRU", "LFU")
+    ORIGINS = ("initial", "demand", "prefetch")
 
     def __init__(self, expert_bytes, cache_bytes, staging_slot_bytes, *, policy="LRU", initial_hotset=()):
-        _nonneg_int(cache_bytes, "cache_bytes")
-        sizes = dict(expert_bytes)
-        if not sizes or not all(isinstance(k, ExpertKey) for k in sizes):
-            raise CacheError("expert_bytes must map ExpertKey to representation bytes")
-        for n in sizes.values():
-            _nonneg_int(n, "expert bytes", 1)
+        _require_int(cache_bytes, "cache_bytes")
+        registry = dict(expert_bytes)
+        if not registry or not all(isinstance(k, ExpertKey) for k in registry):
+            raise CacheError("expert_bytes must map every ExpertKey to its byte size")
+        for n in registry.values():
+            _require_int(n, "expert bytes", 1)
         slots = tuple(staging_slot_bytes)
         if not slots:
-            raise CacheError("at least one demand staging slot is required")
+            raise CacheError("the ledger needs at least one demand staging slot")
         for n in slots:
-            _nonneg_int(n, "staging slot bytes", 1)
-        if max(slots) < max(sizes.values()):
-            raise CacheError("demand staging cannot hold the largest expert; no forward progress")
+            _require_int(n, "staging slot bytes", 1)
+        if max(slots) < max(registry.values()):
+            raise CacheError("no staging slot holds the largest expert, so a miss could never be served")
         hot = tuple(initial_hotset)
-        if len(set(hot)) != len(hot) or any(k not in sizes for k in hot):
-            raise CacheError("initial hotset must contain unique registered keys")
-        if sum(sizes[k] for k in hot) > cache_bytes:
-            raise CacheError("initial hotset exceeds the cache byte budget")
-        if policy not in ("static", "LRU", "LFU"):
-            raise CacheError("policy must be static, LRU or LFU")
-        self.expert_bytes = MappingProxyType(sizes)
+        if len(set(hot)) != len(hot) or not set(hot) <= registry.keys():
+            raise CacheError("the initial hot set must list distinct registered experts")
+        if sum(registry[k] for k in hot) > cache_bytes:
+            raise CacheError("the initial hot set does not fit the cache budget")
+        if policy not in self.POLICIES:
+            raise CacheError(f"policy must be one of {self.POLICIES}")
+        self.expert_bytes = MappingProxyType(registry)
         self.cache_bytes = cache_bytes
         self.staging_slot_bytes = slots
         self.policy = policy
         self.initial_hotset = frozenset(hot)
         self._owner = uuid4().hex
-        self._serial = 0
-        self._copies: dict[ExpertKey, _Copy] = {}
-        self._staging_busy: set[int] = set()
-        self._cache_used = 0
-        self._active: _Demand | None = None
-        self._last_event: dict[str, tuple] = {}
-        self._tick: dict[ExpertKey, int] = {}
-        self._freq: Counter = Counter()
-        self._stats: Counter = Counter()
-        self._retired: list[LoadTicket] = []
-        self._heap: list = []
-        self._protected: frozenset = frozenset()
+        self._serials = itertools.count(1)      # tickets and use handles; never restarts
+        self._copies = {}
+        self._staging_busy = set()
+        self._cache_charged = 0
+        self._retired = []
+        self._reveal = None
+        self._closed = {}                       # request -> last closed (step, layer)
+        self._tick = 0                          # one per revealed layer demand
+        self._last_tick = {}
+        self._times_demanded = Counter()
+        self._counters = Counter()
+        self._unprotected = _Ranking()
+        self._protected_rank = _Ranking()
+        self._protected = frozenset()
+        self._hint = None
 
-    # ------------------------------------------------------------ queries
+    # ------------------------------------------------------------ lookups
 
-    def _known(self, key):
+    def _registered(self, key):
         if key not in self.expert_bytes:
-            raise CacheError(f"unknown expert: {key!r}")
+            raise CacheError(f"unregistered expert {key!r}")
 
-    def _copy_of(self, ticket):
-        c = self._copies.get(ticket.key)
-        if c is None or c.ticket != ticket:
-            raise CacheError("stale or foreign load ticket")
-        return c
+    def _copy_for(self, ticket):
+        copy = self._copies.get(ticket.key)
+        if copy is None or copy.ticket != ticket:
+            raise CacheError("the ticket belongs to no live copy of this ledger")
+        return copy
 
-    def _remaining(self, key):
-        return self._active is not None and key in self._active.remaining
+    def _open(self, key):
+        return self._reveal is not None and key in self._reveal.open_keys
+
+    def _require_open(self, key):
+        self._registered(key)
+        if not self._open(key):
+            raise CacheError(f"{key!r} is not an unfinished expert of the active demand")
 
     def lookup(self, key):
-        """Side-effect-free view of the current copy of `key` (or None)."""
-        self._known(key)
+        """The copy of `key` as it is now (None if absent); observing is not a demand."""
+        self._registered(key)
         c = self._copies.get(key)
         if c is None:
             return None
-        return EntryView(key, c.nbytes, c.ticket.pool, c.state, c.ticket, c.submitted, len(c.users), c.origin,
-                         c.used, c.expired)
+        return EntryView(key, c.nbytes, c.ticket.pool, c.state, c.ticket, c.phase != RESERVED, len(c.holders),
+                         c.origin, c.used, c.expired)
 
     @property
     def resident_payload_bytes(self):
-        return self._cache_used
+        return self._cache_charged
 
     @property
     def active_demand(self):
-        return None if self._active is None else self._active.identity
+        return None if self._reveal is None else self._reveal.identity
 
     @property
     def unfinished_demand_keys(self):
-        return tuple(sorted(self._active.remaining)) if self._active is not None else ()
+        return () if self._reveal is None else tuple(sorted(self._reveal.open_keys))
+
+    @property
+    def retention_hint(self):
+        return self._hint
 
     def stats(self):
-        return dict(self._stats)
+        """Event counters (counts and bytes of ledger events, never times)."""
+        return dict(self._counters)
 
     def memory(self):
         staged = [c for c in self._copies.values() if c.ticket.pool == "demand_staging"]
-        return dict(cache_capacity_bytes=self.cache_bytes, cache_payload_bytes=self._cache_used,
+        return dict(cache_capacity_bytes=self.cache_bytes, cache_payload_bytes=self._cache_charged,
                     staging_reserved_bytes=sum(self.staging_slot_bytes),
                     staging_payload_bytes=sum(c.nbytes for c in staged), staging_occupied_slots=len(staged),
-                    expert_reserved_bytes=self.cache_bytes + sum(self.staging_slot_bytes))
+                    expert_reserved_bytes=self.cache_bytes + sum(self.staging_slot_bytes),
+                    physical_allocation="executor_responsibility_not_measured_here")
 
-    def demand_frequency(self, key):
-        self._known(key)
-        return self._freq[key]
-
-    def take_retired(self):
-        """Copies whose device memory may now be reused (consumed once)."""
-        out = tuple(self._retired)
-        self._retired.clear()
+    def prefetch_inventory(self):
+        """Speculative copies by outcome: counts and bytes."""
+        spec = [c for c in self._copies.values() if c.origin == "prefetch"]
+        groups = dict(unused_ready=[c for c in spec if c.phase == READY and not c.used],
+                      unused_loading=[c for c in spec if c.phase != READY and not c.used],
+                      unused_expired=[c for c in spec if c.expired and not c.used],
+                      used_resident=[c for c in spec if c.used])
+        out = {}
+        for name, members in groups.items():
+            out[f"{name}_copies"] = len(members)
+            out[f"{name}_bytes"] = sum(c.nbytes for c in members)
         return out
 
-    # ------------------------------------------------------------ eviction
+    def demand_frequency(self, key):
+        self._registered(key)
+        return self._times_demanded[key]
 
-    def _evictable(self, c):
-        return (self.policy in self.EVICTING and c.ticket.pool == "cache" and c.ready and not c.users
-                and not self._remaining(c.ticket.key))
+    def take_retired(self):
+        """Tickets whose device storage the executor may now free or reuse."""
+        out, self._retired = tuple(self._retired), []
+        return out
 
-    def _priority(self, c):
-        key = c.ticket.key
-        tick = self._tick.get(key, 0)
-        base = (self._freq[key], tick, key) if self.policy == "LFU" else (tick, key)
-        return (key in self._protected,) + base
+    # ------------------------------------------------------------ replacement
 
-    def _push(self, key):
+    def _evictable(self, key, c):
+        return (self.policy in ("LRU", "LFU") and c.ticket.pool == "cache" and c.phase == READY
+                and not c.holders and not self._open(key))
+
+    def _rank(self, key):
+        tick = self._last_tick.get(key, 0)
+        return (self._times_demanded[key], tick) if self.policy == "LFU" else (tick,)
+
+    def _is_protected(self, key):
+        return key in self._protected or (self._hint is not None and key in self._hint.keys)
+
+    def _reindex(self, key):
+        """Place `key` in the ranking its copy belongs to now (or in none)."""
+        self._unprotected.discard(key)
+        self._protected_rank.discard(key)
         c = self._copies.get(key)
-        if c is not None and self._evictable(c):
-            c.rev += 1
-            heapq.heappush(self._heap, (self._priority(c), c.ticket.generation, c.rev, key))
-            if len(self._heap) > max(64, 4 * len(self._copies)):
-                self._heap = [(self._priority(x), x.ticket.generation, x.rev, x.ticket.key)
-                              for x in self._copies.values() if self._evictable(x)]
-                heapq.heapify(self._heap)
+        if c is not None and self._evictable(key, c):
+            target = self._protected_rank if self._is_protected(key) else self._unprotected
+            target.put(key, self._rank(key))
 
-    def _plan_victims(self, size):
-        """Evictable copies freeing enough bytes, or None.  Changes nothing."""
-        need = self._cache_used + size - self.cache_bytes
-        if need <= 0:
+    def _choose_victims(self, size):
+        """Cheapest evictable copies freeing room for `size` more bytes, or
+        None if even all of them would not suffice (nothing is changed)."""
+        short = self._cache_charged + size - self.cache_bytes
+        if short <= 0:
             return []
-        popped, chosen = [], []
-        while self._heap and need > 0:
-            node = heapq.heappop(self._heap)
-            popped.append(node)
-            prio, gen, rev, key = node
-            c = self._copies.get(key)
-            if c is None or c.ticket.generation != gen or c.rev != rev or not self._evictable(c):
-                continue
-            if prio != self._priority(c):
-                # priority changed since the node was queued: requeue it
-                c.rev += 1
-                heapq.heappush(self._heap, (self._priority(c), gen, c.rev, key))
-                continue
-            chosen.append(key)
-            need -= c.nbytes
-        for node in popped:
-            heapq.heappush(self._heap, node)
-        return chosen if need <= 0 else None
+        chosen = []
+        for ranking in (self._unprotected, self._protected_rank):
+            for key in ranking.ascending():
+                chosen.append(key)
+                short -= self._copies[key].nbytes
+                if short <= 0:
+                    return chosen
+        return None
 
     def _drop(self, key):
         c = self._copies.pop(key)
+        self._unprotected.discard(key)
+        self._protected_rank.discard(key)
         if c.ticket.pool == "cache":
-            self._cache_used -= c.nbytes
+            self._cache_charged -= c.nbytes
         else:
             self._staging_busy.discard(c.ticket.slot)
         self._retired.append(c.ticket)
         return c
 
-    def _evict(self, key):
+    def _evict_now(self, key):
         c = self._drop(key)
-        self._stats["evictions"] += 1
-        self._stats["evicted_bytes"] += c.nbytes
+        self._counters["evictions"] += 1
+        self._counters["evicted_bytes"] += c.nbytes
         if c.origin == "prefetch" and not c.used:
-            self._stats["unused_prefetch_evictions"] += 1
+            self._counters["unused_prefetch_evictions"] += 1
 
     def evict(self, key):
-        self._known(key)
+        self._registered(key)
         c = self._copies.get(key)
-        if c is None or not self._evictable(c):
-            raise CacheError("cannot evict an absent, static, loading, referenced or demanded copy")
-        self._evict(key)
+        if c is None or not self._evictable(key, c):
+            raise CacheError("only a ready, unheld, cached copy outside the active demand can be evicted")
+        self._evict_now(key)
 
     def set_protected(self, keys):
-        """Soft eviction preference: these copies are evicted last (next-layer forecast)."""
-        self._protected = frozenset(keys)
-        for k in self._protected:
-            self._push(k)
+        """Soft preference: these copies are evicted only after every other
+        one (e.g. a next-layer forecast); replaces the previous set."""
+        keys = frozenset(keys)
+        for key in keys:
+            self._registered(key)
+        before, self._protected = self._protected, keys
+        for key in before | keys:
+            self._reindex(key)
+
+    def set_retention_hint(self, source, target, keys):
+        """Protect forecast copies of the next layer of the active demand until
+        the next reveal (LRU only; cache.py:286-313 sets the same horizon).
+        Returns False when the same hint is already set."""
+        if (self.policy != "LRU" or self._reveal is None or self._reveal.identity != source
+                or not isinstance(target, DemandID)
+                or target != DemandID(source.request, source.step, source.layer + 1)):
+            raise CacheError("a retention hint needs an LRU ledger, the active demand as source and its next layer "
+                             "as target")
+        keys = tuple(keys)
+        if len(set(keys)) != len(keys):
+            raise CacheError("retention keys must be distinct")
+        for key in keys:
+            self._registered(key)
+            if key.layer != target.layer:
+                raise CacheError("a retention key must belong to the target layer")
+        hint = RetentionHint(source, target, frozenset(keys))
+        if self._hint is not None:
+            if self._hint == hint:
+                return False
+            raise CacheError("a different retention hint is already set")
+        self._hint = hint
+        for key in hint.keys:
+            self._reindex(key)
+        self._counters["retention_hint_updates"] += 1
+        self._counters["retention_hint_candidates"] += len(keys)
+        return True
+
+    def _drop_hint(self):
+        if self._hint is None:
+            return False
+        keys, self._hint = self._hint.keys, None
+        for key in keys:
+            self._reindex(key)
+        self._counters["retention_hint_expirations"] += 1
+        return True
+
+    def clear_retention_hint(self, request):
+        if self._reveal is not None or request not in self._closed:
+            raise CacheError("a hint is cleared only after its request's demand closed")
+        if self._hint is not None and self._hint.source.request != request:
+            raise CacheError("the retention hint belongs to another request")
+        return self._drop_hint()
 
     # ------------------------------------------------------------ demand
 
-    def on_demand(self, identity, token_counts, *, valid_token_counts=None):
-        """Declare the true demand of one (request, step, layer) before any work."""
-        if not isinstance(identity, DemandID):
-            raise CacheError("only true routing can declare a demand")
+    def on_demand(self, identity, token_counts, *, role="true", valid_token_counts=None):
+        """Reveal the experts one (request, step, layer) routes to and how many
+        tokens each serves; returns one observation per expert (sorted by key).
+        Repeating the active reveal with identical counts returns it again."""
+        if role != "true" or not isinstance(identity, DemandID):
+            raise CacheError("only a true routing reveals demand")
         if not isinstance(token_counts, Mapping):
-            raise CacheError("token_counts must map ExpertKey to token count")
+            raise CacheError("token counts must be a mapping expert -> tokens")
         counts = tuple(sorted(dict(token_counts).items()))
         if not counts:
-            raise CacheError("empty demands are not recorded")
+            raise CacheError("an empty demand cannot be revealed")
         for key, n in counts:
-            self._known(key)
+            self._registered(key)
             if key.layer != identity.layer:
-                raise CacheError("demand keys must belong to the revealed layer")
-            _nonneg_int(n, "tokens per expert", 1)
-        phys = dict(counts)
-        valid = dict(phys if valid_token_counts is None else valid_token_counts)
+                raise CacheError("every demanded expert belongs to the revealed layer")
+            _require_int(n, "tokens per expert", 1)
+        physical = dict(counts)
+        if valid_token_counts is not None and not isinstance(valid_token_counts, Mapping):
+            raise CacheError("valid token counts must be a mapping")
+        valid = dict(physical) if valid_token_counts is None else dict(valid_token_counts)
         for key, n in valid.items():
-            if key not in phys:
-                raise CacheError("valid demand has no physical execution")
-            _nonneg_int(n, "valid tokens", 1)
-            if n > phys[key]:
-                raise CacheError("valid tokens exceed physical tokens")
-        if self._active is not None:
-            if self._active.identity == identity and self._active.counts == counts and self._active.valid == valid:
-                return self._active.observations
-            raise CacheError("another or conflicting layer-step demand is active")
-        prev = self._last_event.get(identity.request)
-        if prev is not None and (identity.step, identity.layer) <= prev:
-            raise CacheError("duplicate or out-of-order demand event")
-        if not self._stats["physical_layer_events"] and any(
-                k not in self._copies or not self._copies[k].ready for k in self.initial_hotset):
-            raise CacheError("initial hotset must finish loading before the first demand")
-        old_protected, self._protected = self._protected, frozenset()
-        for k in old_protected:
-            self._push(k)
-        self._stats["physical_layer_events"] += 1
-        tick = self._stats["physical_layer_events"]
-        obs = []
-        for key, n in counts:
-            c = self._copies.get(key)
-            src = None
-            if c is not None and c.ready:
-                src = "fresh_prefetch" if (c.origin == "prefetch" and not c.used) else "history"
-            o = DemandObservation(key, n, valid.get(key, 0), self.expert_bytes[key],
-                                  c.state if c else "absent", c.ticket.pool if c else None, src)
-            obs.append(o)
-            self._stats["physical_expert_demands"] += 1
-            self._stats["physical_demand_tokens"] += n
+            if key not in physical:
+                raise CacheError("a valid count names an expert outside the demand")
+            _require_int(n, "valid tokens per expert", 1)
+            if n > physical[key]:
+                raise CacheError("valid tokens exceed routed tokens")
+        if self._reveal is not None:
+            r = self._reveal
+            if r.identity == identity and r.counts == counts and r.valid == valid:
+                return r.observations
+            raise CacheError("another layer demand is still open")
+        last = self._closed.get(identity.request)
+        if last is not None and (identity.step, identity.layer) <= last:
+            raise CacheError("demands of a request must arrive in increasing (step, layer) order")
+        if not self._counters["physical_layer_events"]:
+            missing = [k for k in self.initial_hotset
+                       if k not in self._copies or self._copies[k].phase != READY]
+            if missing:
+                raise CacheError("the initial hot set must be loaded before the first demand")
+        self._drop_hint()   # a hint covers one layer ahead only
+        observations = tuple(self._observe(key, n, valid.get(key, 0)) for key, n in counts)
+        self._tick += 1
+        self._count_reveal(observations)
+        for o in observations:
+            if o.valid_tokens:
+                self._times_demanded[o.key] += 1
+                self._last_tick[o.key] = self._tick
+        self._reveal = _Reveal(identity, counts, valid, observations, set(physical))
+        for key in physical:
+            self._reindex(key)  # open experts cannot be evicted
+        return observations
+
+    def _observe(self, key, tokens, valid_tokens):
+        c = self._copies.get(key)
+        source = None
+        if c is not None and c.phase == READY:
+            fresh = c.origin in ("prefetch", "refresh") and not c.used
+            source = f"fresh_{c.origin}" if fresh else "history"
+        return DemandObservation(key, tokens, valid_tokens, self.expert_bytes[key],
+                                 c.state if c is not None else "absent", c.ticket.pool if c is not None else None,
+                                 source)
+
+    def _count_reveal(self, observations):
+        n = self._counters
+        n["physical_layer_events"] += 1
+        n["demand_events"] += int(any(o.valid_tokens for o in observations))
+        for o in observations:
+            n["physical_expert_demands"] += 1
+            n["physical_demand_tokens"] += o.tokens
+            n["padding_token_assignments"] += o.tokens - o.valid_tokens
+            n["physical_ready_hits"] += int(o.ready_hit)
             if not o.valid_tokens:
+                n["padding_only_expert_demands"] += 1
                 continue
-            self._freq[key] += 1
-            self._tick[key] = tick
-            self._stats["expert_demands"] += 1
-            self._stats["demand_tokens"] += o.valid_tokens
-            self._stats["demand_bytes"] += o.nbytes
+            n["expert_demands"] += 1
+            n["demand_tokens"] += o.valid_tokens
+            n["demand_bytes"] += o.nbytes
             if o.ready_hit:
-                self._stats["ready_hits"] += 1
-                self._stats["history_ready_hits" if src == "history" else "fresh_prefetch_hits"] += 1
-                self._stats["cache_resident_hits" if o.pool_at_reveal == "cache" else "staging_ready_hits"] += 1
+                n["ready_hits"] += 1
+                n[f"{o.hit_source}_hits" if o.hit_source != "history" else "history_ready_hits"] += 1
+                n["ready_hit_tokens"] += o.valid_tokens
+                n["ready_hit_bytes"] += o.nbytes
+                n["cache_resident_hits" if o.pool_at_reveal == "cache" else "staging_ready_hits"] += 1
             else:
-                self._stats["loading_misses" if o.state_at_reveal == "loading" else "absent_misses"] += 1
-        self._active = _Demand(identity, counts, valid, tuple(obs), {k for k, _ in counts})
-        return self._active.observations
+                n["loading_misses" if o.state_at_reveal in ("loading", "in_use") else "absent_misses"] += 1
 
     def end_demand(self, identity):
-        if self._active is None or self._active.identity != identity:
-            raise CacheError("no matching active demand")
-        if self._active.remaining:
-            raise CacheError("cannot finish the layer: some demanded experts have not completed")
-        self._last_event[identity.request] = (identity.step, identity.layer)
-        done = self._active.counts
-        self._active = None
-        for key, _ in done:
-            self._push(key)
+        r = self._reveal
+        if r is None or r.identity != identity:
+            raise CacheError("that demand is not the open one")
+        if r.open_keys:
+            raise CacheError("the demand still has unfinished experts")
+        self._closed[identity.request] = (identity.step, identity.layer)
+        self._reveal = None
 
-    # ------------------------------------------------------------ loads
+    # ------------------------------------------------------------ transfers
+
+    def _free_staging_slot(self, size):
+        fits = [(cap, i) for i, cap in enumerate(self.staging_slot_bytes)
+                if cap >= size and i not in self._staging_busy]
+        return min(fits)[1] if fits else None
 
     def begin_load(self, key, *, origin="demand", admit=True):
-        """Reserve one copy (cache pool, or a staging slot for demand misses)."""
-        self._known(key)
-        if origin not in ("initial", "demand", "prefetch"):
-            raise CacheError("unknown load origin")
+        """Reserve one device copy of `key` (the existing ticket if it has one).
+        initial: the pre-run hot set; demand: an open expert, into the cache or
+        (admit=False, or no room) a staging slot; prefetch: a cache copy of an
+        expert outside the open demand."""
+        self._registered(key)
+        if origin not in self.ORIGINS:
+            raise CacheError(f"load origin must be one of {self.ORIGINS}")
         if type(admit) is not bool or (not admit and origin != "demand"):
-            raise CacheError("non-admission is a demand-only option")
+            raise CacheError("admit=False applies to demand loads only")
         if origin == "demand":
-            if not self._remaining(key):
-                raise CacheError("demand load for an expert outside the active demand")
+            self._require_open(key)
         elif origin == "initial":
-            if self._stats["physical_layer_events"] or self._active is not None or key not in self.initial_hotset:
-                raise CacheError("initial loads are limited to the declared hotset before the first demand")
-        elif self.policy == "static" or self._remaining(key):
-            raise CacheError("prefetch is not allowed for a static cache or an already revealed demand")
-        existing = self._copies.get(key)
-        if existing is not None:
-            return existing.ticket
+            if self._counters["physical_layer_events"] or self._reveal is not None or key not in self.initial_hotset:
+                raise CacheError("initial loads are the declared hot set, before any demand")
+        elif self.policy == "static" or self._open(key):
+            raise CacheError("prefetch needs a replacing policy and an expert outside the open demand")
+        if key in self._copies:
+            return self._copies[key].ticket
         size = self.expert_bytes[key]
         victims = None
-        if admit and (self.policy in self.EVICTING or origin == "initial"):
-            victims = self._plan_victims(size)
+        if admit and (self.policy != "static" or origin == "initial"):
+            victims = self._choose_victims(size)
+        slot = None
         if victims is not None:
-            pool, slot = "cache", None
+            pool = "cache"
         elif origin == "demand":
-            free = [(cap, i) for i, cap in enumerate(self.staging_slot_bytes)
-                    if i not in self._staging_busy and cap >= size]
-            if not free:
-                raise CapacityBlocked("demand staging busy: finish transfers/uses in flight first")
-            pool, slot = "demand_staging", min(free)[1]
+            slot = self._free_staging_slot(size)
+            if slot is None:
+                raise CapacityBlocked("every fitting staging slot is busy; finish a transfer or use first")
+            pool = "demand_staging"
         else:
-            raise CapacityBlocked("no evictable cache bytes; speculation cannot use demand staging")
-        for v in victims or ():
-            self._evict(v)
-        self._serial += 1
-        ticket = LoadTicket(self._owner, self._serial, key, pool, slot)
-        self._copies[key] = _Copy(ticket, size, origin)
+            raise CapacityBlocked("the cache has no evictable room and speculation may not use staging")
+        for victim in victims or ():
+            self._evict_now(victim)
+        ticket = LoadTicket(self._owner, next(self._serials), key, pool, slot)
+        self._copies[key] = _Residency(ticket, size, origin)
         if pool == "cache":
-            self._cache_used += size
+            self._cache_charged += size
         else:
             self._staging_busy.add(slot)
         return ticket
 
     def submit(self, ticket):
-        c = self._copy_of(ticket)
-        if c.submitted or c.ready:
-            raise CacheError("transfer already submitted")
-        if c.origin == "prefetch" and self._remaining(ticket.key):
+        """The transfer of this reservation has been issued."""
+        c = self._copy_for(ticket)
+        if c.phase != RESERVED:
+            raise CacheError("this transfer was already submitted")
+        if c.origin == "prefetch" and self._open(ticket.key):
+            # the forecast was overtaken by the true demand: its copy is demand work
             c.origin, c.expired = "demand", True
-        c.submitted = True
-        self._stats[f"{c.origin}_loads_submitted"] += 1
-        self._stats["h2d_bytes_submitted"] += c.nbytes
+        c.phase = IN_FLIGHT
+        self._counters[f"{c.origin}_loads_submitted"] += 1
+        self._counters["h2d_bytes_submitted"] += c.nbytes
+        if c.origin == "demand" and self._reveal is not None and ticket.key not in self._reveal.valid:
+            self._counters["padding_only_h2d_bytes_submitted"] += c.nbytes
 
     def complete_load(self, ticket):
-        """Report that this generation's copy has landed (event completed)."""
-        c = self._copy_of(ticket)
-        if not c.submitted or c.ready:
-            raise CacheError("completion needs one submitted, incomplete transfer")
-        c.ready = True
-        self._stats["h2d_bytes_completed"] += c.nbytes
-        self._push(ticket.key)
+        """The transfer of this exact copy has landed."""
+        c = self._copy_for(ticket)
+        if c.phase != IN_FLIGHT:
+            raise CacheError("only a submitted, unfinished transfer can complete")
+        c.phase = READY
+        self._counters["h2d_bytes_completed"] += c.nbytes
+        self._reindex(ticket.key)
+
+    def expire_prefetch(self, ticket):
+        """Give up a forecast copy: an unsubmitted one outside the open demand
+        is dropped; one the demand adopted becomes demand work."""
+        c = self._copy_for(ticket)
+        if c.expired:
+            return False
+        if c.origin != "prefetch":
+            raise CacheError("only speculative copies expire")
+        c.expired = True
+        self._counters["prefetch_expirations"] += 1
+        if c.phase == RESERVED:
+            if not self._open(ticket.key):
+                self._drop(ticket.key)
+                return True
+            c.origin = "demand"
+        return False
 
     # ------------------------------------------------------------ uses
 
     def acquire(self, key):
-        """Hold a ready copy for GPU compute; pairs with release()."""
-        if not self._remaining(key):
-            raise CacheError("expert is not an unfinished member of the active demand")
+        """Hold a ready copy of an open expert for a computation."""
+        self._require_open(key)
         c = self._copies.get(key)
-        if c is None or not c.ready:
-            raise CacheError("weights are not ready; a loading copy is not a hit")
-        self._serial += 1
-        c.users.add(self._serial)
-        return UseHandle(c.ticket, self._serial)
+        if c is None or c.phase != READY:
+            raise CacheError("no ready copy to compute with (a loading copy is not a hit)")
+        handle = UseHandle(c.ticket, next(self._serials))
+        c.holders.add(handle.serial)
+        self._reindex(key)
+        return handle
 
     def release(self, handle):
-        """Report completed GPU compute; the last release completes the expert."""
-        c = self._copy_of(handle.ticket)
-        if handle.serial not in c.users:
-            raise CacheError("stale, foreign or already released use handle")
-        c.users.remove(handle.serial)
+        """The computation holding this copy has completed; the last release of
+        an expert completes it for the open demand (a staged copy then leaves)."""
+        c = self._copy_for(handle.ticket)
+        if handle.serial not in c.holders:
+            raise CacheError("the use handle is stale, foreign or already released")
         key = handle.ticket.key
-        c.used = c.used or key in self._active.valid
-        if c.users:
+        c.holders.discard(handle.serial)
+        valid = key in self._reveal.valid
+        c.used = c.used or valid
+        if c.holders:
             return
-        self._active.remaining.discard(key)
-        self._stats["gpu_completed_experts"] += 1
-        self._stats["gpu_completed_valid_experts"] += int(key in self._active.valid)
-        if handle.ticket.pool == "demand_staging":
-            self._drop(key)  # a staged miss never stays resident
+        self._reveal.open_keys.discard(key)
+        self._counters["gpu_completed_experts"] += 1
+        self._counters["gpu_completed_valid_experts"] += int(valid)
+        if c.ticket.pool == "demand_staging":
+            self._drop(key)
         else:
-            self._push(key)
+            self._reindex(key)
 
     def finish_cpu(self, key):
-        """The CPU consumed the master copy of `key`; no GPU copy is admitted."""
-        if not self._remaining(key):
-            raise CacheError("expert is not an unfinished member of the active demand")
+        """The expert of the open demand was computed on the CPU from its master."""
+        self._require_open(key)
         c = self._copies.get(key)
-        if c is not None and (c.users or (c.origin == "demand" and not c.ready)):
-            raise CacheError("cannot switch an active GPU use/load to CPU completion")
-        if c is not None and c.ticket.pool == "demand_staging":
-            raise CacheError("a staged copy must complete through the GPU")
-        self._active.remaining.discard(key)
-        self._stats["cpu_completed_experts"] += 1
-        self._stats["cpu_completed_valid_experts"] += int(key in self._active.valid)
-        self._push(key)
+        if c is not None:
+            if c.holders or (c.origin == "demand" and c.phase != READY):
+                raise CacheError("a held copy or a demand transfer in flight cannot turn into CPU work")
+            if c.ticket.pool == "demand_staging":
+                raise CacheError("a staged copy is consumed by its GPU release")
+        self._reveal.open_keys.discard(key)
+        self._counters["cpu_completed_experts"] += 1
+        self._counters["cpu_completed_valid_experts"] += int(key in self._reveal.valid)
+        self._reindex(key)
 
     def reset(self):
-        if self._active is not None or any(not c.ready or c.users for c in self._copies.values()):
-            raise CacheError("cannot reset with active demands, loads or uses")
+        """Forget residency, history and counters once nothing is in flight or held."""
+        if self._reveal is not None or any(c.phase != READY or c.holders for c in self._copies.values()):
+            raise CacheError("reset needs no open demand, transfer or use")
         self._retired.extend(c.ticket for c in self._copies.values())
         self._copies.clear()
-        self._cache_used = 0
         self._staging_busy.clear()
-        self._heap.clear()
-        self._last_event.clear()
-        self._tick.clear()
-        self._freq.clear()
-        self._stats.clear()
-        self._protected = frozenset()
+        self._cache_charged = 0
+        self._closed.clear()
+        self._last_tick.clear()
+        self._times_demanded.clear()
+        self._counters.clear()
+        self._unprotected.clear()
+        self._protected_rank.clear()
+        self._hint = None

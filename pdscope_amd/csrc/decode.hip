@@ -12,8 +12,12 @@
 // Launch 2 (down + merge): each 32-lane half-wave owns one expert row of
 //   down_s (I bf16); a wave walks the k experts in pairs for its output
 //   column j, rounds each expert's y to bf16 (the expert output dtype) and
-//   accumulates w_s * y_s in fp32 in slot order.  h (k*I bf16) is staged in
-//   LDS once per block.  out[j] = bf16(sum_s w_s * y_s[j]).
+//   accumulates w_s * y_s in fp32 in slot order (merge_mode 0:
+//   out[j] = bf16(sum_s w_s * y_s[j]), one rounding), or keeps the y_s and
+//   adds them in ascending expert id in bf16 arithmetic (merge_mode 1, the
+//   reference's merge, expertbench/pdscope_runtime.py:466-468:
+//   acc = bf16(acc + bf16(w_s * y_s[j]))).  h (k*I bf16) is staged in LDS
+//   once per block.
 #include "common.h"
 
 namespace pd {
@@ -79,8 +83,10 @@ __global__ __launch_bounds__(256) void decode_down_kernel(const uint16_t *__rest
                                                           const int32_t *__restrict__ ids,
                                                           const uint16_t *__restrict__ w,
                                                           const uint16_t *const *__restrict__ slots, int H,
-                                                          int I, int k, uint16_t *__restrict__ out) {
+                                                          int I, int k, int merge_mode,
+                                                          uint16_t *__restrict__ out) {
     extern __shared__ uint4 s_h[];
+    __shared__ float s_ys[4][16];  // per wave: bf16 y of each slot (merge_mode 1)
     const int CI = I >> 3;
     for (int idx = threadIdx.x; idx < k * CI; idx += blockDim.x)
         s_h[idx] = reinterpret_cast<const uint4 *>(h_ws)[idx];
@@ -114,6 +120,25 @@ __global__ __launch_bounds__(256) void decode_down_kernel(const uint16_t *__rest
         if (lane == 0) {
             total = __builtin_fmaf(bf2f(w[p]), bf16_round(even), total);
             if (p + 1 < k) total = __builtin_fmaf(bf2f(w[p + 1]), bf16_round(odd), total);
+            s_ys[threadIdx.x >> 6][p] = bf16_round(even);
+            if (p + 1 < k) s_ys[threadIdx.x >> 6][p + 1] = bf16_round(odd);
+        }
+    }
+    if (lane == 0 && merge_mode) {
+        const float *ys = s_ys[threadIdx.x >> 6];
+        total = 0.0f;
+        int prev = -1;
+        for (int n = 0; n < k; ++n) {  // the next larger expert id each round
+            int best = 0x7fffffff, bs = 0;
+            for (int s = 0; s < k; ++s) {
+                const int e = ids[s];
+                if (e > prev && e < best) {
+                    best = e;
+                    bs = s;
+                }
+            }
+            prev = best;
+            total = bf16_round(total + bf16_round(bf2f(w[bs]) * ys[bs]));
         }
     }
     if (lane == 0) out[j] = (uint16_t)f2bf(total);
@@ -125,8 +150,9 @@ using namespace pd;
 
 PD_API int pdscope_swiglu_decode(const void *x, const int32_t *ids, const void *w, int k,
                                  const void *const *slots, int H, int I, void *h_ws, void *out,
-                                 void *stream) {
+                                 int merge_mode, void *stream) {
     if (!x || !ids || !w || !slots || !h_ws || !out) return fail(kEInval, "decode: null pointer");
+    if (merge_mode != 0 && merge_mode != 1) return fail(kEInval, "decode: merge_mode must be 0 or 1");
     if (k < 1 || k > 16) return fail(kEInval, "decode: need 1 <= k <= 16");
     if (H < 8 || H % 8 || H > 4096) return fail(kEInval, "decode: need H % 8 == 0 and H <= 4096");
     if (I < 8 || I % 8 || I > 8192) return fail(kEInval, "decode: need I % 8 == 0 and I <= 8192");
@@ -155,14 +181,14 @@ PD_API int pdscope_swiglu_decode(const void *x, const int32_t *ids, const void *
 #define PD_DN(C)                                                                                           \
     case C:                                                                                                \
         decode_down_kernel<C><<<dblocks, 256, lds, s>>>((const uint16_t *)h_ws, ids, (const uint16_t *)w, sp, H, \
-                                                        I, k, (uint16_t *)out);                            \
+                                                        I, k, merge_mode, (uint16_t *)out);                \
         break;
         PD_DN(1) PD_DN(2) PD_DN(3) PD_DN(4) PD_DN(5) PD_DN(6) PD_DN(7) PD_DN(8)
 #undef PD_DN
     default:
         if (cpl <= 32) {
             decode_down_kernel<32><<<dblocks, 256, lds, s>>>((const uint16_t *)h_ws, ids, (const uint16_t *)w, sp,
-                                                             H, I, k, (uint16_t *)out);
+                                                             H, I, k, merge_mode, (uint16_t *)out);
         } else {
             return fail(kEInval, "decode: unsupported I");
         }

@@ -17,8 +17,11 @@
 //   4. gate/up dot products -> h; then the wave issues its down-projection
 //      rows (two slots x four output columns), which land while h is
 //      handed between blocks;
-//   5. every block collects all of h, finishes its down rows and merges in
-//      slot order: out[j] = bf16(sum_s w_s * bf16(h_s . down_s[j])).
+//   5. every block collects all of h, finishes its down rows and merges:
+//      merge_mode 0: out[j] = bf16(sum_s w_s * y_s[j]) in fp32, slot order,
+//      one rounding; merge_mode 1 (the reference's merge arithmetic,
+//      expertbench/pdscope_runtime.py:466-468): y_s added in ascending
+//      expert id, acc = bf16(acc + bf16(w_s * y_s[j])); y_s = bf16(h_s . down_s[j]).
 //
 // Cross-block hand-off without read-modify-write atomics.  Same-address
 // atomics from hundreds of blocks serialise at the memory side (~14 ns
@@ -151,7 +154,8 @@ __device__ __forceinline__ void collect(const uint32_t *w, int count, int t, int
 template <int NCH, int P, int DC>
 __global__ __launch_bounds__(256, 2) void decode_layer_kernel(
     const uint16_t *__restrict__ x, const uint16_t *__restrict__ gate, const float *__restrict__ bias, int H,
-    int E, int k, int normalize, const uint16_t *const *__restrict__ slots, int I, uint16_t *__restrict__ logits,
+    int E, int k, int normalize, int merge_mode, const uint16_t *const *__restrict__ slots, int I,
+    uint16_t *__restrict__ logits,
     int32_t *__restrict__ ids, uint16_t *__restrict__ weights, float *__restrict__ probs,
     uint16_t *__restrict__ h_ws, uint16_t *__restrict__ out, uint32_t *ws) {
     extern __shared__ uint4 s_h[];       // k * I bf16
@@ -348,11 +352,27 @@ __global__ __launch_bounds__(256, 2) void decode_layer_kernel(
         if (hl == 31 && slot < k) s_y[slot * 4 + c4] = bf16_round(acc[c4]);
     }
     __syncthreads();
-    // merge in slot order, one lane per column
+    // merge, one lane per column
     if (tid < 4) {
         const int col = blockIdx.x * 4 + tid;
         float total = 0.0f;
-        for (int s2 = 0; s2 < k; ++s2) total = __builtin_fmaf(bf2f(s_tk.selw[s2]), s_y[s2 * 4 + tid], total);
+        if (merge_mode) {
+            int prev = -1;
+            for (int n = 0; n < k; ++n) {  // the next larger expert id each round
+                int best = 0x7fffffff, bs = 0;
+                for (int s2 = 0; s2 < k; ++s2) {
+                    const int e = s_tk.seli[s2];
+                    if (e > prev && e < best) {
+                        best = e;
+                        bs = s2;
+                    }
+                }
+                prev = best;
+                total = bf16_round(total + bf16_round(bf2f(s_tk.selw[bs]) * s_y[bs * 4 + tid]));
+            }
+        } else {
+            for (int s2 = 0; s2 < k; ++s2) total = __builtin_fmaf(bf2f(s_tk.selw[s2]), s_y[s2 * 4 + tid], total);
+        }
         if (col < H) out[col] = (uint16_t)f2bf(total);
     }
     // outputs off the critical path: the logits (block 0, from the collected
@@ -366,7 +386,7 @@ __global__ __launch_bounds__(256, 2) void decode_layer_kernel(
     if (tid == 0) __hip_atomic_store(ws + kWsEpoch + blockIdx.x, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-typedef void (*DecodeLayerFn)(const uint16_t *, const uint16_t *, const float *, int, int, int, int,
+typedef void (*DecodeLayerFn)(const uint16_t *, const uint16_t *, const float *, int, int, int, int, int,
                               const uint16_t *const *, int, uint16_t *, int32_t *, uint16_t *, float *, uint16_t *,
                               uint16_t *, uint32_t *);
 
@@ -455,8 +475,8 @@ PD_API int pdscope_decode_layer_supported(int H, int I, int E, int k) {
 }
 
 PD_API int pdscope_decode_layer(const void *x, const void *gate, const float *bias, int H, int E, int k,
-                                int normalize, const void *const *slots, int I, void *logits, int32_t *ids,
-                                void *weights, float *probs, void *h_ws, void *out, void *workspace,
+                                int normalize, int merge_mode, const void *const *slots, int I, void *logits,
+                                int32_t *ids, void *weights, float *probs, void *h_ws, void *out, void *workspace,
                                 void *stream) {
     if (!x || !gate || !slots || !logits || !ids || !weights || !h_ws || !out || !workspace)
         return fail(kEInval, "decode_layer: null pointer");
@@ -464,6 +484,7 @@ PD_API int pdscope_decode_layer(const void *x, const void *gate, const float *bi
     if (I < 8 || I % 8) return fail(kEInval, "decode_layer: need I % 8 == 0");
     if (E < 2 || E > kDecodeMaxE || E % 2) return fail(kEInval, "decode_layer: need even E <= 256");
     if (k < 1 || k > kDecodeMaxK || k > E) return fail(kEInval, "decode_layer: need 1 <= k <= min(E, 8)");
+    if (merge_mode != 0 && merge_mode != 1) return fail(kEInval, "decode_layer: merge_mode must be 0 or 1");
     if ((size_t)I > (size_t)E * H) return fail(kEInval, "decode_layer: need I <= E*H");
     if ((size_t)k * I * 2 > 64 * 1024) return fail(kEInval, "decode_layer: k*I*2 must fit 64 KiB of LDS");
     if ((E + 3) / 4 > (H + 3) / 4) return fail(kEInval, "decode_layer: need E <= H");
@@ -476,7 +497,8 @@ PD_API int pdscope_decode_layer(const void *x, const void *gate, const float *bi
         return fail(kEInval, "decode_layer: the grid would not be resident at once on this device");
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     plan.fn<<<plan.blocks, 256, plan.lds, s>>>(
-        (const uint16_t *)x, (const uint16_t *)gate, bias, H, E, k, normalize, (const uint16_t *const *)slots, I,
+        (const uint16_t *)x, (const uint16_t *)gate, bias, H, E, k, normalize, merge_mode,
+        (const uint16_t *const *)slots, I,
         (uint16_t *)logits, ids, (uint16_t *)weights, probs, (uint16_t *)h_ws, (uint16_t *)out,
         (uint32_t *)workspace);
     return check_launch("decode_layer_kernel");

@@ -4,6 +4,14 @@
 //               expertbench/pdscope_runtime.py:450-469 as a gather: each
 //               thread owns 8 output columns of one token and sums its k
 //               rows in fp32, slot order, rounding once (no atomics).
+//   merge_ordered restates the default per-expert merge of
+//               pdscope_runtime.py:466-468 (merge='reference'): a token's k
+//               rows are added in ascending expert id, each product rounded
+//               to bf16 and each sum rounded to bf16, exactly as the
+//               reference's sequence of per-expert bf16 index_add_ calls
+//               (a token occurs once per expert, so each call is one add).
+//               Grouped rows are sorted by expert, so ascending expert id is
+//               ascending grouped row.
 //   stage_merge restates native/native_layer_dispatch.cpp:83-88 (copy the
 //               CPU block to device scratch, then index_add_ of
 //               scratch * weights into out) in bf16 arithmetic, rows in order.
@@ -15,7 +23,9 @@ namespace pd {
 // loaded before the first is used (two memory latencies per output chunk
 // instead of 2k); KM == 0: any k, one slot at a time.  The fp32
 // accumulation is the same in both: slot order, one rounding.
-template <int KM>
+// ORDERED: the reference's arithmetic instead -- rows in ascending grouped
+// row, acc = bf16(acc + bf16(w * y)) per row, add_in added last.
+template <int KM, bool ORDERED>
 __global__ __launch_bounds__(256) void merge_kernel(const uint16_t *__restrict__ y,
                                                     const int32_t *__restrict__ row_of,
                                                     const uint16_t *__restrict__ w, int T, int k, int H,
@@ -27,7 +37,10 @@ __global__ __launch_bounds__(256) void merge_kernel(const uint16_t *__restrict__
          idx += (int64_t)gridDim.x * blockDim.x) {
         const int t = (int)(idx / CH), c = (int)(idx - (int64_t)t * CH);
         float acc[8];
-        if (add_in) {
+        if (ORDERED) {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) acc[q] = 0.0f;
+        } else if (add_in) {
             const uint4 v = reinterpret_cast<const uint4 *>(add_in + (size_t)t * H)[c];
             acc[0] = lo_bf(v.x); acc[1] = hi_bf(v.x); acc[2] = lo_bf(v.y); acc[3] = hi_bf(v.y);
             acc[4] = lo_bf(v.z); acc[5] = hi_bf(v.z); acc[6] = lo_bf(v.w); acc[7] = hi_bf(v.w);
@@ -36,6 +49,13 @@ __global__ __launch_bounds__(256) void merge_kernel(const uint16_t *__restrict__
             for (int q = 0; q < 8; ++q) acc[q] = 0.0f;
         }
         auto add = [&](float ws, uint4 v) __attribute__((always_inline)) {
+            if constexpr (ORDERED) {
+                const float yv[8] = {lo_bf(v.x), hi_bf(v.x), lo_bf(v.y), hi_bf(v.y),
+                                     lo_bf(v.z), hi_bf(v.z), lo_bf(v.w), hi_bf(v.w)};
+#pragma unroll
+                for (int q = 0; q < 8; ++q) acc[q] = bf16_round(acc[q] + bf16_round(ws * yv[q]));
+                return;
+            }
             acc[0] = __builtin_fmaf(ws, lo_bf(v.x), acc[0]);
             acc[1] = __builtin_fmaf(ws, hi_bf(v.x), acc[1]);
             acc[2] = __builtin_fmaf(ws, lo_bf(v.y), acc[2]);
@@ -53,6 +73,22 @@ __global__ __launch_bounds__(256) void merge_kernel(const uint16_t *__restrict__
                 r[s] = s < k ? row_of[(size_t)t * k + s] : 0;
                 ws[s] = s < k ? bf2f(w[(size_t)t * k + s]) : 0.0f;
             }
+            if constexpr (ORDERED) {
+                // ascending grouped row (= ascending expert id): compare-exchange
+                // passes over the live entries, indices static after unrolling
+#pragma unroll
+                for (int a = 1; a < KM; ++a)
+#pragma unroll
+                    for (int b = KM - 1; b >= a; --b)
+                        if (b < k && r[b - 1] > r[b]) {
+                            const int tr = r[b];
+                            r[b] = r[b - 1];
+                            r[b - 1] = tr;
+                            const float tw = ws[b];
+                            ws[b] = ws[b - 1];
+                            ws[b - 1] = tw;
+                        }
+            }
             uint4 v[KM];
 #pragma unroll
             for (int s = 0; s < KM; ++s)
@@ -60,11 +96,33 @@ __global__ __launch_bounds__(256) void merge_kernel(const uint16_t *__restrict__
 #pragma unroll
             for (int s = 0; s < KM; ++s)
                 if (s < k) add(ws[s], v[s]);
+        } else if constexpr (ORDERED) {
+            // any k: the next larger grouped row each round
+            int prev = -1;
+            for (int n = 0; n < k; ++n) {
+                int best = 0x7fffffff, bs = 0;
+                for (int s = 0; s < k; ++s) {
+                    const int r = row_of[(size_t)t * k + s];
+                    if (r > prev && r < best) {
+                        best = r;
+                        bs = s;
+                    }
+                }
+                prev = best;
+                add(bf2f(w[(size_t)t * k + bs]), reinterpret_cast<const uint4 *>(y + (size_t)best * H)[c]);
+            }
         } else {
             for (int s = 0; s < k; ++s) {
                 const int r = row_of[(size_t)t * k + s];
                 add(bf2f(w[(size_t)t * k + s]), reinterpret_cast<const uint4 *>(y + (size_t)r * H)[c]);
             }
+        }
+        if (ORDERED && add_in) {
+            const uint4 v = reinterpret_cast<const uint4 *>(add_in + (size_t)t * H)[c];
+            const float av[8] = {lo_bf(v.x), hi_bf(v.x), lo_bf(v.y), hi_bf(v.y),
+                                 lo_bf(v.z), hi_bf(v.z), lo_bf(v.w), hi_bf(v.w)};
+#pragma unroll
+            for (int q = 0; q < 8; ++q) acc[q] = bf16_round(acc[q] + av[q]);
         }
         uint4 o;
         o.x = f2bf(acc[0]) | (f2bf(acc[1]) << 16);
@@ -92,8 +150,9 @@ __global__ __launch_bounds__(256) void stage_merge_kernel(const uint16_t *__rest
 
 using namespace pd;
 
-PD_API int pdscope_merge(const void *y, const int32_t *row_of, const void *w, int T, int k, int H,
-                         const void *add_in, void *out, void *stream) {
+template <bool ORDERED>
+static int launch_merge(const void *y, const int32_t *row_of, const void *w, int T, int k, int H,
+                        const void *add_in, void *out, void *stream) {
     if (!y || !row_of || !w || !out) return fail(kEInval, "merge: null pointer");
     if (T < 1 || k < 1 || H < 8 || H % 8) return fail(kEInval, "merge: need T,k >= 1 and H % 8 == 0");
     const int64_t total = (int64_t)T * (H / 8);
@@ -105,12 +164,22 @@ PD_API int pdscope_merge(const void *y, const int32_t *row_of, const void *w, in
     // slot-at-a-time loop keeps more threads resident (T=4096: 29.5 us
     // against 33.3 us)
     if (k <= 8 && T <= 1024)
-        merge_kernel<8><<<blocks, 256, 0, s>>>(yy, row_of, ww, T, k, H, aa, (uint16_t *)out);
+        merge_kernel<8, ORDERED><<<blocks, 256, 0, s>>>(yy, row_of, ww, T, k, H, aa, (uint16_t *)out);
     else if (k <= 16 && T <= 1024)
-        merge_kernel<16><<<blocks, 256, 0, s>>>(yy, row_of, ww, T, k, H, aa, (uint16_t *)out);
+        merge_kernel<16, ORDERED><<<blocks, 256, 0, s>>>(yy, row_of, ww, T, k, H, aa, (uint16_t *)out);
     else
-        merge_kernel<0><<<blocks, 256, 0, s>>>(yy, row_of, ww, T, k, H, aa, (uint16_t *)out);
+        merge_kernel<0, ORDERED><<<blocks, 256, 0, s>>>(yy, row_of, ww, T, k, H, aa, (uint16_t *)out);
     return check_launch("merge_kernel");
+}
+
+PD_API int pdscope_merge(const void *y, const int32_t *row_of, const void *w, int T, int k, int H,
+                         const void *add_in, void *out, void *stream) {
+    return launch_merge<false>(y, row_of, w, T, k, H, add_in, out, stream);
+}
+
+PD_API int pdscope_merge_ordered(const void *y, const int32_t *row_of, const void *w, int T, int k, int H,
+                                 const void *add_in, void *out, void *stream) {
+    return launch_merge<true>(y, row_of, w, T, k, H, add_in, out, stream);
 }
 
 PD_API int pdscope_stage_merge(const void *host_block, int64_t rows, int64_t row_bytes, void *scratch,

@@ -496,6 +496,32 @@ class ExpertExecutor:
         pending.input_ref = None
         return out
 
+    def submit_cpu_many(self, jobs):
+        """Several experts of one layer in one packed backend submission
+        (executor.py:580-596): ``cpu_backend.submit_many({key: rows})`` returns
+        one future per expert; each expert keeps its own ledger demand."""
+        self._open()
+        backend = self.cpu_backend
+        if not jobs or not callable(getattr(backend, "submit_many", None)):
+            raise ValueError("packed CPU execution needs a backend with submit_many")
+        active = self.cache.unfinished_demand_keys
+        for key, inputs in jobs.items():
+            if (key in self._cpu_tasks or key not in active or inputs.device.type != "cpu"
+                    or inputs.dtype != torch.bfloat16 or inputs.ndim != 2
+                    or inputs.shape[1] != self.masters[key].tensors["gate_proj"].shape[1]):
+                raise ValueError("packed CPU submission requires unique active BF16 demands")
+        futures = backend.submit_many(dict(jobs))
+        if set(futures) != set(jobs):
+            raise AssertionError("packed CPU backend lost expert ownership")
+        pending = {key: PendingCpu(key, futures[key], inputs) for key, inputs in jobs.items()}
+        self._cpu_tasks.update(pending)
+        return pending
+
+    def finish_cpu_group(self, pendings):
+        """Outputs {expert id: rows} of a packed submission, each expert's
+        demand completed in the ledger (waits for every future)."""
+        return {p.key.expert: self.finish_cpu(p, wait=True) for p in pendings}
+
     def shutdown(self):
         if self._cpu_pool is not None:
             self._cpu_pool.shutdown(wait=True)

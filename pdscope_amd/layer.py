@@ -55,6 +55,22 @@ class MoEWorkspace:
             self.shared_tiles = torch.zeros(2, **i32)
             self.shared_sel = torch.zeros(1, **i32)
 
+    def pregathered(self, n: int) -> torch.Tensor:
+        """[n, H] bf16 buffer for activation rows gathered into grouped order."""
+        buf = getattr(self, "_xg", None)
+        if buf is None or buf.shape[0] < n:
+            buf = torch.empty((max(n, self.max_tokens * self.k), self.H), dtype=BF16, device=self.device)
+            self._xg = buf
+        return buf[:n]
+
+    def identity_rows(self, n: int) -> torch.Tensor:
+        """int32 [n] = 0..n-1: the row map of activations already in grouped order."""
+        buf = getattr(self, "_ident", None)
+        if buf is None or buf.numel() < n:
+            buf = torch.arange(max(n, self.max_tokens * self.k), dtype=torch.int32, device=self.device)
+            self._ident = buf
+        return buf[:n]
+
     def views(self, T: int):
         if not 0 < T <= self.max_tokens:
             raise ValueError(f"token count {T} outside workspace capacity {self.max_tokens}")
@@ -99,14 +115,17 @@ def shared_forward(x, shared_slot, ws: MoEWorkspace):
     return ws.y_shared[:T]
 
 
-def experts_resident(x, ids, weights, slots, ws: MoEWorkspace, out=None, *, block_m=None, add_in=None):
+def experts_resident(x, ids, weights, slots, ws: MoEWorkspace, out=None, *, block_m=None, add_in=None,
+                     merge="fused"):
     """K4 (T == 1) or K2+K3+K5 (T > 1) over experts that are all addressable in `slots`.
-    add_in [T, H] bf16 (shared-expert output) is added unweighted in the merge."""
+    add_in [T, H] bf16 (shared-expert output) is added unweighted in the merge.
+    merge: 'fused' (fp32 sum, one rounding) or 'reference' (bf16 adds in
+    ascending expert id, the reference runtime's default merge)."""
     T = x.shape[0]
     H, I, E, k = ws.H, ws.I, ws.E, ws.k
     out = ws.out[:T] if out is None else out
     if T == 1 and add_in is None:
-        ops.swiglu_decode(x, ids, weights, slots, H, I, ws.h_ws, out)
+        ops.swiglu_decode(x, ids, weights, slots, H, I, ws.h_ws, out, merge=merge)
         return out
     _, _, _, packed = ws.views(T)
     ops.pack(ids, E, out=packed, workspace=ws.pack_ws)
@@ -114,7 +133,7 @@ def experts_resident(x, ids, weights, slots, ws: MoEWorkspace, out=None, *, bloc
     bmd = down_block_m(bm, H, I)
     grouped_ffn(x, packed, ws.sel_all, bm, (T * k + bm - 1) // bm + E, slots, ws,
                 max_tiles_down=(T * k + bmd - 1) // bmd + E)
-    ops.merge(ws.y, packed.row_of, weights, out, add_in=add_in)
+    ops.merge(ws.y, packed.row_of, weights, out, add_in=add_in, mode=merge)
     return out
 
 
@@ -127,29 +146,33 @@ def down_block_m(bm: int, H: int, I: int) -> int:
     return 256 if bm == 384 and H % 256 == 0 and I % 128 == 0 else bm
 
 
-def grouped_ffn(x, packed, sel, bm, max_tiles, slots, ws: MoEWorkspace, *, max_tiles_down):
+def grouped_ffn(x, packed, sel, bm, max_tiles, slots, ws: MoEWorkspace, *, max_tiles_down, perm=None):
     """Grouped SwiGLU over the experts in `sel` (int32 device): gate/up on
     bm-row tiles into ws.h_ws, down on down_block_m(bm, H, I)-row tiles into ws.y.
-    max_tiles / max_tiles_down bound the two launches' tile counts."""
+    max_tiles / max_tiles_down bound the two launches' tile counts.  perm
+    (default packed.perm_token) maps grouped rows to rows of x."""
     H, I = ws.H, ws.I
+    perm = packed.perm_token if perm is None else perm
     nsel = sel.numel()
     tile_start, order = ws.tile_start[:nsel + 1], ws.sel_order[:nsel]
     ops.schedule(packed.counts, sel, bm, out=tile_start, order=order)
     bmd = down_block_m(bm, H, I)
     if bmd == bm:
-        ops.swiglu_grouped(x, packed.perm_token, packed.offsets, order, tile_start, max_tiles, bm, slots, H, I,
-                           ws.h_ws, ws.y)
+        ops.swiglu_grouped(x, perm, packed.offsets, order, tile_start, max_tiles, bm, slots, H, I, ws.h_ws, ws.y)
         return
     tile_down, order_down = ws.tile_start_down[:nsel + 1], ws.sel_order_down[:nsel]
     ops.schedule(packed.counts, sel, bmd, out=tile_down, order=order_down)
-    ops.swiglu_grouped_gateup(x, packed.perm_token, packed.offsets, order, tile_start, max_tiles, bm, slots, H, I,
-                              ws.h_ws)
+    ops.swiglu_grouped_gateup(x, perm, packed.offsets, order, tile_start, max_tiles, bm, slots, H, I, ws.h_ws)
     ops.swiglu_grouped_down(ws.h_ws, packed.offsets, order_down, tile_down, max_tiles_down, bmd, slots, H, I, ws.y)
 
 
 def moe_forward(x, gate, slots, ws: MoEWorkspace, *, normalize=True, bias=None, block_m=None, fused_decode=True,
-                shared_slot=None):
+                shared_slot=None, merge="fused"):
     """Full layer: returns (out [T,H] bf16, logits, ids int32 [T,k], weights bf16 [T,k]).
+
+    merge: 'fused' (each token's k weighted rows summed in fp32, one
+    rounding) or 'reference' (added in ascending expert id in bf16
+    arithmetic, bit-exact with the reference runtime's default merge).
 
     T == 1 runs the single-launch decode kernel (K4f) when the shape and the
     device allow it (fused_decode), else route (K1) + decode GEMV (K4).
@@ -162,15 +185,15 @@ def moe_forward(x, gate, slots, ws: MoEWorkspace, *, normalize=True, bias=None, 
             raise ValueError("shared experts need a workspace built with shared_I")
         logits, ids, weights = route(x, gate, ws, normalize=normalize, bias=bias)
         y_shared = shared_forward(x, shared_slot, ws)
-        out = experts_resident(x, ids, weights, slots, ws, block_m=block_m, add_in=y_shared)
+        out = experts_resident(x, ids, weights, slots, ws, block_m=block_m, add_in=y_shared, merge=merge)
         return out, logits, ids, weights
     if (T == 1 and fused_decode and ws.k <= 8
             and ops.decode_layer_supported(ws.H, ws.I, ws.E, ws.k, x.device)):
         logits, ids, weights, _ = ws.views(1)
         out = ws.out[:1]
         ops.decode_layer(x, gate, slots, ws.I, ws.k, normalize, bias=bias, out=out, logits=logits, ids=ids,
-                         weights=weights, h_ws=ws.h_ws)
+                         weights=weights, h_ws=ws.h_ws, merge=merge)
         return out, logits, ids, weights
     logits, ids, weights = route(x, gate, ws, normalize=normalize, bias=bias)
-    out = experts_resident(x, ids, weights, slots, ws, block_m=block_m)
+    out = experts_resident(x, ids, weights, slots, ws, block_m=block_m, merge=merge)
     return out, logits, ids, weights

@@ -226,7 +226,18 @@ def swiglu_grouped_down(h_ws, offsets, sel, tile_start, max_tiles, block_m, slot
               int(max_tiles), int(block_m), _p(slots), H, I, _p(y), _stream(dev))
 
 
-def swiglu_decode(x, ids, w, slots, H, I, h_ws, out):
+MERGE_MODES = {"fused": 0, "reference": 1}
+
+
+def merge_mode(merge: str) -> int:
+    """C-ABI merge_mode of a runtime merge name: 'fused' (fp32, one rounding)
+    or 'reference' (bf16 adds in ascending expert id, the reference's default)."""
+    if merge not in MERGE_MODES:
+        raise ValueError("invalid merge mode")
+    return MERGE_MODES[merge]
+
+
+def swiglu_decode(x, ids, w, slots, H, I, h_ws, out, *, merge="fused"):
     _need(x, "inputs", BF16)
     dev = x.device
     _need(ids, "ids", torch.int32, None, dev)
@@ -237,7 +248,8 @@ def swiglu_decode(x, ids, w, slots, H, I, h_ws, out):
     k = ids.numel()
     if x.numel() != H or out.numel() != H or w.numel() != k or h_ws.numel() < k * I:
         raise ValueError("decode expects one token: x/out [H], ids/weights [k], h_ws >= k*I")
-    _lib.call("pdscope_swiglu_decode", _p(x), _p(ids), _p(w), k, _p(slots), H, I, _p(h_ws), _p(out), _stream(dev))
+    _lib.call("pdscope_swiglu_decode", _p(x), _p(ids), _p(w), k, _p(slots), H, I, _p(h_ws), _p(out),
+              merge_mode(merge), _stream(dev))
     return out
 
 
@@ -282,7 +294,8 @@ def decode_layer_supported(H, I, E, k, device) -> bool:
     return ok
 
 
-def decode_layer(x, gate, slots, I, top_k, normalize, *, bias=None, out, logits, ids, weights, h_ws, probs=None):
+def decode_layer(x, gate, slots, I, top_k, normalize, *, bias=None, out, logits, ids, weights, h_ws, probs=None,
+                 merge="fused"):
     """K4f: route + top-k + SwiGLU GEMV + down/merge of one token in one launch."""
     _need(x, "inputs", BF16)
     dev = x.device
@@ -300,7 +313,8 @@ def decode_layer(x, gate, slots, I, top_k, normalize, *, bias=None, out, logits,
         _need(bias, "bias", torch.float32, 1, dev)
     if probs is not None:
         _need(probs, "probs", torch.float32, None, dev)
-    _lib.call("pdscope_decode_layer", _p(x), _p(gate), _p(bias), H, E, top_k, int(bool(normalize)), _p(slots), I,
+    _lib.call("pdscope_decode_layer", _p(x), _p(gate), _p(bias), H, E, top_k, int(bool(normalize)),
+              merge_mode(merge), _p(slots), I,
               _p(logits), _p(ids), _p(weights), _p(probs), _p(h_ws), _p(out), _p(decode_workspace(dev, H)),
               _stream(dev))
     return out
@@ -308,7 +322,7 @@ def decode_layer(x, gate, slots, I, top_k, normalize, *, bias=None, out, logits,
 
 # --------------------------------------------------------------------- A8/A9
 
-def merge(y, row_of, w, out, add_in=None):
+def merge(y, row_of, w, out, add_in=None, *, mode="fused"):
     _need(w, "weights", BF16, 2)
     dev = w.device
     _need(y, "y", BF16, None, dev)
@@ -318,7 +332,8 @@ def merge(y, row_of, w, out, add_in=None):
     H = out.shape[1]
     if add_in is not None:
         _need(add_in, "add_in", BF16, 2, dev)
-    _lib.call("pdscope_merge", _p(y), _p(row_of), _p(w), T, k, H, _p(add_in), _p(out), _stream(dev))
+    name = "pdscope_merge_ordered" if merge_mode(mode) else "pdscope_merge"
+    _lib.call(name, _p(y), _p(row_of), _p(w), T, k, H, _p(add_in), _p(out), _stream(dev))
     return out
 
 

@@ -37,7 +37,9 @@ expert runs on the GPU.  There is no built-in CPU expert path.
 """
 from __future__ import annotations
 
+import ctypes
 import hashlib
+import statistics
 import time
 from pathlib import Path
 
@@ -52,18 +54,33 @@ from .policy import plan_pdscope
 
 
 def load_hot_profile(path, masters, slots):
-    """Static hot-expert table, one ``layer,expert`` per line (hot/qwen.txt format;
-    pdscope_runtime.py:62-72)."""
-    raw = Path(path).read_bytes()
-    rows = [tuple(map(int, line.split(","))) for line in raw.decode().splitlines() if line.strip()]
-    if (type(slots) is not int or slots < 0 or len(set(rows)) != len(rows)
-            or any(len(r) != 2 or r[0] < 0 or r[1] < 0 for r in rows)):
+    """The static hot set from a profile file (the hot/qwen.txt format read by
+    expertbench/pdscope_runtime.py:62-72): one ``layer,expert`` pair per
+    non-blank line.  Returns the first `slots` listed experts that have a
+    master, in file order, and a provenance record (path, sha256, entry
+    counts).  A malformed or duplicated line, a negative index, a bad
+    capacity, or too few listed experts with masters raise ValueError."""
+    blob = Path(path).read_bytes()
+    if type(slots) is not int or slots < 0:
         raise ValueError("invalid static hot profile or capacity")
-    keys = [ExpertKey(l, e, "bf16") for l, e in rows if ExpertKey(l, e, "bf16") in masters]
-    if len(keys) < slots:
+    listed, seen = [], set()
+    for number, line in enumerate(blob.decode().splitlines(), 1):
+        if not line.strip():
+            continue
+        fields = line.split(",")
+        try:
+            pair = tuple(int(f) for f in fields)
+        except ValueError:
+            raise ValueError(f"invalid static hot profile or capacity (line {number}: {line!r})") from None
+        if len(pair) != 2 or min(pair) < 0 or pair in seen:
+            raise ValueError(f"invalid static hot profile or capacity (line {number}: {line!r})")
+        seen.add(pair)
+        listed.append(ExpertKey(pair[0], pair[1], "bf16"))
+    eligible = [key for key in listed if key in masters]
+    if len(eligible) < slots:
         raise ValueError("hot table cannot fill the declared static capacity")
-    return keys[:slots], dict(path=str(Path(path).resolve()), sha256=hashlib.sha256(raw).hexdigest(),
-                              entries=len(rows), eligible_entries=len(keys), selected=slots)
+    return eligible[:slots], dict(path=str(Path(path).resolve()), sha256=hashlib.sha256(blob).hexdigest(),
+                                  entries=len(listed), eligible_entries=len(eligible), selected=slots)
 
 
 class PDScopeCudaRuntime:
@@ -84,6 +101,11 @@ class PDScopeCudaRuntime:
             raise ValueError("invalid merge mode or pre-gather switch")
         if type(graph_output_pool) is not bool or type(resident_graphs) is not bool:
             raise ValueError("graph switches must be boolean")
+        if graph_cost_mode not in ("eager_bound", "measured"):
+            raise ValueError("invalid resident graph cost mode")
+        if native_dispatch is not None and not all(
+                callable(getattr(native_dispatch, f, None)) for f in ("submit_group", "finish_and_merge")):
+            raise ValueError("native dispatch must provide submit_group and finish_and_merge")
         # the reference allows 2..4 staging slots (pdscope_runtime.py:108-109); this
         # path also serves configurations with 8
         if type(demand_slots) is not int or not 2 <= demand_slots <= 8:
@@ -102,8 +124,9 @@ class PDScopeCudaRuntime:
         self.speculative_slots = speculative_slots
         self.costs, self.cpu_backend, self.native_dispatch = costs, cpu_backend, native_dispatch
         self.demand_slots, self.diagnostics = demand_slots, diagnostics
-        self.merge, self.dispatch = merge, dispatch
+        self.merge, self.dispatch, self.cpu_batch = merge, dispatch, cpu_batch
         self.input_pregather, self.graph_output_pool = input_pregather, graph_output_pool
+        self.graph_cost_mode, self.graph_cost_calibration = graph_cost_mode, None
         self.balance_profile, self.decode_cpu_target = balance_profile, decode_cpu_target
         self.resident_graphs = resident_graphs
         self.cache = ExpertCache(sizes, (len(hot_keys) + speculative_slots) * self.size, [self.size] * demand_slots,
@@ -119,12 +142,16 @@ class PDScopeCudaRuntime:
         self._ws = {}
         self._pws = {}
         self._graphs = {}
+        self._graph_turn = {}
+        self._dispatch_buffers = {}
         self._pinned_counts = torch.empty(2 * self.E + 64, dtype=torch.int32, pin_memory=True)
         self._copy_done = torch.cuda.Event()
         try:
             for key in hot_keys:
                 self.executor.finish_load(self.executor.load(key, origin="initial"), wait=True)
             self.initial_stats = self.cache.stats()
+            if resident_graphs and costs is not None and hot_keys:
+                self._calibrate_graph_costs(hot_keys)
         except BaseException:
             self.close()
             raise
@@ -203,17 +230,27 @@ class PDScopeCudaRuntime:
         # and the same graph is replayed once more over the completed table
         # (with fewer slots than k only a fully resident layer replays)
         planned = self.costs is not None and self.cpu_backend is not None
-        graph_path = (self.resident_graphs and phase == "decode" and bias is None and not planned
-                      and ops.decode_layer_supported(H, self.I, E, k, self.device)
-                      and (k <= self.demand_slots or self._layer_fully_resident(layer)))
+        graph_ok = (self.resident_graphs and phase == "decode" and bias is None
+                    and ops.decode_layer_supported(H, self.I, E, k, self.device)
+                    and (k <= self.demand_slots or self._layer_fully_resident(layer)))
+        # unplanned: the first replay also routes; planned: routing comes
+        # first, and the graph serves the layer when the plan keeps every
+        # routed expert on the GPU (decided below)
+        graph_path = graph_ok and not planned
+        ring = 0
+        if graph_ok and self.graph_output_pool:
+            ring = self._graph_turn.get(layer, 0)
+            self._graph_turn[layer] = ring ^ 1
+        replay_table, late_replays = None, 0
 
         # ---- 1-2: route (+ predictor), grouping, one D2H of the demand
         out = torch.empty((T, H), dtype=torch.bfloat16, device=self.device)
         if graph_path:
             # entries the first replay saw (a copy still in flight reads as null)
             replay_table = list(self.executor.table(layer, E)[1])
-            logits, ids, weights = self._replay_decode_graph(layer, x, gate, normalize, k, out)
-            fused_replays = 1
+            logits, ids, weights, gout = self._replay_decode_graph(layer, x, gate, normalize, k, out, ring=ring)
+            if self.graph_output_pool:
+                out = gout
         else:
             logits, ids, weights = L.route(x, gate, ws, normalize=normalize, bias=bias)
         predict = prefetch and next_gate is not None
@@ -280,6 +317,8 @@ class PDScopeCudaRuntime:
             cpu_list = list(decision["cpu_queue"])
             resident = list(decision["gpu_resident_queue"])
             demand = list(decision["on_demand_queue"])
+            if graph_ok and not cpu_list:
+                graph_path = True  # replayed below over the (completed) slot table
         else:
             decision = None
             cpu_list = []
@@ -309,26 +348,58 @@ class PDScopeCudaRuntime:
         decode_fast = (T == 1 and not demand and not cpu_list and not graph_path)
         if T == 1 and (demand or cpu_list) and not graph_path:
             ops.pack(ids, E, out=packed, workspace=ws.pack_ws)  # decode misses take the grouped path
-        # ---- CPU experts start before the GPU launches (pdscope_runtime.py:300-336):
-        # each gets its routed rows in grouped order, and its output later fills
-        # the same rows of the grouped output, so the merge is unchanged
-        cpu_tasks = {}
-        if cpu_list:
+        # grouped launches read the activation rows through perm_token; with
+        # input_pregather the rows are first gathered into grouped order by
+        # one gather launch and the grouped kernels read them in order
+        x_src, perm_src = x, None
+        if self.input_pregather and T > 1 and not graph_path:
+            n = T * k
+            x_src, perm_src = ws.pregathered(n), ws.identity_rows(n)
+            with torch.cuda.stream(ex.compute_stream):
+                ex.compute_stream.wait_stream(cur)
+                torch.index_select(x, 0, packed.perm_token, out=x_src)
+        # ---- CPU experts start before the GPU launches (pdscope_runtime.py:284-336):
+        # a decode group through the native dispatch module (merge='fused'),
+        # else per expert, or packed into one backend submission (cpu_batch);
+        # each expert gets its routed rows in grouped order, and its output
+        # later fills the same rows of the grouped output
+        cpu_tasks, cpu_group, native_cpu = {}, None, None
+        packed_cpu = self.cpu_batch == "both" or (self.cpu_batch == "decode" and phase == "decode")
+        if (cpu_list and self.native_dispatch is not None and self.merge == "fused" and phase == "decode"):
+            handles = self.cpu_backend.native_group_handles(layer) if callable(
+                getattr(self.cpu_backend, "native_group_handles", None)) else None
+            if handles is not None:
+                native_cpu = sorted(cpu_list)
+                pool, layer_obj = handles
+                dws = self._dispatch_workspace(len(native_cpu), H)
+                row = x.cpu().contiguous()
+                self.native_dispatch.submit_group(
+                    pool, layer_obj, row.data_ptr(), len(native_cpu), H * 2, dws["packed"].data_ptr(),
+                    dws["block"].data_ptr(), ctypes.addressof(dws["count"]), ctypes.addressof(dws["selected"]),
+                    ctypes.addressof(dws["coeff"]), list(native_cpu))
+                del handles, pool, layer_obj, row
+        late_cpu = [] if native_cpu is not None else cpu_list
+        if late_cpu:
             x_host = x.cpu()
             if T > 1:
                 offs = packed.offsets.cpu().tolist()
                 perm = packed.perm_token.cpu()
-            for e in cpu_list:
-                rows = x_host if T == 1 else x_host.index_select(0, perm[offs[e]:offs[e + 1]].long())
-                cpu_tasks[e] = ex.submit_cpu(key(e), rows.contiguous())
+            jobs = {e: (x_host if T == 1 else x_host.index_select(0, perm[offs[e]:offs[e + 1]].long())).contiguous()
+                    for e in late_cpu}
+            if packed_cpu:
+                cpu_group = ex.submit_cpu_many({key(e): r for e, r in jobs.items()})
+            else:
+                for e, r in jobs.items():
+                    cpu_tasks[e] = ex.submit_cpu(key(e), r)
         if graph_path:
             if not demand:  # with misses the demand batch below replays over the completed table
-                if any(replay_table[e] == 0 for e in counts):
-                    # a routed copy landed after the first replay: replay over the completed table
-                    fused_replays += 1
+                if replay_table is None or any(replay_table[e] == 0 for e in counts):
+                    # not replayed yet (planned path), or a routed copy landed
+                    # after the first replay: replay over the completed table
+                    late_replays += 1
 
                     def launch():
-                        self._replay_decode_graph(layer, x, gate, normalize, k, out)
+                        self._replay_decode_graph(layer, x, gate, normalize, k, out, ring=ring)
                 else:
                     def launch():  # the replay already produced `out`; account the uses it made
                         pass
@@ -339,12 +410,12 @@ class PDScopeCudaRuntime:
             slots_dev = ex.upload_table(layer, E, ex.compute_stream)
             if decode_fast:
                 def launch():
-                    ops.swiglu_decode(x, ids, weights, slots_dev, H, self.I, ws.h_ws, out)
+                    ops.swiglu_decode(x, ids, weights, slots_dev, H, self.I, ws.h_ws, out, merge=self.merge)
             else:
                 sel_dev = ex.upload_ints(resident, ex.compute_stream)
 
                 def launch():
-                    self._grouped(x, packed, sel_dev, [counts[e] for e in resident], slots_dev, ws)
+                    self._grouped(x_src, packed, sel_dev, [counts[e] for e in resident], slots_dev, ws, perm_src)
             tasks.append(ex.gpu_group([key(e) for e in resident], launch, input_ref=x, wait_for=cur))
 
         # ---- demand misses through the staging slots
@@ -357,17 +428,17 @@ class PDScopeCudaRuntime:
                 ex.table(layer, E)
                 require_copies(batch)
                 if graph_path:
-                    fused_replays += 1
+                    late_replays += 1
 
                     def launch():
-                        self._replay_decode_graph(layer, x, gate, normalize, k, out)
+                        self._replay_decode_graph(layer, x, gate, normalize, k, out, ring=ring)
                     comp = ex.gpu_group([key(e) for e in resident + batch], launch, input_ref=x, wait_for=cur)
                 else:
                     tab = ex.upload_table(layer, E, ex.compute_stream)
                     sel_dev = ex.upload_ints(batch, ex.compute_stream)
 
                     def launch(sel_dev=sel_dev, tab=tab, rows=[counts[e] for e in batch]):
-                        self._grouped(x, packed, sel_dev, rows, tab, ws)
+                        self._grouped(x_src, packed, sel_dev, rows, tab, ws, perm_src)
                     comp = ex.gpu_group([key(e) for e in batch], launch, input_ref=x, wait_for=cur)
                 ping_pong += [dict(expert=e, slot=t.slot, generation=t.generation) for e, t in zip(batch, tickets)]
                 live = [t.slot for b in inflight for t in b]
@@ -407,19 +478,48 @@ class PDScopeCudaRuntime:
         # ---- finish GPU work, place the CPU experts' rows, merge in token order
         for task in tasks:
             ex.finish_gpu(task, wait=True)
-        if cpu_tasks:
+        if graph_path and self.graph_output_pool:
+            out = self._graphs[(layer, k, normalize, gate.data_ptr(), ring)][2]
+        cpu_rows = dict((e, ex.finish_cpu(p, wait=True)) for e, p in cpu_tasks.items())
+        if cpu_group is not None:
+            cpu_rows.update(ex.finish_cpu_group(cpu_group.values()))
+        add_in = None
+        if cpu_rows or native_cpu:
             offs = packed.offsets.cpu().tolist() if T == 1 else offs
-            with torch.cuda.stream(ex.compute_stream):
-                for e, pending in cpu_tasks.items():
-                    rows = ex.finish_cpu(pending, wait=True)
-                    ws.y[offs[e] * H:offs[e + 1] * H].view(-1, H).copy_(rows)
-        if not (decode_fast or graph_path):
-            with torch.cuda.stream(ex.compute_stream):
-                ops.merge(ws.y, packed.row_of, weights, out)
+        with torch.cuda.stream(ex.compute_stream):
+            for e, rows in cpu_rows.items():
+                ws.y[offs[e] * H:offs[e + 1] * H].view(-1, H).copy_(rows)
+            if native_cpu:
+                # join the native queue, stage its block and add it (bf16 index_add)
+                # into a zero output; the GPU rows are then merged on top of it
+                # and the CPU experts' own rows contribute nothing there
+                # (pdscope_runtime.py:407-426, then the fused merge :455-464)
+                sel_host = ids.reshape(-1).tolist()
+                slot_idx = torch.tensor([sel_host.index(e) for e in native_cpu], dtype=torch.long,
+                                        device=self.device)
+                w_cpu = weights.reshape(-1).index_select(0, slot_idx)
+                dws = self._dispatch_workspace(len(native_cpu), H)
+                handles = self.cpu_backend.native_group_handles(layer)
+                if handles is None:
+                    raise AssertionError("native CPU group lost its handles")
+                add_in = torch.zeros((1, H), dtype=torch.bfloat16, device=self.device)
+                add_in = self.native_dispatch.finish_and_merge(handles[0], dws["block"].data_ptr(), len(native_cpu),
+                                                               H * 2, dws["scratch"], add_in, dws["tokens"], w_cpu)
+                del handles
+                for e in native_cpu:
+                    ws.y[offs[e] * H:offs[e + 1] * H].zero_()
+            if not (decode_fast or graph_path):
+                ops.merge(ws.y, packed.row_of, weights, out, add_in=add_in, mode=self.merge)
+        if native_cpu:
+            for e in native_cpu:
+                self.cache.finish_cpu(key(e))
+            note = getattr(self.cpu_backend, "note_native_dispatch", None)
+            if note is not None:
+                note(len(native_cpu))
         done = torch.cuda.Event()
         done.record(ex.compute_stream)
         cur.wait_event(done)
-        if graph_path and fused_replays > 1:
+        if graph_path and late_replays:
             # replays after the demand reveal: their error word, read once they completed
             host[err_at:err_at + 1].copy_(self._decode_error_word(), non_blocking=True)
             self._copy_done.record(cur)
@@ -449,9 +549,10 @@ class PDScopeCudaRuntime:
                    if self.balance_profile else None)
         digest = lambda t: hashlib.sha256(t.detach().cpu().contiguous().numpy().tobytes()).hexdigest()  # noqa: E731
         row = dict(phase=phase, step=step, layer=layer, token_counts=counts, balance=balance,
-                   cpu_packing=False, cpu_batched_io=False, dispatch=self.dispatch,
-                   decode_submission="single_launch" if phase == "decode" and (decode_fast or graph_path)
-                   else "grouped_launch",
+                   cpu_packing=bool(packed_cpu and cpu_list), cpu_batched_io=bool(packed_cpu and cpu_list),
+                   dispatch=self.dispatch,
+                   decode_submission=("native_group" if native_cpu else "single_launch"
+                                      if phase == "decode" and (decode_fast or graph_path) else "grouped_launch"),
                    decision=decision, prefetch_issued=issued, prefetch_capacity_skipped=skipped,
                    next_prediction_counts=next_counts, causal_hit_counts=observed,
                    predictor="next_layer_gate_on_current_activation",
@@ -470,6 +571,60 @@ class PDScopeCudaRuntime:
                    if phase == "decode" else "grouped",
                    measured_performance=False)
         return out, routing, row
+
+    def _calibrate_graph_costs(self, hot_keys, reps=48, warm=16):
+        """Replay cost of the resident decode graph for the planner
+        (pdscope_runtime.py:143-175 calibrates its per-expert graphs the same
+        way): a layer graph over the first hot layer, routed by a calibration
+        gate onto k of its resident experts, is replayed `reps` times; the
+        median over the last reps-warm, divided by k, is one expert's graph
+        cost.  'measured' charges it to one-row GPU work in the cost table,
+        'eager_bound' keeps the table's eager cost (the cost model of the
+        reference's ResidentGraphCosts)."""
+        from .costs import ResidentGraphCosts
+        layer = min(k.layer for k in hot_keys)
+        resident = sorted(k.expert for k in hot_keys if k.layer == layer)
+        kk = min(8, len(resident))
+        if kk < 1 or not ops.decode_layer_supported(self.H, self.I, self.E, kk, self.device):
+            return
+        x = torch.linspace(-.5, .5, self.H, device=self.device).to(torch.bfloat16).reshape(1, -1)
+        gate = torch.zeros((self.E, self.H), dtype=torch.bfloat16, device=self.device)
+        for j, e in enumerate(resident[:kk]):
+            gate[e] = (x[0].float() * (0.01 * (kk - j))).to(torch.bfloat16)
+        out = torch.empty_like(x)
+        samples = []
+        for i in range(reps):
+            t0 = time.perf_counter()
+            self._replay_decode_graph(layer, x, gate, True, kk, out, cache=False)
+            torch.cuda.synchronize(self.device)
+            if i >= warm:
+                samples.append((time.perf_counter() - t0) * 1e3)
+        self._graphs.pop(("calibration", layer, kk), None)
+        gpu_ms = statistics.median(samples) / kk
+        base = self.costs.for_load(1)
+        self.graph_cost_calibration = dict(samples_ms=samples, median_ms=statistics.median(samples),
+                                           per_expert_ms=gpu_ms, experts_per_replay=kk, previous_gpu_ms=base["gpu_ms"],
+                                           scheduler_cost_mode=self.graph_cost_mode,
+                                           scheduler_gpu_ms=base["gpu_ms"] if self.graph_cost_mode == "eager_bound"
+                                           else gpu_ms,
+                                           scope="host wall time of one decode-layer graph replay over resident "
+                                                 "experts, per routed expert")
+        self.costs = ResidentGraphCosts(self.costs, gpu_ms, self.graph_cost_mode)
+
+    def _dispatch_workspace(self, rows, hidden):
+        """Borrowed buffers of the native decode tail (pdscope_runtime.py:177-192):
+        host packed/block rows, count/selected/coeff words, device token index
+        and scratch."""
+        ws = self._dispatch_buffers.get((rows, hidden))
+        if ws is None:
+            ws = dict(packed=torch.empty((rows, hidden), dtype=torch.bfloat16),
+                      block=torch.empty((rows, hidden), dtype=torch.bfloat16),
+                      count=ctypes.c_int32(rows), selected=(ctypes.c_int64 * rows)(),
+                      coeff=(ctypes.c_float * rows)(*([1.0] * rows)),
+                      tokens=torch.zeros(rows, dtype=torch.long, device=self.device),
+                      scratch=torch.empty((rows, hidden), dtype=torch.bfloat16, device=self.device))
+            self._dispatch_buffers[(rows, hidden)] = ws
+        return ws
 
     def _decode_error_word(self):
         """The fused decode kernel's sticky error word (int32 [1] device view)."""
@@ -504,19 +659,26 @@ class PDScopeCudaRuntime:
             return self.demand_slots // 2, 2
         return 1, self.demand_slots
 
-    def _grouped(self, x, packed, sel_dev, rows, slots_dev, ws):
+    def _grouped(self, x, packed, sel_dev, rows, slots_dev, ws, perm=None):
         """One grouped SwiGLU launch over the experts in sel_dev, whose routed
         row counts (known on the host since the demand reveal) are `rows`:
-        the row-tile height follows their mean, the grid their exact tile count."""
+        the row-tile height follows their mean, the grid their exact tile count.
+        perm overrides packed.perm_token (pre-gathered rows read in order)."""
         bm = ops.grouped_block_m(sum(rows) // len(rows), max(rows))
         bmd = L.down_block_m(bm, self.H, self.I)
         L.grouped_ffn(x, packed, sel_dev, bm, sum((r + bm - 1) // bm for r in rows), slots_dev, ws,
-                      max_tiles_down=sum((r + bmd - 1) // bmd for r in rows))
+                      max_tiles_down=sum((r + bmd - 1) // bmd for r in rows), perm=perm)
 
     # ------------------------------------------------------------ resident decode graph
 
-    def _replay_decode_graph(self, layer, x, gate, normalize, k, out):
-        gkey = (layer, k, normalize, gate.data_ptr())
+    def _replay_decode_graph(self, layer, x, gate, normalize, k, out, *, ring=0, cache=True):
+        """Replay the captured single-launch decode layer of `layer` over its
+        current slot table (capturing it on first use, checked bit for bit
+        against the eager launch).  With graph_output_pool the graph of ring
+        entry `ring` (two per layer) writes its own output buffer, which is
+        returned as is; otherwise the output is copied into `out`.
+        Returns (logits, ids, weights, output) views of the graph's buffers."""
+        gkey = (layer, k, normalize, gate.data_ptr(), ring) if cache else ("calibration", layer, k)
         g = self._graphs.get(gkey)
         ex = self.executor
         ex.table(layer, self.E)
@@ -533,12 +695,12 @@ class PDScopeCudaRuntime:
             side.wait_stream(torch.cuda.current_stream(self.device))
             # whole layer (fused single-launch decode where the device allows)
             with torch.cuda.stream(side):
-                L.moe_forward(xin, gate, slots_dev, gws, normalize=normalize)
+                L.moe_forward(xin, gate, slots_dev, gws, normalize=normalize, merge=self.merge)
             torch.cuda.current_stream(self.device).wait_stream(side)
             eager = [t.clone() for t in (gout, gws.logits[:1], gws.ids[:1], gws.weights[:1])]
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
-                L.moe_forward(xin, gate, slots_dev, gws, normalize=normalize)
+                L.moe_forward(xin, gate, slots_dev, gws, normalize=normalize, merge=self.merge)
             # a captured graph must reproduce the eager launch bit for bit
             # before it serves (the reference checks the same at capture,
             # expertbench/executor.py:95-96)
@@ -551,8 +713,9 @@ class PDScopeCudaRuntime:
         graph, xin, gout, gws, _ = g
         xin.copy_(x)
         graph.replay()
-        out.copy_(gout)
-        return gws.logits[:1], gws.ids[:1], gws.weights[:1]
+        if not self.graph_output_pool:
+            out.copy_(gout)
+        return gws.logits[:1], gws.ids[:1], gws.weights[:1], gout
 
     def close(self):
         self._graphs.clear()

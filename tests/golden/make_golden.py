@@ -14,7 +14,18 @@ the same library arithmetic the reference uses (torch 2.10):
 * expert groups   expertbench/adapters/qwen.py:155-174 (torch.where over the
                   transposed expert mask) -- a second, independent grouping;
 * expert_forward  expertbench/adapters/qwen.py:87-90 on CPU bf16 tensors and
-                  reference_fp32 qwen.py:93-98.
+                  reference_fp32 qwen.py:93-98;
+* merge           the default merge='reference' of
+                  expertbench/pdscope_runtime.py:454-468 (zero output, one bf16
+                  index_add_ of parts[e] * coeff per expert, experts ascending);
+* native tail     the out.index_add_(0, tokens, scratch * weights[:, None]) of
+                  native/native_layer_dispatch.cpp:88,129.  On the reference's
+                  CUDA device, rows with the same token are bf16 atomic adds
+                  (each add rounded, order unspecified); torch CPU instead sums
+                  duplicate indices of one call in fp32.  So the decode group
+                  (every row is token 0) is restated as one index_add_ call per
+                  row in row order (one valid order of the device's adds), and a
+                  group of distinct tokens as one call.
 
 Run:  python tests/golden/make_golden.py      (writes tests/golden/*.npz)
 """
@@ -104,6 +115,37 @@ def expert_case(name, m, H, I, seed=SEED + 7):
                         y_bf16=bits(y), y_fp32=yf.numpy())
 
 
+def merge_case(name, T, H, E, k, seed=SEED + 9):
+    g = torch.Generator().manual_seed(seed)
+    sel = torch.argsort(torch.rand((T, E), generator=g), dim=1)[:, :k]       # k distinct experts per token
+    w = torch.softmax(torch.randn((T, k), generator=g), dim=-1).to(torch.bfloat16)
+    groups = torch_expert_groups(sel)                                         # (slot, token) order per expert
+    parts = {e: (torch.randn((len(t), H), generator=g) * 0.5).to(torch.bfloat16) for e, t, _ in groups}
+    output = torch.zeros((T, H), dtype=torch.bfloat16)                        # runtime:454 (zeros_like)
+    for e, tokens, slots in groups:                                           # runtime:465 ordered=sorted(groups)
+        coeff = w[tokens, slots]
+        output.index_add_(0, tokens, (parts[e] * coeff[:, None]).to(output.dtype))   # runtime:466-468
+    y = torch.cat([parts[e] for e, _, _ in groups])                           # grouped row order
+    np.savez_compressed(HERE / f'merge_{name}.npz', ids=sel.numpy().astype(np.int32), weights=bits(w), y=bits(y),
+                        out=bits(output))
+
+
+def native_tail_case(name, rows, H, seed=SEED + 10):
+    g = torch.Generator().manual_seed(seed)
+    scratch = (torch.randn((rows, H), generator=g) * 0.5).to(torch.bfloat16)
+    weights = torch.softmax(torch.randn(rows, generator=g), dim=-1).to(torch.bfloat16)
+    out0 = (torch.randn((rows, H), generator=g) * 0.25).to(torch.bfloat16)
+    prod = scratch * weights.unsqueeze(1)                                     # native_layer_dispatch.cpp:88
+    decode = out0[:1].clone()
+    for r in range(rows):                                                     # every row is token 0
+        decode.index_add_(0, torch.zeros(1, dtype=torch.long), prod[r:r + 1])
+    tokens = torch.randperm(rows, generator=g)                                # distinct tokens
+    distinct = out0.clone()
+    distinct.index_add_(0, tokens, prod)
+    np.savez_compressed(HERE / f'native_tail_{name}.npz', scratch=bits(scratch), weights=bits(weights),
+                        out0=bits(out0), out_decode=bits(decode), tokens=tokens.numpy(), out_distinct=bits(distinct))
+
+
 def main():
     torch.set_num_threads(4)
     route_case('qwen_t64', 64, 2048, 128, 8, True)
@@ -118,6 +160,8 @@ def main():
     route_case('zipf_t64', 64, 2048, 128, 8, True, bias=bias, seed=SEED + 4)
     expert_case('small', 16, 256, 128)
     expert_case('h2048_m4', 4, 2048, 64)
+    merge_case('t48', 48, 256, 32, 8)
+    native_tail_case('r6', 6, 512)
     print('wrote', sorted(p.name for p in HERE.glob('*.npz')))
 
 

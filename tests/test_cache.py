@@ -194,3 +194,106 @@ def test_random_lifecycles_keep_invariants():
         assert st["h2d_bytes_submitted"] == st["h2d_bytes_completed"]
         assert (st.get("gpu_completed_experts", 0) + st.get("cpu_completed_experts", 0)
                 == st["physical_expert_demands"])
+
+
+def _brute_force_victims(c, size, protected):
+    """Victims by the policy's definition, recomputed from scratch: every
+    ready, unheld cache copy outside the open demand, ordered by (protected,
+    LRU tick | LFU (frequency, tick), key), taken until the new copy fits."""
+    short = c.memory()["cache_payload_bytes"] + size - c.cache_bytes
+    if short <= 0:
+        return []
+    open_keys = set(c.unfinished_demand_keys)
+    cands = []
+    for key in c.expert_bytes:
+        v = c.lookup(key)
+        if v is None or v.pool != "cache" or v.state != "ready" or key in open_keys:
+            continue
+        tick = c._last_tick.get(key, 0)
+        rank = (c.demand_frequency(key), tick) if c.policy == "LFU" else (tick,)
+        cands.append(((key in protected,) + rank + (key,), key))
+    out = []
+    for _, key in sorted(cands):
+        out.append(key)
+        short -= c.expert_bytes[key]
+        if short <= 0:
+            return out
+    return None
+
+
+@pytest.mark.parametrize("policy", ["LRU", "LFU"])
+def test_victims_match_brute_force_priority_order(policy):
+    rng = random.Random(11 if policy == "LRU" else 12)
+    for trial in range(40):
+        E, size = 10, 10
+        c = make(E=E, cache_slots=rng.randint(1, 5), staging=(10, 10), policy=policy)
+        protected = set()
+        for step in range(10):
+            layer = step % 2
+            keys = {K(layer, e): 1 for e in rng.sample(range(E), rng.randint(1, 4))}
+            c.on_demand(DemandID("v", step, layer), keys)
+            for key in sorted(keys):
+                if c.lookup(key) is None:
+                    before = {k for k in c.expert_bytes if c.lookup(k) is not None}
+                    want = _brute_force_victims(c, size, protected)
+                    try:
+                        t = c.begin_load(key)
+                    except CapacityBlocked:
+                        raise AssertionError("a demand load always has a staging fallback here")
+                    if t.pool == "cache":
+                        gone = before - {k for k in c.expert_bytes if c.lookup(k) is not None}
+                        assert want is not None and gone == set(want)
+                    else:
+                        assert want is None
+                    c.submit(t)
+                    c.complete_load(t)
+                c.release(c.acquire(key))
+            c.end_demand(DemandID("v", step, layer))
+            if rng.random() < 0.4:
+                protected = {K(1 - layer, e) for e in rng.sample(range(E), 2)}
+                c.set_protected(protected)
+            for _ in range(rng.randint(0, 2)):
+                key = K(1 - layer, rng.randrange(E))
+                if c.lookup(key) is not None:
+                    continue
+                before = {k for k in c.expert_bytes if c.lookup(k) is not None}
+                want = _brute_force_victims(c, size, protected)
+                try:
+                    t = c.begin_load(key, origin="prefetch")
+                except CapacityBlocked:
+                    assert want is None
+                    continue
+                gone = before - {k for k in c.expert_bytes if c.lookup(k) is not None}
+                assert gone == set(want)
+                c.submit(t)
+                c.complete_load(t)
+
+
+def test_retention_hint_lasts_one_reveal_and_expire_prefetch():
+    c = make(cache_slots=2, staging=(10,))
+    c.on_demand(DemandID("r", 0, 0), {K(0, 0): 1})
+    load_ready(c, K(0, 0))
+    c.release(c.acquire(K(0, 0)))
+    # a forecast for layer 1: protected until the next reveal
+    t = load_ready(c, K(1, 3), origin="prefetch")
+    assert c.set_retention_hint(DemandID("r", 0, 0), DemandID("r", 0, 1), [K(1, 3)])
+    assert not c.set_retention_hint(DemandID("r", 0, 0), DemandID("r", 0, 1), [K(1, 3)])
+    with pytest.raises(CacheError):   # target must be the next layer of the active demand
+        c.set_retention_hint(DemandID("r", 0, 0), DemandID("r", 0, 2), [K(1, 3)])
+    c.end_demand(DemandID("r", 0, 0))
+    load_ready(c, K(1, 4), origin="prefetch")   # full: evicts K(0,0), not the protected forecast
+    assert c.lookup(K(0, 0)) is None and c.lookup(K(1, 3)) is not None
+    c.on_demand(DemandID("r", 0, 1), {K(1, 3): 2})
+    assert c.retention_hint is None and c.stats()["retention_hint_expirations"] == 1
+    assert c.stats()["fresh_prefetch_hits"] == 1
+    c.release(c.acquire(K(1, 3)))
+    c.end_demand(DemandID("r", 0, 1))
+    inv = c.prefetch_inventory()
+    assert inv["used_resident_copies"] == 1 and inv["unused_ready_copies"] == 1
+    # an unsubmitted forecast outside the open demand is dropped on expiry
+    c.on_demand(DemandID("r", 1, 0), {K(0, 1): 1})
+    c.finish_cpu(K(0, 1))
+    c.end_demand(DemandID("r", 1, 0))
+    t5 = c.begin_load(K(1, 5), origin="prefetch")
+    assert c.expire_prefetch(t5) and c.lookup(K(1, 5)) is None and t5 in c.take_retired()
+    assert t not in c.take_retired()

@@ -54,7 +54,8 @@ def test_load_expert_and_router_round_trip(tmp_path):
         assert torch.equal(w.tensors[proj], tensors[f"model.layers.2.mlp.experts.3.{proj}.weight"])
         assert w.tensors[proj].is_contiguous() and w.tensors[proj].dtype == torch.bfloat16
     assert w.nbytes == 3 * I * H * 2
-    assert w.provenance["tensor_sha256"]["up_proj"] == tensor_hash(tensors["model.layers.2.mlp.experts.3.up_proj.weight"])
+    assert w.provenance["tensors"]["up_proj"]["sha256"] == tensor_hash(
+        tensors["model.layers.2.mlp.experts.3.up_proj.weight"])
     gate, cfg, info = load_router(tmp_path, 1)
     assert torch.equal(gate, tensors["model.layers.1.mlp.gate.weight"])
     assert cfg["num_experts_per_tok"] == 2 and info["shape"] == [E, H] and info["bytes"] == E * H * 2

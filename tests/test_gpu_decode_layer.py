@@ -26,7 +26,7 @@ def pd():
     return ops, layer, synthetic
 
 
-def _three_launch(ops, x, gate, slots, I, k, normalize, bias=None):
+def _three_launch(ops, x, gate, slots, I, k, normalize, bias=None, merge="fused"):
     E, H = gate.shape
     logits = torch.empty((1, E), dtype=torch.bfloat16, device=DEV)
     ids = torch.empty((1, k), dtype=torch.int32, device=DEV)
@@ -34,11 +34,11 @@ def _three_launch(ops, x, gate, slots, I, k, normalize, bias=None):
     ops.route_topk(x, gate, k, normalize, bias=bias, out=(logits, ids, w))
     h = torch.empty(k * I, dtype=torch.bfloat16, device=DEV)
     out = torch.empty((1, H), dtype=torch.bfloat16, device=DEV)
-    ops.swiglu_decode(x, ids, w, slots, H, I, h, out)
+    ops.swiglu_decode(x, ids, w, slots, H, I, h, out, merge=merge)
     return logits, ids, w, out
 
 
-def _fused(ops, x, gate, slots, I, k, normalize, bias=None):
+def _fused(ops, x, gate, slots, I, k, normalize, bias=None, merge="fused"):
     E, H = gate.shape
     logits = torch.empty((1, E), dtype=torch.bfloat16, device=DEV)
     ids = torch.empty((1, k), dtype=torch.int32, device=DEV)
@@ -47,7 +47,7 @@ def _fused(ops, x, gate, slots, I, k, normalize, bias=None):
     out = torch.empty((1, H), dtype=torch.bfloat16, device=DEV)
     probs = torch.empty((1, E), dtype=torch.float32, device=DEV)
     ops.decode_layer(x, gate, slots, I, k, normalize, bias=bias, out=out, logits=logits, ids=ids, weights=w,
-                     h_ws=h, probs=probs)
+                     h_ws=h, probs=probs, merge=merge)
     return logits, ids, w, out, probs
 
 
@@ -66,23 +66,22 @@ SHAPES = [
     dict(H=2048, I=768, E=128, k=8, normalize=True),    # Qwen3-30B-A3B
     dict(H=1024, I=512, E=64, k=4, normalize=True),
     dict(H=2048, I=1408, E=64, k=2, normalize=False),  # DeepSeek-V2-Lite widths, k within the fused limits
-    dict(H=4096, I=256, E=32, k=3, normalize=True),
     dict(H=2048, I=512, E=256, k=8, normalize=True),   # 256 experts: four candidates per lane in the top-k
 ]
 
 
+@pytest.mark.parametrize("merge", ["fused", "reference"])
 @pytest.mark.parametrize("shape", SHAPES, ids=lambda s: f"H{s['H']}_I{s['I']}_E{s['E']}_k{s['k']}")
-def test_fused_equals_three_launch(pd, shape):
+def test_fused_equals_three_launch(pd, shape, merge):
     ops, layer, synthetic = pd
     H, I, E, k, nrm = shape["H"], shape["I"], shape["E"], shape["k"], shape["normalize"]
-    if not ops.decode_layer_supported(H, I, E, k, DEV):
-        pytest.skip("shape not resident on this device")
+    assert ops.decode_layer_supported(H, I, E, k, DEV), "the fused kernel should cover this shape"
     lay = synthetic.make_layer(H, I, E, k, nrm, seed=900 + H + I, device=DEV)
     slots = ops.slot_table([lay.experts[e] for e in range(E)], DEV)
     for seed in (1, 2, 3, 4):
         x = synthetic.make_tokens(1, H, seed=seed * 31 + E, device=DEV)
-        a = _three_launch(ops, x, lay.gate, slots, I, k, nrm)
-        b = _fused(ops, x, lay.gate, slots, I, k, nrm)
+        a = _three_launch(ops, x, lay.gate, slots, I, k, nrm, merge=merge)
+        b = _fused(ops, x, lay.gate, slots, I, k, nrm, merge=merge)
         torch.cuda.synchronize()
         for name, u, v in zip(("logits", "ids", "weights", "out"), a, b[:4]):
             assert torch.equal(u.view(torch.int16) if u.dtype == torch.bfloat16 else u,
@@ -168,10 +167,63 @@ def test_fused_graph_replay(pd):
     _assert_sync_clean(ops)
 
 
+def test_decode_reference_merge_is_the_ordered_merge_of_the_expert_rows(orc, pd):
+    """merge='reference' in both decode paths: the k expert outputs added in
+    ascending expert id in bf16 arithmetic.  Each expert's output y_s is read
+    off a k=1 decode call with weight 1.0 (bf16(1 * y_s) = y_s, and a slot's
+    down dot product does not depend on k), and the layer output must equal
+    the oracle's ordered merge of those rows bit for bit.  The grouped path's
+    ordered merge is checked against the oracle on its own rows."""
+    ops, layer, synthetic = pd
+    H, I, E, k = 2048, 768, 128, 8
+    lay = synthetic.make_layer(**synthetic.QWEN, seed=79, device=DEV)
+    slots = ops.slot_table([lay.experts[e] for e in range(E)], DEV)
+    one = torch.ones(1, dtype=torch.bfloat16, device=DEV)
+    h = torch.empty(I, dtype=torch.bfloat16, device=DEV)
+    ws = layer.MoEWorkspace(2, H, I, E, k, DEV)
+    for seed in (21, 22, 23):
+        x = synthetic.make_tokens(1, H, seed=seed, device=DEV)
+        a = _three_launch(ops, x, lay.gate, slots, I, k, True, merge="reference")
+        b = _fused(ops, x, lay.gate, slots, I, k, True, merge="reference")
+        torch.cuda.synchronize()
+        ids = a[1].cpu().numpy()[0]
+        rank = np.argsort(np.argsort(ids)).astype(np.int32)   # grouped row of slot s: rank of its expert id
+        y = np.empty((k, H), np.uint16)
+        for s in range(k):
+            ys = torch.empty((1, H), dtype=torch.bfloat16, device=DEV)
+            ops.swiglu_decode(x, a[1][:, s:s + 1].contiguous(), one.view(1, 1), slots, H, I, h, ys)
+            torch.cuda.synchronize()
+            y[rank[s]] = u16(ys)[0]
+        ref = orc.merge_ordered(y, rank, u16(a[2]))
+        assert np.array_equal(u16(a[3]), ref), "three-launch decode, reference merge"
+        assert np.array_equal(u16(b[3]), ref), "single-launch decode, reference merge"
+        # grouped path, two tokens: ordered merge of its own expert rows
+        x2 = torch.cat([x, synthetic.make_tokens(1, H, seed=seed + 50, device=DEV)])
+        out2, _, ids2, w2 = layer.moe_forward(x2, lay.gate, slots, ws, merge="reference")
+        torch.cuda.synchronize()
+        p = orc.pack(ids2.cpu().numpy(), E)
+        y2 = u16(ws.y[:2 * k * H]).reshape(2 * k, H)
+        assert np.array_equal(u16(out2), orc.merge_ordered(y2, p["row_of"], u16(w2)))
+    _assert_sync_clean(ops)
+
+
 def test_unsupported_shape_falls_back(pd):
     """DeepSeek-V2-Lite top-6 with I=1408 exceeds the fused kernel's register
-    plan: moe_forward falls back to route + decode GEMV, which still matches."""
+    plan: moe_forward falls back to route + decode GEMV, which still matches.
+    So does H=4096 with three experts of 256, whose 1024 blocks cannot all be
+    resident under the kernel's two-blocks-per-CU register budget."""
     ops, layer, synthetic = pd
+    assert not ops.decode_layer_supported(4096, 256, 32, 3, DEV)
+    lay = synthetic.make_layer(4096, 256, 32, 3, True, seed=6, device=DEV)
+    slots = ops.slot_table([lay.experts[e] for e in range(32)], DEV)
+    x = synthetic.make_tokens(1, 4096, seed=4, device=DEV)
+    with pytest.raises(ValueError):
+        _fused(ops, x, lay.gate, slots, 256, 3, True)
+    ws = layer.MoEWorkspace(1, 4096, 256, 32, 3, DEV)
+    out, _, ids, _ = layer.moe_forward(x, lay.gate, slots, ws)
+    a = _three_launch(ops, x, lay.gate, slots, 256, 3, True)
+    torch.cuda.synchronize()
+    assert torch.equal(ids, a[1]) and torch.equal(out.view(torch.int16), a[3].view(torch.int16))
     assert not ops.decode_layer_supported(2048, 1408, 64, 6, DEV)
     lay = synthetic.make_layer(2048, 1408, 64, 6, False, seed=5, device=DEV)
     slots = ops.slot_table([lay.experts[e] for e in range(64)], DEV)

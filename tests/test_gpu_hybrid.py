@@ -205,3 +205,209 @@ def test_transformers_model_through_expert_blocks(orc):
         closure(session.runtime)
     finally:
         session.close()
+
+
+# ---------------------------------------------------------------- drop-in switches of the runtime
+
+class NativeOracleBackend(OracleCpuBackend):
+    """A CPU backend that also exposes the native queue objects the decode
+    tail drives (native_group_handles / note_native_dispatch) and a packed
+    submit_many; every expert is computed by the oracle."""
+
+    def __init__(self, orc, masters, layers_u16, H, I):
+        super().__init__(orc, masters)
+        from tests.test_gpu_runtime import _OracleLayer, _Pool
+        self.pool = _Pool()
+        self.native_layers = {l: _OracleLayer(orc, e, H, I) for l, e in layers_u16.items()}
+        self.native_rows, self.packed_calls = 0, 0
+
+    def native_group_handles(self, layer):
+        obj = self.native_layers.get(layer)
+        return None if obj is None else (self.pool, obj)
+
+    def note_native_dispatch(self, rows):
+        self.native_rows += rows
+
+    def submit_many(self, jobs):
+        from concurrent.futures import Future
+        self.packed_calls += 1
+        out = {}
+        for key, rows in jobs.items():
+            f = Future()
+            f.set_result(self(key, rows))
+            out[key] = f
+        return out
+
+
+def test_runtime_native_dispatch_runs_the_decode_cpu_group(orc, tmp_path):
+    """merge='fused' with native_dispatch: decode CPU experts go through
+    submit_group / finish_and_merge as one native group (pdscope_runtime.py:
+    284-298, 407-426), their rows staged and added into the output before the
+    GPU rows are merged on top; every output within tolerance of the oracle."""
+    from pdscope_amd import pdscope_layer_dispatch
+    from pdscope_amd.cache import ExpertKey
+    from pdscope_amd.pdscope_runtime import PDScopeCudaRuntime
+    H, I, E, k = 256, 128, 32, 4
+    layers, masters = build(2, H, I, E, k, seed=61)
+    backend = NativeOracleBackend(orc, masters, {l: u16(layers[l].experts) for l in range(2)}, H, I)
+    hot = [ExpertKey(l, e, "bf16") for l in range(2) for e in range(6)]
+    rt = PDScopeCudaRuntime(masters, hot_keys=hot, speculative_slots=2, demand_slots=2, merge="fused",
+                            costs=cost_table(tmp_path, 0.02), cpu_backend=backend,
+                            native_dispatch=pdscope_layer_dispatch, decode_cpu_target=2)
+    native_layers = 0
+    try:
+        gen = torch.Generator(device=DEV).manual_seed(62)
+        for step, T in enumerate((16, 1, 1, 1)):
+            x = torch.randn((T, H), generator=gen, device=DEV).to(torch.bfloat16)
+            for l in range(2):
+                out, routing, row = rt.forward(x, layers[l].gate, layer=l, step=step, top_k=k,
+                                               next_gate=layers[1].gate if l == 0 else None)
+                torch.cuda.synchronize()
+                check_output(orc, out, routing, x, layers[l], H, I, k, row=row)
+                if row["decode_submission"] == "native_group":
+                    native_layers += 1
+                    assert row["counters"]["cpu_completed_experts"] == len(row["decision"]["cpu_queue"]) > 0
+        assert native_layers > 0 and backend.native_rows > 0
+        closure(rt)
+    finally:
+        rt.close()
+
+
+def test_runtime_cpu_batch_packs_cpu_experts_into_one_submission(orc, tmp_path):
+    from pdscope_amd.cache import ExpertKey
+    from pdscope_amd.pdscope_runtime import PDScopeCudaRuntime
+    H, I, E, k = 256, 128, 32, 4
+    layers, masters = build(1, H, I, E, k, seed=63)
+    backend = NativeOracleBackend(orc, masters, {}, H, I)
+    rt = PDScopeCudaRuntime(masters, hot_keys=[ExpertKey(0, e, "bf16") for e in range(4)], speculative_slots=0,
+                            costs=cost_table(tmp_path, 0.02), cpu_backend=backend, cpu_batch="both")
+    try:
+        x = torch.randn((24, H), generator=torch.Generator(device=DEV).manual_seed(64), device=DEV).to(torch.bfloat16)
+        out, routing, row = rt.forward(x, layers[0].gate, layer=0, step=0, top_k=k)
+        torch.cuda.synchronize()
+        check_output(orc, out, routing, x, layers[0], H, I, k, row=row)
+        assert row["decision"]["cpu_queue"] and backend.packed_calls == 1 and row["cpu_packing"] is True
+        closure(rt)
+    finally:
+        rt.close()
+    # a backend without submit_many cannot run packed CPU groups
+    rt = PDScopeCudaRuntime(masters, hot_keys=[ExpertKey(0, e, "bf16") for e in range(4)], speculative_slots=0,
+                            costs=cost_table(tmp_path, 0.02), cpu_backend=OracleCpuBackend(orc, masters),
+                            cpu_batch="both")
+    try:
+        with pytest.raises(ValueError, match="submit_many"):
+            rt.forward(x, layers[0].gate, layer=0, step=0, top_k=k)
+    finally:
+        rt.close()
+
+
+def test_runtime_input_pregather_gives_the_same_bits(orc):
+    """input_pregather gathers the activation rows into grouped order once and
+    the grouped kernels read them in order: same tiles, same arithmetic, the
+    same output bit for bit (also through the demand staging batches)."""
+    from pdscope_amd.cache import ExpertKey
+    from pdscope_amd.pdscope_runtime import PDScopeCudaRuntime
+    H, I, E, k = 256, 128, 32, 4
+    layers, masters = build(1, H, I, E, k, seed=65)
+    hot = [ExpertKey(0, e, "bf16") for e in range(12)]
+    x = torch.randn((200, H), generator=torch.Generator(device=DEV).manual_seed(66), device=DEV).to(torch.bfloat16)
+    outs = []
+    for pre in (False, True):
+        rt = PDScopeCudaRuntime(masters, hot_keys=hot, speculative_slots=0, demand_slots=8, input_pregather=pre)
+        try:
+            out, routing, row = rt.forward(x, layers[0].gate, layer=0, step=0, top_k=k)
+            torch.cuda.synchronize()
+            assert row["input_pregather"] is pre and row["decision"]["on_demand_queue"]
+            outs.append(out.clone())
+            closure(rt)
+        finally:
+            rt.close()
+    assert torch.equal(outs[0], outs[1])
+    check_output(orc, outs[1], routing, x, layers[0], H, I, k)
+
+
+def test_runtime_graph_output_pool_is_a_two_deep_ring(orc):
+    """graph_output_pool: decode layers return a view of one of two graph
+    output buffers per layer, alternating, with no copy per call; each output
+    equals the eager single-launch layer until the call after next."""
+    from pdscope_amd import layer, ops, synthetic
+    from pdscope_amd.cache import ExpertKey
+    from pdscope_amd.pdscope_runtime import PDScopeCudaRuntime
+    q = synthetic.QWEN
+    layers, masters = build(1, q["H"], q["I"], q["E"], q["k"], seed=67)
+    rt = PDScopeCudaRuntime(masters, hot_keys=[ExpertKey(0, e, "bf16") for e in range(q["E"])], speculative_slots=0,
+                            resident_graphs=True, graph_output_pool=True)
+    slots = ops.slot_table([layers[0].experts[e] for e in range(q["E"])], DEV)
+    ws = layer.MoEWorkspace(1, q["H"], q["I"], q["E"], 8, DEV)
+    try:
+        rt.forward(synthetic.make_tokens(4, q["H"], seed=68), layers[0].gate, layer=0, step=0)
+        ptrs = []
+        for step in range(1, 5):
+            x = synthetic.make_tokens(1, q["H"], seed=68 + step)
+            out, routing, row = rt.forward(x, layers[0].gate, layer=0, step=step)
+            ref, _, _, _ = layer.moe_forward(x, layers[0].gate, slots, ws, merge=rt.merge)
+            torch.cuda.synchronize()
+            assert row["decode_path"] == "graph" and row["graph_output_pool"] is True
+            assert torch.equal(out, ref)
+            ptrs.append(out.data_ptr())
+        assert ptrs[0] == ptrs[2] and ptrs[1] == ptrs[3] and ptrs[0] != ptrs[1]
+        closure(rt)
+    finally:
+        rt.close()
+
+
+def test_runtime_planned_decode_replays_graphs_with_calibrated_costs(orc, tmp_path):
+    """With a cost table, a CPU backend and resident_graphs, construction
+    calibrates the graph replay (graph_cost_mode='measured' charges it to
+    one-token GPU work); a decode plan that keeps every expert on the GPU is
+    served by the layer graph."""
+    from pdscope_amd.cache import ExpertKey
+    from pdscope_amd.costs import ResidentGraphCosts
+    from pdscope_amd.pdscope_runtime import PDScopeCudaRuntime
+    H, I, E, k = 256, 128, 32, 4
+    layers, masters = build(1, H, I, E, k, seed=69)
+    base = cost_table(tmp_path, 50.0)
+    rt = PDScopeCudaRuntime(masters, hot_keys=[ExpertKey(0, e, "bf16") for e in range(E)], speculative_slots=0,
+                            costs=base, cpu_backend=OracleCpuBackend(orc, masters), resident_graphs=True,
+                            graph_cost_mode="measured", decode_cpu_target=0)
+    try:
+        cal = rt.graph_cost_calibration
+        assert cal is not None and cal["scheduler_cost_mode"] == "measured" and cal["per_expert_ms"] > 0
+        assert isinstance(rt.costs, ResidentGraphCosts) and rt.costs.for_load(1)["gpu_ms"] == cal["per_expert_ms"]
+        gen = torch.Generator(device=DEV).manual_seed(70)
+        rt.forward(torch.randn((8, H), generator=gen, device=DEV).to(torch.bfloat16), layers[0].gate, layer=0,
+                   step=0, top_k=k)
+        for step in range(1, 4):
+            x = torch.randn((1, H), generator=gen, device=DEV).to(torch.bfloat16)
+            out, routing, row = rt.forward(x, layers[0].gate, layer=0, step=step, top_k=k)
+            torch.cuda.synchronize()
+            assert row["decision"]["cpu_queue"] == [] and row["decode_path"] == "graph"
+            check_output(orc, out, routing, x, layers[0], H, I, k)
+        closure(rt)
+    finally:
+        rt.close()
+    with pytest.raises(ValueError):
+        PDScopeCudaRuntime(masters, hot_keys=[], speculative_slots=0, graph_cost_mode="other")
+
+
+def test_runtime_reference_merge_is_the_bf16_expert_order_sum(orc):
+    """merge='reference' (the default): the layer output is the reference's
+    per-expert bf16 index_add_ sequence over the runtime's own expert rows,
+    bit for bit (the oracle's ordered merge of ws.y)."""
+    from pdscope_amd.cache import ExpertKey
+    from pdscope_amd.pdscope_runtime import PDScopeCudaRuntime
+    H, I, E, k = 256, 128, 32, 4
+    layers, masters = build(1, H, I, E, k, seed=71)
+    rt = PDScopeCudaRuntime(masters, hot_keys=[ExpertKey(0, e, "bf16") for e in range(E)], speculative_slots=0)
+    try:
+        assert rt.merge == "reference"
+        x = torch.randn((64, H), generator=torch.Generator(device=DEV).manual_seed(72), device=DEV).to(torch.bfloat16)
+        out, routing, row = rt.forward(x, layers[0].gate, layer=0, step=0, top_k=k)
+        torch.cuda.synchronize()
+        ws = rt._ws[k]
+        y = u16(ws.y[:64 * k * H]).reshape(64 * k, H)
+        p = orc.pack(routing.selected.cpu().numpy().astype(np.int32), E)
+        assert np.array_equal(u16(out), orc.merge_ordered(y, p["row_of"], u16(routing.weights)))
+        check_output(orc, out, routing, x, layers[0], H, I, k)
+    finally:
+        rt.close()

@@ -412,6 +412,26 @@ def test_merge_matches_oracle(orc, pd):
     assert m["max_rel"] < 1e-2
 
 
+@pytest.mark.parametrize("T,k", [(300, 8), (40, 6), (1500, 8), (200, 16)])
+def test_merge_ordered_matches_oracle_bit_exact(orc, pd, T, k):
+    """merge='reference': rows added in ascending grouped row (expert id) in
+    bf16 arithmetic, bit-exact with the oracle, with and without the
+    unweighted add_in (added last); T > 1024 runs the any-k loop."""
+    ops, _, _ = pd
+    rng = np.random.default_rng(13 + T + k)
+    H = 2048
+    y = orc.f32_to_bf16(rng.standard_normal((T * k, H)).astype(np.float32) * 0.3)
+    w = orc.f32_to_bf16(rng.random((T, k)).astype(np.float32) / k)
+    row_of = rng.permutation(T * k).astype(np.int32)
+    add = orc.f32_to_bf16(rng.standard_normal((T, H)).astype(np.float32))
+    out = torch.empty((T, H), dtype=torch.bfloat16, device=DEV)
+    for add_in in (None, add):
+        ops.merge(from_u16(y), torch.from_numpy(row_of).to(DEV), from_u16(w), out,
+                  add_in=None if add_in is None else from_u16(add_in), mode="reference")
+        torch.cuda.synchronize()
+        assert np.array_equal(u16(out), orc.merge_ordered(y, row_of, w, add_in=add_in))
+
+
 def test_stage_merge_matches_bf16_index_add(pd):
     ops, _, _ = pd
     rows, H = 8, 2048

@@ -332,3 +332,55 @@ def test_cpu_baseline_kernel_matches_oracle(orc):
                             orc.bf16_to_f32(w[0]), ptrs, H, I, 4)
     merged = (orc.bf16_to_f32(rows).astype(np.float64)).sum(0)
     assert np.abs(merged - b).max() / np.abs(b).max() < 2e-2
+
+
+# ------------------------------------------------------------------ reference-order merge / native tail
+
+def test_merge_ordered_matches_torch_per_expert_index_add(orc):
+    """merge='reference' (pdscope_runtime.py:454-468): the torch-CPU fixture adds
+    each expert's weighted rows with index_add_ in ascending expert id; the
+    oracle's per-token restatement must equal it bit for bit, and so must the
+    row-by-row index_add over the grouped rows."""
+    d = np.load(GOLDEN / "merge_t48.npz")
+    ids, w, y, want = d["ids"], d["weights"], d["y"], d["out"]
+    T, k = ids.shape
+    p = orc.pack(ids, 32)
+    assert np.array_equal(orc.merge_ordered(y, p["row_of"], w), want)
+    rows_w = w.reshape(-1)[p["perm_pos"]]
+    got = orc.index_add_bf16(np.zeros_like(want), p["perm_token"], y, rows_w)
+    assert np.array_equal(got, want)
+
+
+def test_merge_ordered_planted_mistakes_are_caught(orc):
+    d = np.load(GOLDEN / "merge_t48.npz")
+    ids, w, y, want = d["ids"], d["weights"], d["y"], d["out"]
+    p = orc.pack(ids, 32)
+    # one rounding in fp32 instead of bf16 sequential adds
+    assert not np.array_equal(orc.merge(y, p["row_of"], w), want)
+    # descending instead of ascending expert order
+    rows_w = w.reshape(-1)[p["perm_pos"]]
+    rev = np.arange(y.shape[0])[::-1].copy()
+    got = orc.index_add_bf16(np.zeros_like(want), p["perm_token"][rev], y[rev], rows_w[rev])
+    assert not np.array_equal(got, want)
+
+
+def test_index_add_bf16_matches_native_tail_fixture(orc):
+    """native_layer_dispatch.cpp:88: out.index_add_(0, tokens, scratch * weights[:, None]).
+    Decode group (every row adds into token 0): each add rounded to bf16, rows
+    in order; a group of distinct tokens: one add per token."""
+    d = np.load(GOLDEN / "native_tail_r6.npz")
+    rows = d["scratch"].shape[0]
+    got = orc.index_add_bf16(d["out0"][:1], np.zeros(rows, np.int64), d["scratch"], d["weights"])
+    assert np.array_equal(got, d["out_decode"])
+    got = orc.index_add_bf16(d["out0"], d["tokens"], d["scratch"], d["weights"])
+    assert np.array_equal(got, d["out_distinct"])
+    # a single row reduces to one bf16 product and one bf16 sum
+    one = orc.index_add_bf16(d["out0"][:1], np.zeros(1, np.int64), d["scratch"][:1], d["weights"][:1])
+    prod = orc.f32_to_bf16(orc.bf16_to_f32(d["scratch"][0]) * orc.bf16_to_f32(d["weights"][:1])[0])
+    assert np.array_equal(one[0], orc.f32_to_bf16(orc.bf16_to_f32(d["out0"][0]) + orc.bf16_to_f32(prod)))
+    # planted: fp32 accumulation of the decode group's rows (one rounding) differs
+    acc = orc.bf16_to_f32(d["out0"][0]).astype(np.float32)
+    for r in range(rows):
+        acc = acc + orc.bf16_to_f32(orc.f32_to_bf16(orc.bf16_to_f32(d["scratch"][r]) *
+                                                    orc.bf16_to_f32(d["weights"][r:r + 1])[0]))
+    assert not np.array_equal(orc.f32_to_bf16(acc), d["out_decode"][0])
