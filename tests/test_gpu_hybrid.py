@@ -411,3 +411,45 @@ def test_runtime_reference_merge_is_the_bf16_expert_order_sum(orc):
         check_output(orc, out, routing, x, layers[0], H, I, k)
     finally:
         rt.close()
+
+
+def test_measured_requests_write_the_reference_run_files(tmp_path):
+    """pdscope_amd.compare on a small random Qwen3-MoE model: two warm-up and
+    one measured request, each a prefill plus decode forwards through the
+    runtime, recorded as manifest / cases / requests / traces / result with
+    the reference's key sets; trace rows and ledger counters close."""
+    import gzip
+    import json
+    from pdscope_amd import compare
+    from tests.test_records import MANIFEST_END_KEYS, MANIFEST_KEYS, METRIC_KEYS, REQUEST_KEYS, RESULT_KEYS
+    model = compare.random_qwen3_moe(2, vocab_size=512, hidden_size=256, intermediate_size=512,
+                                     moe_intermediate_size=128, num_attention_heads=4, num_key_value_heads=2,
+                                     head_dim=64, num_experts=32, num_experts_per_tok=4)
+    with torch.no_grad():
+        for d in model.model.layers:
+            d.mlp.gate.weight.normal_(0.0, 0.5)
+    specs = compare.build_cases([24], repetitions=1, output_tokens=4, warmups=2, demand_slots=4,
+                                resident_graphs=True, merge="reference")
+    out = tmp_path / "run" / "result.json"
+    result = compare.run(model, specs, output=out, argv=["test"], config=dict(test=True), model_name="tiny",
+                         hot_per_layer=8, speculative_slots=4, demand_slots=4, resident_graphs=True,
+                         merge="reference")
+    run = out.parent
+    man = json.loads((run / "manifest.json").read_text())
+    assert MANIFEST_KEYS | MANIFEST_END_KEYS <= set(man) and man["status"] == "completed"
+    res = json.loads(out.read_text())
+    assert RESULT_KEYS <= set(res) and res["status"] == "completed" and res["measured_performance"]
+    reqs = [json.loads(x) for x in (run / "requests.jsonl").read_text().splitlines()]
+    assert len(reqs) == 3 and [r["case"]["role"] for r in reqs] == ["warmup", "warmup", "measure"]
+    for r in reqs:
+        assert REQUEST_KEYS <= set(r) and METRIC_KEYS == set(r["metrics"])
+        assert len(r["generated_ids"]) == 4 and r["kv_final_length"] == 24 + 3
+        with gzip.open(run / r["trace"]["path"], "rt") as f:
+            rows = json.load(f)
+        assert len(rows) == 4 * 2 and [x["step"] for x in rows] == [0, 0, 1, 1, 2, 2, 3, 3]
+        assert all(x["decode_path"] == "graph" for x in rows if x["phase"] == "decode")
+        assert r["cache_stats"]["physical_demand_tokens"] == (24 + 3) * 2 * 4
+    assert result["requests"][-1]["generated_ids"] == reqs[-1]["generated_ids"]
+    # the three requests share the prompt and the model: the same greedy tokens
+    assert len({tuple(r["generated_ids"]) for r in reqs}) == 1
+    assert res["attention_cost_table"] and res["master_storage"]["experts_copied"] == 64
