@@ -236,6 +236,28 @@ int pdscope_decode_layer(const void *x, const void *gate, const float *bias, int
                          void *stream);
 
 /*
+ * pdscope_decode_layer for one layer of a chain of decode layers, with the
+ * residual sum and the next layer's gate-fallback prediction folded in:
+ * replaces, besides what pdscope_decode_layer replaces, the predictor route
+ * route(inputs, next_gate, top_k, normalize) of
+ * expertbench/pdscope_runtime.py:245-249 (the ids that pick the next layer's
+ * prefetches).
+ *   resid, x_out   both NULL, or both [H] bf16: the layer input is then
+ *                  bf16(x + resid) (fp32 sum, one rounding), written to x_out;
+ *   next_gate, pred_out  both NULL, or [E,H] bf16 and [k] int32: pred_out
+ *                  receives the top-k of next_gate . input (no bias), the
+ *                  ids pdscope_route_topk gives for that gate and input.
+ *                  Needs E <= H/2.
+ * Every other argument and output is as in pdscope_decode_layer, and with
+ * all four NULL the call is pdscope_decode_layer.
+ */
+int pdscope_decode_layer_chained(const void *x, const void *resid, void *x_out, const void *gate,
+                                 const float *bias, int H, int E, int k, int normalize, int merge_mode,
+                                 const void *const *slots, int I, const void *next_gate, int32_t *pred_out,
+                                 void *logits, int32_t *ids, void *weights, float *probs, void *h_ws, void *out,
+                                 void *workspace, void *stream);
+
+/*
  * A7 demand staging: replaces the three per-projection non_blocking copies
  * (expertbench/executor.py:341-363).  One hipMemcpyAsync of `bytes` from
  * page-locked host memory into a cache or staging slot on `stream`, then

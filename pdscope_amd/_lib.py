@@ -41,6 +41,8 @@ SIGNATURES = {
     "pdscope_decode_layer_supported": ([_i32, _i32, _i32, _i32], _i32),
     "pdscope_decode_layer": ([_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
                               _vp, _vp], _i32),
+    "pdscope_decode_layer_chained": ([_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _i32, _vp, _vp,
+                                      _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp], _i32),
     "pdscope_stage_expert": ([_vp, _vp, _sz, _vp, _vp], _i32),
     "pdscope_stage_merge": ([_vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp], _i32),
     "pdscope_dispatch_pack": ([_vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp], _i32),

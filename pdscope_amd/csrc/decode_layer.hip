@@ -75,7 +75,8 @@ constexpr int kWsEpoch = 0;                          // [kDecodeMaxBlocks] per-b
 constexpr int kWsError = kDecodeMaxBlocks;           // sticky error word
 constexpr int kWsLogit = kWsError + 32;              // [kDecodeMaxE / 4] lines of 4 published logits
 constexpr int kWsH = kWsLogit + kDecodeMaxE * 8;     // [kDecodeMaxKI] published h
-constexpr int kWsWords = kWsH + kDecodeMaxKI;
+constexpr int kWsPLogit = kWsH + kDecodeMaxKI;       // [kDecodeMaxE / 4] lines of next-layer predictor logits
+constexpr int kWsWords = kWsPLogit + kDecodeMaxE * 8;
 
 __device__ __forceinline__ uint64_t load_pair(const uint32_t *w) {
     return __hip_atomic_load(reinterpret_cast<const uint64_t *>(w), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -148,123 +149,12 @@ __device__ __forceinline__ void collect(const uint32_t *w, int count, int t, int
     }
 }
 
-// NCH: 16-byte chunks per lane of an H row (>= H/8/64); P: gate/up row pairs
-// per wave (>= k*I / waves); DC: 16-byte chunks per half-wave lane of a
-// down row (>= I/8/32).  Larger values than needed are masked.
-template <int NCH, int P, int DC>
-__global__ __launch_bounds__(256, 2) void decode_layer_kernel(
-    const uint16_t *__restrict__ x, const uint16_t *__restrict__ gate, const float *__restrict__ bias, int H,
-    int E, int k, int normalize, int merge_mode, const uint16_t *const *__restrict__ slots, int I,
-    uint16_t *__restrict__ logits,
-    int32_t *__restrict__ ids, uint16_t *__restrict__ weights, float *__restrict__ probs,
-    uint16_t *__restrict__ h_ws, uint16_t *__restrict__ out, uint32_t *ws) {
-    extern __shared__ uint4 s_h[];       // k * I bf16
-    __shared__ float s_logit[kDecodeMaxE];
-    __shared__ uint32_t s_pub[16];
-    __shared__ float s_y[kDecodeMaxK * 4];
-    __shared__ const uint16_t *s_slot[kDecodeMaxE];
-    __shared__ TopkScratch s_tk;
-    __shared__ uint32_t s_epoch;
-
-    const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
-    const int C = H >> 3, CI = I >> 3;
-    const int RB = (E + 3) / 4;
-    uint32_t *err = ws + kWsError;
-    uint32_t budget = kSpinBudget;
-
-    if (tid == 0) {
-        uint32_t ep = (__hip_atomic_load(ws + kWsEpoch + blockIdx.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u) &
-                      0xffffu;
-        s_epoch = ep ? ep : 1u;
-    }
-    // router rows first (blocks 0 .. RB-1): their latency starts the chain
-    const int e_route = blockIdx.x * 4 + wave;
-    const bool routes = (int)blockIdx.x < RB;
-    uint4 wv[NCH];
-    if (routes) {
-        const uint4 *wrow = reinterpret_cast<const uint4 *>(gate + (size_t)min(e_route, E - 1) * H);
-#pragma unroll
-        for (int j = 0; j < NCH; ++j) wv[j] = wrow[min(lane + 64 * j, C - 1)];
-    }
-    uint4 xv[NCH];
-#pragma unroll
-    for (int j = 0; j < NCH; ++j) xv[j] = reinterpret_cast<const uint4 *>(x)[min(lane + 64 * j, C - 1)];
-    for (int e = tid; e < E; e += blockDim.x) s_slot[e] = slots[e];
-    __syncthreads();
-    const uint32_t epoch = s_epoch;
-
-    // ---- 1. router logits: block r computes experts 4r..4r+3 and publishes
-    // them as one 16-byte write into a 128-byte line of its own (one writer
-    // per line: partial writes of one line by many agents serialise)
-    if (routes) {
-        const int e = e_route;
-        uint32_t b = 0;
-        if (e < E) {
-            float a = 0.0f;
-#pragma unroll
-            for (int j = 0; j < NCH; ++j)
-                if (lane + 64 * j < C) a = dot8(xv[j], wv[j], a);
-            a = wave_sum_dpp(a);
-            b = f2bf(a);
-        }
-        if (lane == 0) s_pub[wave] = (epoch << 16) | b;
-        __syncthreads();
-        if (tid == kPublisher) {
-            uint64_t *line = reinterpret_cast<uint64_t *>(ws + kWsLogit + blockIdx.x * 32);
-            __hip_atomic_store(line, (uint64_t)s_pub[0] | ((uint64_t)s_pub[1] << 32), __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(line + 1, (uint64_t)s_pub[2] | ((uint64_t)s_pub[3] << 32), __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-        }
-    }
-
-    // ---- 2. routing, computed by every block from the published logits
-    // (one wave collects them: pair j holds experts 2j, 2j+1 and sits in the
-    // line of route block j/2)
-    if (wave == 0) {
-        for (int j = lane; j < 2 * RB; j += 64) {
-            const uint32_t *w = ws + kWsLogit + (j >> 1) * 32 + (j & 1) * 2;
-            const uint64_t v = poll_pair(w, epoch, err, budget);
-            if (2 * j < E) s_logit[2 * j] = bf2f((uint32_t)v & 0xffffu);
-            if (2 * j + 1 < E) s_logit[2 * j + 1] = bf2f((uint32_t)(v >> 32) & 0xffffu);
-        }
-    }
-    __syncthreads();
-    {
-        const bool pub = blockIdx.x == 0;
-        if (E <= 128)
-            topk_block<2>(s_logit, bias, E, k, normalize, pub ? ids : nullptr, pub ? weights : nullptr,
-                          pub ? probs : nullptr, &s_tk);
-        else
-            topk_block<4>(s_logit, bias, E, k, normalize, pub ? ids : nullptr, pub ? weights : nullptr,
-                          pub ? probs : nullptr, &s_tk);
-    }
-
-    // ---- 3. issue the gate/up weight loads of this wave; block b owns the
-    // 4P consecutive (gate, up) row pairs q = 4P*b + P*wave + p
-    const int KI = k * I;
-    const int q0 = blockIdx.x * 4 * P + wave * P;
-    uint4 gv[P][NCH], uv[P][NCH];
-    bool has[P];
-#pragma unroll
-    for (int p = 0; p < P; ++p) {
-        const int q = min(q0 + p, KI - 1);
-        const int s = q / I, i = q - s * I;
-        const uint16_t *base = s_slot[s_tk.seli[s]];
-        // an expert without a ready copy reads the activation row instead
-        // (H elements, in bounds) and contributes h = 0
-        has[p] = base != nullptr;
-        const uint16_t *grow = base ? base + (size_t)i * H : x;
-        const uint16_t *urow = base ? base + (size_t)(I + i) * H : x;
-#pragma unroll
-        for (int j = 0; j < NCH; ++j) {
-            gv[p][j] = ld_nt(grow + 8 * min(lane + 64 * j, C - 1));
-            uv[p][j] = ld_nt(urow + 8 * min(lane + 64 * j, C - 1));
-        }
-    }
-    // ---- 4. gate/up -> h.  The 2P dot products are independent chains
-    // (each keeps its chunk order); interleaved, their latencies overlap.
-    float g[P], u[P];
+// g[p] = sum over the H row of gate row p times x, u[p] likewise for the up
+// row: per lane over its chunks in order, then across the wave.  The 2P
+// chains are independent and interleaved so that their latencies overlap.
+template <int P, int NCH>
+__device__ __forceinline__ void gate_up_dots(const uint4 (&gv)[P][NCH], const uint4 (&uv)[P][NCH],
+                                             const uint4 (&xv)[NCH], int C, int lane, float (&g)[P], float (&u)[P]) {
 #pragma unroll
     for (int p = 0; p < P; ++p) g[p] = u[p] = 0.0f;
 #pragma unroll
@@ -282,6 +172,168 @@ __global__ __launch_bounds__(256, 2) void decode_layer_kernel(
         g[p] = wave_sum_dpp(g[p]);
         u[p] = wave_sum_dpp(u[p]);
     }
+}
+
+// x_eff = bf16(x + r) for the 8 bf16 pairs of two uint4 (fp32 sum, one
+// round-to-nearest-even rounding by the hardware pair convert)
+__device__ __forceinline__ uint4 add_bf16x8(uint4 a, uint4 r) {
+    auto pair = [](uint32_t u, uint32_t v) { return f2bf2_hw(lo_bf(u) + lo_bf(v), hi_bf(u) + hi_bf(v)); };
+    return make_uint4(pair(a.x, r.x), pair(a.y, r.y), pair(a.z, r.z), pair(a.w, r.w));
+}
+
+// NCH: 16-byte chunks per lane of an H row (>= H/8/64); P: gate/up row pairs
+// per wave (>= k*I / waves); DC: 16-byte chunks per half-wave lane of a
+// down row (>= I/8/32).  Larger values than needed are masked.
+//
+// Optional inputs (all may be null):
+//   resid    the layer input is x_eff = bf16(x + resid) (a residual stream);
+//            x_out receives x_eff (block 0) for the next layer's residual;
+//   next_gate / pred_out  the gate-fallback predictor of the next layer:
+//            top-k of next_gate . x_eff (no bias) into pred_out[k].
+template <int NCH, int P, int DC, bool CHAIN>
+__global__ __launch_bounds__(256, 2) void decode_layer_kernel(
+    const uint16_t *__restrict__ x, const uint16_t *__restrict__ resid, uint16_t *__restrict__ x_out,
+    const uint16_t *__restrict__ gate, const float *__restrict__ bias, int H, int E, int k, int normalize,
+    int merge_mode, const uint16_t *const *__restrict__ slots, int I, const uint16_t *__restrict__ next_gate,
+    int32_t *__restrict__ pred_out, uint16_t *__restrict__ logits, int32_t *__restrict__ ids, uint16_t *__restrict__ weights, float *__restrict__ probs,
+    uint16_t *__restrict__ h_ws, uint16_t *__restrict__ out, uint32_t *ws) {
+    extern __shared__ uint4 s_h[];       // k * I bf16
+    __shared__ float s_logit[kDecodeMaxE];
+    __shared__ uint32_t s_pub[16];
+    __shared__ float s_y[kDecodeMaxK * 4];
+    __shared__ const uint16_t *s_slot[kDecodeMaxE];
+    __shared__ TopkScratch s_tk;
+    __shared__ uint32_t s_epoch;
+
+    const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
+    const int C = H >> 3, CI = I >> 3;
+    const int RB = (E + 3) / 4;
+    uint32_t *err = ws + kWsError;
+    uint32_t budget = kSpinBudget;
+
+    // router rows first (blocks 0 .. RB-1): their latency starts the chain;
+    // with a next gate, blocks RB .. 2RB-1 compute the next layer's
+    // predictor logits
+    const bool routes = (int)blockIdx.x < RB;
+    const bool predicts = CHAIN && next_gate != nullptr && !routes && (int)blockIdx.x < 2 * RB;
+    const int e_route = (routes ? (int)blockIdx.x : (int)blockIdx.x - RB) * 4 + wave;
+    uint4 wv[NCH];
+    if (routes || predicts) {
+        const uint4 *wrow = reinterpret_cast<const uint4 *>((routes ? gate : next_gate) + (size_t)min(e_route, E - 1) * H);
+#pragma unroll
+        for (int j = 0; j < NCH; ++j) wv[j] = wrow[min(lane + 64 * j, C - 1)];
+    }
+    uint4 xv[NCH], rv[NCH];
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) xv[j] = reinterpret_cast<const uint4 *>(x)[min(lane + 64 * j, C - 1)];
+    const bool has_resid = CHAIN && resid != nullptr;
+    if (has_resid) {
+#pragma unroll
+        for (int j = 0; j < NCH; ++j) rv[j] = reinterpret_cast<const uint4 *>(resid)[min(lane + 64 * j, C - 1)];
+    }
+    // then the small words: this block's epoch and the slot table (one wait
+    // covers them and the rows above)
+    if (tid == 0) {
+        uint32_t ep = (__hip_atomic_load(ws + kWsEpoch + blockIdx.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u) &
+                      0xffffu;
+        s_epoch = ep ? ep : 1u;
+    }
+    for (int e = tid; e < E; e += blockDim.x) s_slot[e] = slots[e];
+    __syncthreads();
+    const uint32_t epoch = s_epoch;
+    // the residual sum: now where the router dot needs it, else while the
+    // gate/up rows stream
+    const bool add_now = has_resid && (routes || predicts);
+    if (add_now) {
+#pragma unroll
+        for (int j = 0; j < NCH; ++j) xv[j] = add_bf16x8(xv[j], rv[j]);
+    }
+
+    // ---- 1. router (or predictor) logits: block r computes experts
+    // 4r..4r+3 and publishes them as one 16-byte write into a 128-byte line
+    // of its own (one writer per line: partial writes of one line by many
+    // agents serialise)
+    if (routes || predicts) {
+        const int e = e_route;
+        uint32_t b = 0;
+        if (e < E) {
+            float a = 0.0f;
+#pragma unroll
+            for (int j = 0; j < NCH; ++j)
+                if (lane + 64 * j < C) a = dot8(xv[j], wv[j], a);
+            a = wave_sum_dpp(a);
+            b = f2bf(a);
+        }
+        if (lane == 0) s_pub[wave] = (epoch << 16) | b;
+        __syncthreads();
+        if (tid == kPublisher) {
+            uint64_t *line = reinterpret_cast<uint64_t *>(
+                ws + (routes ? kWsLogit + blockIdx.x * 32 : kWsPLogit + (blockIdx.x - RB) * 32));
+            __hip_atomic_store(line, (uint64_t)s_pub[0] | ((uint64_t)s_pub[1] << 32), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(line + 1, (uint64_t)s_pub[2] | ((uint64_t)s_pub[3] << 32), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+
+    // Block b owns the 4P consecutive (gate, up) row pairs q = 4P*b + P*wave + p
+    // of the k*I slot-major rows; slot s = q / I.
+    const int KI = k * I;
+    const int q0 = blockIdx.x * 4 * P + wave * P;
+
+    // ---- 2. routing, computed by every block from the published logits
+    // (one wave collects them: pair j holds experts 2j, 2j+1 and sits in the
+    // line of route block j/2)
+    if (wave == 0) {
+        for (int j = lane; j < 2 * RB; j += 64) {
+            const uint32_t *w = ws + kWsLogit + (j >> 1) * 32 + (j & 1) * 2;
+            const uint64_t v = poll_pair(w, epoch, err, budget);
+            if (2 * j < E) s_logit[2 * j] = bf2f((uint32_t)v & 0xffffu);
+            if (2 * j + 1 < E) s_logit[2 * j + 1] = bf2f((uint32_t)(v >> 32) & 0xffffu);
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {
+        const bool pub = blockIdx.x == 0;
+        if (E <= 128)
+            topk_token<2>(s_logit, bias, E, k, normalize, 0, pub ? ids : nullptr, pub ? weights : nullptr,
+                          pub ? probs : nullptr, &s_tk);
+        else
+            topk_token<4>(s_logit, bias, E, k, normalize, 0, pub ? ids : nullptr, pub ? weights : nullptr,
+                          pub ? probs : nullptr, &s_tk);
+    }
+    __syncthreads();
+
+    // ---- 3. the gate/up rows this wave computes
+    uint4 gv[P][NCH], uv[P][NCH];
+    bool has[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const int q = min(q0 + p, KI - 1);
+        const int sl = q / I, i = q - sl * I;
+        const uint16_t *base = s_slot[s_tk.seli[sl]];
+        // an expert without a ready copy reads the activation row instead
+        // (H elements, in bounds) and contributes h = 0
+        has[p] = base != nullptr;
+        const uint16_t *grow = base ? base + (size_t)i * H : x;
+        const uint16_t *urow = base ? base + (size_t)(I + i) * H : x;
+#pragma unroll
+        for (int j = 0; j < NCH; ++j) {
+            gv[p][j] = ld_nt(grow + 8 * min(lane + 64 * j, C - 1));
+            uv[p][j] = ld_nt(urow + 8 * min(lane + 64 * j, C - 1));
+        }
+    }
+    if (has_resid && !add_now) {
+#pragma unroll
+        for (int j = 0; j < NCH; ++j) xv[j] = add_bf16x8(xv[j], rv[j]);
+    }
+    // ---- 4. gate/up -> h
+    float g[P], u[P];
+    gate_up_dots<P, NCH>(gv, uv, xv, C, lane, g, u);
+    // h = bf16(silu(bf16(g)) * bf16(u)), lane 0 for the wave's P rows.  (One
+    // lane per row would publish earlier, but then the down rows below start
+    // earlier too and slow the blocks whose gate/up rows are still streaming:
+    // the last block's h, which every block waits for, comes later.)
     if (lane == 0) {
 #pragma unroll
         for (int p = 0; p < P; ++p) {
@@ -296,19 +348,19 @@ __global__ __launch_bounds__(256, 2) void decode_layer_kernel(
     if (tid >= kPublisher && tid < kPublisher + 2 * P) {
         const int t2 = tid - kPublisher;
         const int qb = blockIdx.x * 4 * P + 2 * t2;
-        if (qb < KI)
+        if (qb < KI) {
             __hip_atomic_store(reinterpret_cast<uint64_t *>(ws + kWsH + qb),
                                (uint64_t)s_pub[2 * t2] | ((uint64_t)s_pub[2 * t2 + 1] << 32), __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
 
-    // down rows, issued once every wave of the block has consumed its
-    // gate/up rows (the gate/up rows feed the h hand-off, the critical path;
-    // a wave that issued its down rows as soon as its own gate/up rows were
-    // in would slow its sibling waves' gate/up rows down; the down rows land
-    // during the hand-off): block b owns output columns
-    // 4b..4b+3; half-wave (wave w, half h) owns slot s = 2w + h and reads
-    // that expert's 4 rows, so a wave touches two experts' pages instead of k
+    // down rows, issued once the block has published its h words (the
+    // gate/up rows feed the h hand-off, the critical path; down rows issued
+    // while other waves' or blocks' gate/up rows stream delay them; these
+    // land during the hand-off): block b owns output columns 4b..4b+3;
+    // half-wave (wave w, half h) owns slot s = 2w + h and reads that
+    // expert's 4 rows, so a wave touches two experts' pages instead of k
     const int half = lane >> 5, hl = lane & 31;
     const int slot = 2 * wave + half;
     const size_t IH2 = 2 * (size_t)I * H;
@@ -323,7 +375,6 @@ __global__ __launch_bounds__(256, 2) void decode_layer_kernel(
 #pragma unroll
         for (int c = 0; c < DC; ++c) dv[c4][c] = ld_nt(row + 8 * min(hl + 32 * c, CI - 1));
     }
-
 
     // ---- 5. collect h (the other waves), then down + merge
     if (tid < kPublisher)
@@ -376,22 +427,54 @@ __global__ __launch_bounds__(256, 2) void decode_layer_kernel(
         if (col < H) out[col] = (uint16_t)f2bf(total);
     }
     // outputs off the critical path: the logits (block 0, from the collected
-    // words) and this block's h values
-    if (blockIdx.x == 0)
+    // words), this block's h values and the effective input
+    if (blockIdx.x == 0) {
         for (int e = tid; e < E; e += blockDim.x) logits[e] = (uint16_t)(__float_as_uint(s_logit[e]) >> 16);
+        if (CHAIN && x_out && wave == 0) {
+#pragma unroll
+            for (int j = 0; j < NCH; ++j)
+                if (lane + 64 * j < C) reinterpret_cast<uint4 *>(x_out)[lane + 64 * j] = xv[j];
+        }
+    }
     if (tid < 4 * P) {
         const int q = blockIdx.x * 4 * P + tid;
         if (q < KI) h_ws[q] = (uint16_t)s_pub[tid];
     }
+    // without a next gate, block 0 marks the predictor words invalid (epoch
+    // 0 is never current), so that words left by an earlier predicting
+    // launch cannot pass for a later one's when the 16-bit epoch wraps
+    if (CHAIN && !next_gate && blockIdx.x == 0 && tid < 2 * RB)
+        __hip_atomic_store(reinterpret_cast<uint64_t *>(ws + kWsPLogit + (tid >> 1) * 32 + (tid & 1) * 2), 0ull,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // the last block routes the next layer from the predictor logits (all
+    // published early in the launch) into pred_out
+    if (CHAIN && next_gate && blockIdx.x == gridDim.x - 1) {
+        __syncthreads();
+        if (wave == 0) {
+            for (int j = lane; j < 2 * RB; j += 64) {
+                const uint32_t *w = ws + kWsPLogit + (j >> 1) * 32 + (j & 1) * 2;
+                const uint64_t v = poll_pair(w, epoch, err, budget);
+                if (2 * j < E) s_logit[2 * j] = bf2f((uint32_t)v & 0xffffu);
+                if (2 * j + 1 < E) s_logit[2 * j + 1] = bf2f((uint32_t)(v >> 32) & 0xffffu);
+            }
+        }
+        __syncthreads();
+        if (E <= 128)
+            topk_block<2>(s_logit, nullptr, E, k, normalize, pred_out, nullptr, nullptr, &s_tk);
+        else
+            topk_block<4>(s_logit, nullptr, E, k, normalize, pred_out, nullptr, nullptr, &s_tk);
+    }
     if (tid == 0) __hip_atomic_store(ws + kWsEpoch + blockIdx.x, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-typedef void (*DecodeLayerFn)(const uint16_t *, const uint16_t *, const float *, int, int, int, int, int,
-                              const uint16_t *const *, int, uint16_t *, int32_t *, uint16_t *, float *, uint16_t *,
-                              uint16_t *, uint32_t *);
+typedef void (*DecodeLayerFn)(const uint16_t *, const uint16_t *, uint16_t *, const uint16_t *, const float *, int,
+                              int, int, int, int, const uint16_t *const *, int, const uint16_t *,
+                              int32_t *, uint16_t *, int32_t *, uint16_t *, float *, uint16_t *, uint16_t *,
+                              uint32_t *);
 
 struct DecodePlan {
-    DecodeLayerFn fn;
+    DecodeLayerFn fn;        // plain launch
+    DecodeLayerFn fn_chain;  // with the residual / next-layer predictor code
     int blocks;
     size_t lds;
 };
@@ -411,9 +494,12 @@ static int pick_decode(int H, int I, int k, DecodePlan *plan, std::string *why) 
         *why = "decode_layer: shape outside the fused kernel (needs H <= 4096, I <= 1536, k*I <= 4*H)";
         return kEInval;
     }
-    DecodeLayerFn fn = nullptr;
-#define PD_DL(N, PP, D) \
-    if (nch == N && p == PP && dc == D) fn = decode_layer_kernel<N, PP, D>;
+    DecodeLayerFn fn = nullptr, fn_chain = nullptr;
+#define PD_DL(N, PP, D)                                     \
+    if (nch == N && p == PP && dc == D) {                   \
+        fn = decode_layer_kernel<N, PP, D, false>;          \
+        fn_chain = decode_layer_kernel<N, PP, D, true>;     \
+    }
     PD_DL(2, 2, 3) PD_DL(2, 3, 3) PD_DL(2, 4, 3) PD_DL(2, 2, 6) PD_DL(2, 3, 6) PD_DL(2, 4, 6)
     PD_DL(4, 2, 3) PD_DL(4, 3, 3) PD_DL(4, 4, 3) PD_DL(4, 2, 6) PD_DL(4, 3, 6) PD_DL(4, 4, 6)
     PD_DL(8, 2, 3) PD_DL(8, 2, 6)
@@ -423,6 +509,7 @@ static int pick_decode(int H, int I, int k, DecodePlan *plan, std::string *why) 
         return kEInval;
     }
     plan->fn = fn;
+    plan->fn_chain = fn_chain;
     plan->blocks = blocks;
     plan->lds = (size_t)k * I * 2;
     return kOk;
@@ -474,10 +561,12 @@ PD_API int pdscope_decode_layer_supported(int H, int I, int E, int k) {
     return n >= plan.blocks ? 1 : 0;
 }
 
-PD_API int pdscope_decode_layer(const void *x, const void *gate, const float *bias, int H, int E, int k,
-                                int normalize, int merge_mode, const void *const *slots, int I, void *logits,
-                                int32_t *ids, void *weights, float *probs, void *h_ws, void *out, void *workspace,
-                                void *stream) {
+// Shared by both entry points: checks, plan, launch.
+static int launch_decode_layer(const void *x, const void *resid, void *x_out, const void *gate, const float *bias,
+                               int H, int E, int k, int normalize, int merge_mode, const void *const *slots, int I,
+                               const void *next_gate, int32_t *pred_out, void *logits,
+                               int32_t *ids, void *weights, float *probs, void *h_ws, void *out, void *workspace,
+                               void *stream) {
     if (!x || !gate || !slots || !logits || !ids || !weights || !h_ws || !out || !workspace)
         return fail(kEInval, "decode_layer: null pointer");
     if (H < 16 || H % 16) return fail(kEInval, "decode_layer: need H % 16 == 0");
@@ -488,18 +577,42 @@ PD_API int pdscope_decode_layer(const void *x, const void *gate, const float *bi
     if ((size_t)I > (size_t)E * H) return fail(kEInval, "decode_layer: need I <= E*H");
     if ((size_t)k * I * 2 > 64 * 1024) return fail(kEInval, "decode_layer: k*I*2 must fit 64 KiB of LDS");
     if ((E + 3) / 4 > (H + 3) / 4) return fail(kEInval, "decode_layer: need E <= H");
+    if (!next_gate != !pred_out) return fail(kEInval, "decode_layer: next_gate and pred_out go together");
+    if (next_gate && 2 * ((E + 3) / 4) > (H + 3) / 4)
+        return fail(kEInval, "decode_layer: the next-layer predictor needs E <= H/2");
     DecodePlan plan;
     std::string why;
     if (pick_decode(H, I, k, &plan, &why) != kOk) return fail(kEInval, why);
-    const int resident = resident_blocks(plan.fn, plan.lds, &why);
+    const bool chain = resid || next_gate;
+    const DecodeLayerFn fn = chain ? plan.fn_chain : plan.fn;
+    const int resident = resident_blocks(fn, plan.lds, &why);
     if (resident < 0) return fail(kEHip, why);
     if (resident < plan.blocks)
         return fail(kEInval, "decode_layer: the grid would not be resident at once on this device");
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    plan.fn<<<plan.blocks, 256, plan.lds, s>>>(
-        (const uint16_t *)x, (const uint16_t *)gate, bias, H, E, k, normalize, merge_mode,
-        (const uint16_t *const *)slots, I,
+    fn<<<plan.blocks, 256, plan.lds, s>>>(
+        (const uint16_t *)x, (const uint16_t *)resid, (uint16_t *)x_out, (const uint16_t *)gate, bias, H, E, k,
+        normalize, merge_mode, (const uint16_t *const *)slots, I, (const uint16_t *)next_gate, pred_out,
         (uint16_t *)logits, ids, (uint16_t *)weights, probs, (uint16_t *)h_ws, (uint16_t *)out,
         (uint32_t *)workspace);
     return check_launch("decode_layer_kernel");
+}
+
+PD_API int pdscope_decode_layer(const void *x, const void *gate, const float *bias, int H, int E, int k,
+                                int normalize, int merge_mode, const void *const *slots, int I, void *logits,
+                                int32_t *ids, void *weights, float *probs, void *h_ws, void *out, void *workspace,
+                                void *stream) {
+    return launch_decode_layer(x, nullptr, nullptr, gate, bias, H, E, k, normalize, merge_mode, slots, I, nullptr,
+                               nullptr, logits, ids, weights, probs, h_ws, out, workspace, stream);
+}
+
+PD_API int pdscope_decode_layer_chained(const void *x, const void *resid, void *x_out, const void *gate,
+                                        const float *bias, int H, int E, int k, int normalize, int merge_mode,
+                                        const void *const *slots, int I, const void *next_gate,
+                                        int32_t *pred_out, void *logits, int32_t *ids,
+                                        void *weights, float *probs, void *h_ws, void *out, void *workspace,
+                                        void *stream) {
+    if (!resid != !x_out) return fail(kEInval, "decode_layer_chained: resid and x_out go together");
+    return launch_decode_layer(x, resid, x_out, gate, bias, H, E, k, normalize, merge_mode, slots, I, next_gate,
+                               pred_out, logits, ids, weights, probs, h_ws, out, workspace, stream);
 }

@@ -295,8 +295,13 @@ def decode_layer_supported(H, I, E, k, device) -> bool:
 
 
 def decode_layer(x, gate, slots, I, top_k, normalize, *, bias=None, out, logits, ids, weights, h_ws, probs=None,
-                 merge="fused"):
-    """K4f: route + top-k + SwiGLU GEMV + down/merge of one token in one launch."""
+                 merge="fused", resid=None, x_out=None, next_gate=None, pred_out=None):
+    """K4f: route + top-k + SwiGLU GEMV + down/merge of one token in one launch.
+
+    Chain arguments (pdscope_decode_layer_chained): the input is
+    bf16(x + resid) when `resid` is given (written to `x_out`); with
+    `next_gate`, `pred_out` receives the next layer's gate-fallback
+    prediction top-k(next_gate . input)."""
     _need(x, "inputs", BF16)
     dev = x.device
     _need(gate, "gate", BF16, 2, dev)
@@ -313,8 +318,32 @@ def decode_layer(x, gate, slots, I, top_k, normalize, *, bias=None, out, logits,
         _need(bias, "bias", torch.float32, 1, dev)
     if probs is not None:
         _need(probs, "probs", torch.float32, None, dev)
-    _lib.call("pdscope_decode_layer", _p(x), _p(gate), _p(bias), H, E, top_k, int(bool(normalize)),
-              merge_mode(merge), _p(slots), I,
+    chained = any(t is not None for t in (resid, x_out, next_gate, pred_out))
+    if not chained:
+        _lib.call("pdscope_decode_layer", _p(x), _p(gate), _p(bias), H, E, top_k, int(bool(normalize)),
+                  merge_mode(merge), _p(slots), I,
+                  _p(logits), _p(ids), _p(weights), _p(probs), _p(h_ws), _p(out), _p(decode_workspace(dev, H)),
+                  _stream(dev))
+        return out
+    if (resid is None) != (x_out is None):
+        raise ValueError("decode_layer: resid and x_out go together")
+    if (next_gate is None) != (pred_out is None):
+        raise ValueError("decode_layer: next_gate and pred_out go together")
+    for t, n in ((resid, "resid"), (x_out, "x_out")):
+        if t is not None:
+            _need(t, n, BF16, None, dev)
+            if t.numel() != H:
+                raise ValueError(f"decode_layer: {n} must hold H values")
+    if pred_out is not None:
+        _need(pred_out, "pred_out", torch.int32, None, dev)
+        if pred_out.numel() != top_k:
+            raise ValueError("decode_layer: pred_out must hold k ids")
+    if next_gate is not None:
+        _need(next_gate, "next_gate", BF16, 2, dev)
+        if tuple(next_gate.shape) != (E, H):
+            raise ValueError("decode_layer: next_gate must be [E, H] like gate")
+    _lib.call("pdscope_decode_layer_chained", _p(x), _p(resid), _p(x_out), _p(gate), _p(bias), H, E, top_k,
+              int(bool(normalize)), merge_mode(merge), _p(slots), I, _p(next_gate), _p(pred_out),
               _p(logits), _p(ids), _p(weights), _p(probs), _p(h_ws), _p(out), _p(decode_workspace(dev, H)),
               _stream(dev))
     return out

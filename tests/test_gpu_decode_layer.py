@@ -236,3 +236,147 @@ def test_unsupported_shape_falls_back(pd):
     torch.cuda.synchronize()
     assert torch.equal(ids, a[1])
     assert torch.equal(out.view(torch.int16), a[3].view(torch.int16))
+
+
+def _chained(ops, x, gate, slots, I, k, normalize, *, resid, next_gate, bias=None, merge="fused"):
+    E, H = gate.shape
+    r = dict(logits=torch.empty((1, E), dtype=torch.bfloat16, device=DEV),
+             ids=torch.empty((1, k), dtype=torch.int32, device=DEV),
+             weights=torch.empty((1, k), dtype=torch.bfloat16, device=DEV),
+             h_ws=torch.empty(k * I, dtype=torch.bfloat16, device=DEV),
+             out=torch.empty((1, H), dtype=torch.bfloat16, device=DEV),
+             probs=torch.empty((1, E), dtype=torch.float32, device=DEV))
+    extra = {}
+    if resid is not None:
+        extra.update(resid=resid, x_out=torch.empty((1, H), dtype=torch.bfloat16, device=DEV))
+    if next_gate is not None:
+        extra.update(next_gate=next_gate, pred_out=torch.full((k,), -7, dtype=torch.int32, device=DEV))
+    ops.decode_layer(x, gate, slots, I, k, normalize, bias=bias, merge=merge, **r, **extra)
+    r.update(extra)
+    return r
+
+
+def _route_ids(ops, x, gate, k, normalize):
+    E = gate.shape[0]
+    ids = torch.empty((1, k), dtype=torch.int32, device=DEV)
+    ops.route_topk(x, gate, k, normalize, out=(torch.empty((1, E), dtype=torch.bfloat16, device=DEV), ids,
+                                                torch.empty((1, k), dtype=torch.bfloat16, device=DEV)))
+    return ids
+
+
+CHAIN_SHAPES = [dict(H=2048, I=768, E=128, k=8, normalize=True),
+                dict(H=1024, I=512, E=64, k=4, normalize=True),
+                dict(H=2048, I=512, E=256, k=8, normalize=True)]
+
+
+@pytest.mark.parametrize("merge", ["fused", "reference"])
+@pytest.mark.parametrize("shape", CHAIN_SHAPES, ids=lambda s: f"H{s['H']}_E{s['E']}_k{s['k']}")
+def test_chained_equals_plain_launch_on_the_residual_sum(pd, shape, merge):
+    """pdscope_decode_layer_chained: every output is bitwise that of
+    pdscope_decode_layer on x_eff = bf16(x + resid); x_out holds x_eff, and
+    pred_out the ids pdscope_route_topk gives for the next gate on x_eff (no
+    bias).  With only one of the two extras given the rest is unchanged."""
+    ops, layer, synthetic = pd
+    H, I, E, k, nrm = shape["H"], shape["I"], shape["E"], shape["k"], shape["normalize"]
+    lay = synthetic.make_layer(H, I, E, k, nrm, seed=1200 + E, device=DEV)
+    nxt = synthetic.make_layer(H, 8, E, k, nrm, seed=1300 + E, device=DEV).gate
+    slots = ops.slot_table([lay.experts[e] for e in range(E)], DEV)
+    for seed in (1, 2, 3):
+        x = synthetic.make_tokens(1, H, seed=seed * 7 + E, device=DEV)
+        resid = synthetic.make_tokens(1, H, seed=seed * 7 + E + 500, device=DEV)
+        x_eff = x + resid                                   # fp32 sum, one bf16 rounding
+        base = _fused(ops, x_eff, lay.gate, slots, I, k, nrm, merge=merge)
+        h_base = torch.empty(k * I, dtype=torch.bfloat16, device=DEV)
+        ops.decode_layer(x_eff, lay.gate, slots, I, k, nrm, out=torch.empty_like(base[3]),
+                         logits=torch.empty_like(base[0]), ids=torch.empty_like(base[1]),
+                         weights=torch.empty_like(base[2]), h_ws=h_base, merge=merge)
+        nids = _route_ids(ops, x_eff, nxt, k, nrm)
+        torch.cuda.synchronize()
+        for kind, rs, ng in (("both", resid, nxt), ("resid", resid, None), ("predictor", None, nxt)):
+            xin = x if rs is not None else x_eff
+            c = _chained(ops, xin, lay.gate, slots, I, k, nrm, resid=rs, next_gate=ng, merge=merge)
+            torch.cuda.synchronize()
+            checks = [("logits", base[0]), ("ids", base[1]), ("weights", base[2]), ("out", base[3]),
+                      ("probs", base[4]), ("h_ws", h_base)]
+            if rs is not None:
+                checks.append(("x_out", x_eff))
+            for name, want in checks:
+                got = c[name]
+                eq = torch.equal(got.view(torch.int16), want.view(torch.int16)) if got.dtype == torch.bfloat16 \
+                    else torch.equal(got.view(torch.int32), want.view(torch.int32))
+                assert eq, (kind, name, seed)
+            if ng is not None:
+                assert torch.equal(c["pred_out"], nids[0]), (kind, seed)
+    _assert_sync_clean(ops, H)
+
+
+def test_chain_of_layers_equals_layer_by_layer(pd):
+    """Four layers chained the way a decode step runs them: each launch takes
+    the previous output and residual and predicts the next layer's experts.
+    Equal to plain launches on the explicit residual sums; pred_out of each
+    layer is the next gate's routing of that layer's input.  Launches
+    without a next gate in between keep the predictor words current (the
+    next predicting launch still waits for this launch's words)."""
+    ops, layer, synthetic = pd
+    H, I, E, k = 2048, 768, 128, 8
+    layers = [synthetic.make_layer(**dict(synthetic.QWEN, seed=90 + l), device=DEV) for l in range(4)]
+    slots = [ops.slot_table([ly.experts[e] for e in range(E)], DEV) for ly in layers]
+    x0 = synthetic.make_tokens(1, H, seed=41, device=DEV)
+    r0 = synthetic.make_tokens(1, H, seed=42, device=DEV)
+    x, resid = x0, r0
+    outs = []
+    for l, ly in enumerate(layers):
+        nxt = layers[l + 1].gate if l + 1 < len(layers) else None
+        c = _chained(ops, x, ly.gate, slots[l], I, k, True, resid=resid, next_gate=nxt, merge="reference")
+        outs.append(c)
+        x, resid = c["out"], c["x_out"]
+    torch.cuda.synchronize()
+    x, resid = x0, r0
+    for l, ly in enumerate(layers):
+        x_eff = x + resid
+        b = _fused(ops, x_eff, ly.gate, slots[l], I, k, True, merge="reference")
+        torch.cuda.synchronize()
+        assert torch.equal(outs[l]["x_out"].view(torch.int16), x_eff.view(torch.int16)), l
+        assert torch.equal(outs[l]["ids"], b[1]), l
+        assert torch.equal(outs[l]["out"].view(torch.int16), b[3].view(torch.int16)), l
+        if l + 1 < len(layers):
+            nids = _route_ids(ops, x_eff, layers[l + 1].gate, k, True)
+            torch.cuda.synchronize()
+            assert torch.equal(outs[l]["pred_out"], nids[0]), l
+        x, resid = b[3], x_eff
+    _assert_sync_clean(ops, H)
+
+
+def test_chained_argument_checks(pd):
+    ops, layer, synthetic = pd
+    H, I, E, k = 2048, 768, 128, 8
+    lay = synthetic.make_layer(**synthetic.QWEN, seed=82, device=DEV)
+    slots = ops.slot_table([lay.experts[e] for e in range(E)], DEV)
+    x = synthetic.make_tokens(1, H, seed=1, device=DEV)
+    args = dict(out=torch.empty((1, H), dtype=torch.bfloat16, device=DEV),
+                logits=torch.empty((1, E), dtype=torch.bfloat16, device=DEV),
+                ids=torch.empty((1, k), dtype=torch.int32, device=DEV),
+                weights=torch.empty((1, k), dtype=torch.bfloat16, device=DEV),
+                h_ws=torch.empty(k * I, dtype=torch.bfloat16, device=DEV))
+    with pytest.raises(ValueError):          # resid without x_out
+        ops.decode_layer(x, lay.gate, slots, I, k, True, resid=x, **args)
+    with pytest.raises(ValueError):          # pred_out without next_gate
+        ops.decode_layer(x, lay.gate, slots, I, k, True, pred_out=args["ids"][0], **args)
+    with pytest.raises(ValueError):          # next gate of another shape
+        ops.decode_layer(x, lay.gate, slots, I, k, True, next_gate=lay.gate[:64].contiguous(),
+                         pred_out=args["ids"][0].clone(), **args)
+    with pytest.raises(ValueError):          # pred_out of the wrong length
+        ops.decode_layer(x, lay.gate, slots, I, k, True, next_gate=lay.gate,
+                         pred_out=args["ids"][0, :3].contiguous(), **args)
+    # the predictor needs E <= H/2: 256 experts over H = 256 (64 blocks) is refused by the library
+    small = synthetic.make_layer(256, 64, 256, 2, True, seed=3, device=DEV)
+    sl = ops.slot_table([small.experts[e] for e in range(256)], DEV)
+    xs = synthetic.make_tokens(1, 256, seed=2, device=DEV)
+    with pytest.raises(ValueError):
+        ops.decode_layer(xs, small.gate, sl, 64, 2, True, next_gate=small.gate,
+                         pred_out=torch.empty(2, dtype=torch.int32, device=DEV),
+                         out=torch.empty((1, 256), dtype=torch.bfloat16, device=DEV),
+                         logits=torch.empty((1, 256), dtype=torch.bfloat16, device=DEV),
+                         ids=torch.empty((1, 2), dtype=torch.int32, device=DEV),
+                         weights=torch.empty((1, 2), dtype=torch.bfloat16, device=DEV),
+                         h_ws=torch.empty(128, dtype=torch.bfloat16, device=DEV))
