@@ -167,7 +167,7 @@ def grouped_ffn(x, packed, sel, bm, max_tiles, slots, ws: MoEWorkspace, *, max_t
 
 
 def moe_forward(x, gate, slots, ws: MoEWorkspace, *, normalize=True, bias=None, block_m=None, fused_decode=True,
-                shared_slot=None, merge="fused"):
+                shared_slot=None, merge="fused", next_gate=None, pred_out=None):
     """Full layer: returns (out [T,H] bf16, logits, ids int32 [T,k], weights bf16 [T,k]).
 
     merge: 'fused' (each token's k weighted rows summed in fp32, one
@@ -178,6 +178,9 @@ def moe_forward(x, gate, slots, ws: MoEWorkspace, *, normalize=True, bias=None, 
     device allow it (fused_decode), else route (K1) + decode GEMV (K4).
     shared_slot (int64 [1] device table) adds always-on shared experts
     (DeepSeek-V2); the workspace must have been built with shared_I.
+    next_gate / pred_out (T == 1 on the single-launch kernel only, see
+    ops.decode_predictor_fits): the next layer's gate-fallback prediction,
+    top-k of next_gate . x, is written to pred_out [k] int32 by the same launch.
     """
     T = x.shape[0]
     if shared_slot is not None:
@@ -187,12 +190,18 @@ def moe_forward(x, gate, slots, ws: MoEWorkspace, *, normalize=True, bias=None, 
         y_shared = shared_forward(x, shared_slot, ws)
         out = experts_resident(x, ids, weights, slots, ws, block_m=block_m, add_in=y_shared, merge=merge)
         return out, logits, ids, weights
-    if (T == 1 and fused_decode and ws.k <= 8
-            and ops.decode_layer_supported(ws.H, ws.I, ws.E, ws.k, x.device)):
+    fused = (T == 1 and fused_decode and ws.k <= 8 and shared_slot is None
+             and ops.decode_layer_supported(ws.H, ws.I, ws.E, ws.k, x.device))
+    if (next_gate is None) != (pred_out is None):
+        raise ValueError("next_gate and pred_out go together")
+    if next_gate is not None and not (fused and ops.decode_predictor_fits(ws.H, ws.E)):
+        raise ValueError("the fused next-layer prediction needs one token on the single-launch decode kernel "
+                         "with E <= H/2")
+    if fused:
         logits, ids, weights, _ = ws.views(1)
         out = ws.out[:1]
         ops.decode_layer(x, gate, slots, ws.I, ws.k, normalize, bias=bias, out=out, logits=logits, ids=ids,
-                         weights=weights, h_ws=ws.h_ws, merge=merge)
+                         weights=weights, h_ws=ws.h_ws, merge=merge, next_gate=next_gate, pred_out=pred_out)
         return out, logits, ids, weights
     logits, ids, weights = route(x, gate, ws, normalize=normalize, bias=bias)
     out = experts_resident(x, ids, weights, slots, ws, block_m=block_m, merge=merge)

@@ -294,6 +294,12 @@ def decode_layer_supported(H, I, E, k, device) -> bool:
     return ok
 
 
+def decode_predictor_fits(H, E) -> bool:
+    """Whether the single-launch decode kernel can also compute the next
+    layer's prediction (its router and predictor blocks both fit the grid)."""
+    return 2 * ((E + 3) // 4) <= (H + 3) // 4
+
+
 def decode_layer(x, gate, slots, I, top_k, normalize, *, bias=None, out, logits, ids, weights, h_ws, probs=None,
                  merge="fused", resid=None, x_out=None, next_gate=None, pred_out=None):
     """K4f: route + top-k + SwiGLU GEMV + down/merge of one token in one launch.

@@ -245,20 +245,25 @@ class PDScopeCudaRuntime:
 
         # ---- 1-2: route (+ predictor), grouping, one D2H of the demand
         out = torch.empty((T, H), dtype=torch.bfloat16, device=self.device)
+        predict = prefetch and next_gate is not None
+        # the graph's launch also predicts the next layer where its grid allows
+        graph_pred = next_gate if (graph_path and predict and ops.decode_predictor_fits(H, E)) else None
+        pred_ids = None
         if graph_path:
             # entries the first replay saw (a copy still in flight reads as null)
             replay_table = list(self.executor.table(layer, E)[1])
-            logits, ids, weights, gout = self._replay_decode_graph(layer, x, gate, normalize, k, out, ring=ring)
+            logits, ids, weights, gout, pred_ids = self._replay_decode_graph(layer, x, gate, normalize, k, out,
+                                                                             ring=ring, next_gate=graph_pred)
             if self.graph_output_pool:
                 out = gout
         else:
             logits, ids, weights = L.route(x, gate, ws, normalize=normalize, bias=bias)
-        predict = prefetch and next_gate is not None
         nws = None
-        if predict:
+        pred_sel = pred_ids.view(1, k) if pred_ids is not None else None
+        if predict and pred_ids is None:
             nws = self._pred_workspace(T, k)
-            _, nids, _ = L.route(x, next_gate, nws, normalize=normalize)
-            ops.route_hist(nids, E, out=nws.hist)
+            _, pred_sel, _ = L.route(x, next_gate, nws, normalize=normalize)
+            ops.route_hist(pred_sel, E, out=nws.hist)
         _, _, _, packed = ws.views(T)
         if T > 1:
             ops.pack(ids, E, out=packed, workspace=ws.pack_ws)
@@ -268,7 +273,9 @@ class PDScopeCudaRuntime:
         host = self._pinned_counts
         n0 = counts_dev.numel()
         host[:n0].copy_(counts_dev, non_blocking=True)
-        if predict:
+        if pred_ids is not None:
+            host[n0:n0 + k].copy_(pred_ids, non_blocking=True)
+        elif predict:
             host[n0:n0 + E].copy_(nws.hist, non_blocking=True)
         err_at = 2 * E + 8
         if graph_path:
@@ -285,7 +292,12 @@ class PDScopeCudaRuntime:
             if len(set(sel)) != k:
                 raise AssertionError("decode routing selected duplicate experts")
             counts = {e: 1 for e in sel}
-        next_counts = ({e: int(c) for e, c in enumerate(host[n0:n0 + E].tolist()) if c} if predict else {})
+        if pred_ids is not None:   # one token: each predicted expert once
+            next_counts = {int(e): 1 for e in host[n0:n0 + k].tolist()}
+            if len(next_counts) != k:
+                raise AssertionError("decode prediction selected duplicate experts")
+        else:
+            next_counts = ({e: int(c) for e, c in enumerate(host[n0:n0 + E].tolist()) if c} if predict else {})
         if sum(counts.values()) != T * k:
             raise AssertionError("lost or duplicated routed assignment")
 
@@ -399,7 +411,8 @@ class PDScopeCudaRuntime:
                     late_replays += 1
 
                     def launch():
-                        self._replay_decode_graph(layer, x, gate, normalize, k, out, ring=ring)
+                        self._replay_decode_graph(layer, x, gate, normalize, k, out, ring=ring,
+                                                  next_gate=graph_pred)
                 else:
                     def launch():  # the replay already produced `out`; account the uses it made
                         pass
@@ -431,7 +444,8 @@ class PDScopeCudaRuntime:
                     late_replays += 1
 
                     def launch():
-                        self._replay_decode_graph(layer, x, gate, normalize, k, out, ring=ring)
+                        self._replay_decode_graph(layer, x, gate, normalize, k, out, ring=ring,
+                                                  next_gate=graph_pred)
                     comp = ex.gpu_group([key(e) for e in resident + batch], launch, input_ref=x, wait_for=cur)
                 else:
                     tab = ex.upload_table(layer, E, ex.compute_stream)
@@ -479,7 +493,7 @@ class PDScopeCudaRuntime:
         for task in tasks:
             ex.finish_gpu(task, wait=True)
         if graph_path and self.graph_output_pool:
-            out = self._graphs[(layer, k, normalize, gate.data_ptr(), ring)][2]
+            out = self._graphs[self._graph_key(layer, k, normalize, gate, ring, graph_pred)][2]
         cpu_rows = dict((e, ex.finish_cpu(p, wait=True)) for e, p in cpu_tasks.items())
         if cpu_group is not None:
             cpu_rows.update(ex.finish_cpu_group(cpu_group.values()))
@@ -558,7 +572,7 @@ class PDScopeCudaRuntime:
                    predictor="next_layer_gate_on_current_activation",
                    scheduler="cross_layer" if planned else "gpu_all", predictor_prior_hit_rate=0.0,
                    selected_sha256=digest(routing.selected) if self.diagnostics else None,
-                   next_selected_sha256=digest(nids.long()) if self.diagnostics and predict else None,
+                   next_selected_sha256=digest(pred_sel.long()) if self.diagnostics and predict else None,
                    ready_at_reveal=sum(o.ready_hit for o in observations),
                    loading_at_reveal=sum(o.state_at_reveal == "loading" for o in observations),
                    counters=delta, ping_pong_slots=ping_pong,
@@ -671,14 +685,20 @@ class PDScopeCudaRuntime:
 
     # ------------------------------------------------------------ resident decode graph
 
-    def _replay_decode_graph(self, layer, x, gate, normalize, k, out, *, ring=0, cache=True):
+    @staticmethod
+    def _graph_key(layer, k, normalize, gate, ring, next_gate):
+        return (layer, k, normalize, gate.data_ptr(), ring, next_gate.data_ptr() if next_gate is not None else 0)
+
+    def _replay_decode_graph(self, layer, x, gate, normalize, k, out, *, ring=0, cache=True, next_gate=None):
         """Replay the captured single-launch decode layer of `layer` over its
         current slot table (capturing it on first use, checked bit for bit
         against the eager launch).  With graph_output_pool the graph of ring
         entry `ring` (two per layer) writes its own output buffer, which is
-        returned as is; otherwise the output is copied into `out`.
-        Returns (logits, ids, weights, output) views of the graph's buffers."""
-        gkey = (layer, k, normalize, gate.data_ptr(), ring) if cache else ("calibration", layer, k)
+        returned as is; otherwise the output is copied into `out`.  With
+        next_gate the same launch predicts the next layer's experts.
+        Returns (logits, ids, weights, output, predicted ids or None) views of
+        the graph's buffers."""
+        gkey = self._graph_key(layer, k, normalize, gate, ring, next_gate) if cache else ("calibration", layer, k)
         g = self._graphs.get(gkey)
         ex = self.executor
         ex.table(layer, self.E)
@@ -687,6 +707,7 @@ class PDScopeCudaRuntime:
         slots_dev = ex.upload_table(layer, self.E, torch.cuda.current_stream(self.device))
         if g is None:
             gws = L.MoEWorkspace(1, self.H, self.I, self.E, k, self.device)
+            pred = torch.full((k,), -1, dtype=torch.int32, device=self.device) if next_gate is not None else None
             xin = torch.empty_like(x)
             gout = gws.out[:1]
             xin.copy_(x)
@@ -694,28 +715,30 @@ class PDScopeCudaRuntime:
             side = torch.cuda.Stream(self.device)
             side.wait_stream(torch.cuda.current_stream(self.device))
             # whole layer (fused single-launch decode where the device allows)
+            fwd = dict(normalize=normalize, merge=self.merge, next_gate=next_gate, pred_out=pred)
             with torch.cuda.stream(side):
-                L.moe_forward(xin, gate, slots_dev, gws, normalize=normalize, merge=self.merge)
+                L.moe_forward(xin, gate, slots_dev, gws, **fwd)
             torch.cuda.current_stream(self.device).wait_stream(side)
-            eager = [t.clone() for t in (gout, gws.logits[:1], gws.ids[:1], gws.weights[:1])]
+            watched = lambda: [t for t in (gout, gws.logits[:1], gws.ids[:1], gws.weights[:1], pred)  # noqa: E731
+                               if t is not None]
+            eager = [t.clone() for t in watched()]
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
-                L.moe_forward(xin, gate, slots_dev, gws, normalize=normalize, merge=self.merge)
+                L.moe_forward(xin, gate, slots_dev, gws, **fwd)
             # a captured graph must reproduce the eager launch bit for bit
             # before it serves (the reference checks the same at capture,
             # expertbench/executor.py:95-96)
             graph.replay()
-            replayed = (gout, gws.logits[:1], gws.ids[:1], gws.weights[:1])
-            if not all(torch.equal(a, b) for a, b in zip(eager, replayed)):
+            if not all(torch.equal(a, b) for a, b in zip(eager, watched())):
                 raise AssertionError(f"captured decode graph of layer {layer} differs from its eager launch")
-            g = (graph, xin, gout, gws, slots_dev)
+            g = (graph, xin, gout, gws, slots_dev, pred)
             self._graphs[gkey] = g
-        graph, xin, gout, gws, _ = g
+        graph, xin, gout, gws, _, pred = g
         xin.copy_(x)
         graph.replay()
         if not self.graph_output_pool:
             out.copy_(gout)
-        return gws.logits[:1], gws.ids[:1], gws.weights[:1], gout
+        return gws.logits[:1], gws.ids[:1], gws.weights[:1], gout, pred
 
     def close(self):
         self._graphs.clear()

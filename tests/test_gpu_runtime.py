@@ -388,6 +388,14 @@ def test_runtime_partial_resident_decode_graph(orc):
                 assert torch.equal(routing.selected, ids.long())
                 assert torch.equal(out, ref_out)
                 check_output(orc, out, routing, x, layers[l], q["H"], q["I"], 8)
+                if l == 0:
+                    # the prediction the graph's launch made equals the router on the next gate
+                    nids = torch.empty((1, 8), dtype=torch.int32, device=DEV)
+                    ops.route_topk(x, layers[1].gate, 8, True,
+                                   out=(torch.empty((1, q["E"]), dtype=torch.bfloat16, device=DEV), nids,
+                                        torch.empty((1, 8), dtype=torch.bfloat16, device=DEV)))
+                    torch.cuda.synchronize()
+                    assert row["next_prediction_counts"] == {int(e): 1 for e in nids[0].tolist()}
         assert misses > 0
         closure(rt)
         assert rt.cache.stats().get("prefetch_loads_submitted", 0) > 0
