@@ -62,6 +62,16 @@ __device__ __forceinline__ void wait_vm() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// wait_vm<n> for a wave-uniform n in [0, 24] known only at run time
+__device__ __forceinline__ void wait_vm_rt(int n) {
+#define PD_W(K) else if (n == K) wait_vm<K>();
+    if (n <= 0) wait_vm<0>();
+    PD_W(1) PD_W(2) PD_W(3) PD_W(4) PD_W(5) PD_W(6) PD_W(7) PD_W(8) PD_W(9) PD_W(10) PD_W(11) PD_W(12)
+    PD_W(13) PD_W(14) PD_W(15) PD_W(16) PD_W(17) PD_W(18) PD_W(19) PD_W(20) PD_W(21) PD_W(22) PD_W(23)
+    else wait_vm<24>();
+#undef PD_W
+}
+
 // Workgroup barrier for the LDS ring.  __syncthreads() would also wait for
 // every outstanding direct-to-LDS load (its release fence covers them) and
 // drain the pipeline; here the caller waits for exactly the stage it needs
@@ -127,6 +137,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void grouped_kernel(
     constexpr int AL = BM / G::RPI / NWA, BL = BN / G::RPI / NWB;  // 1 KB loads per loading wave per stage
     static_assert(AL >= 1 && BL >= 1 && AL * G::RPI * NWA == BM && BL * G::RPI * NWB == BN, "tile / load shape");
     constexpr int LW = SPLIT ? (AL > BL ? AL : BL) : AL + BL;  // load pointers per wave
+    static_assert(!SPLIT || (SA - 1) * AL <= 24, "A-wave waits count live loads up to wait_vm_rt's range");
     constexpr int ASTAGE = BM * G::RB, BSTAGE = BN * G::RB;
     __shared__ __attribute__((aligned(1024))) uint8_t smem[SA * ASTAGE + SB * BSTAGE];
     uint8_t *const ring_a = smem;
@@ -170,6 +181,13 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void grouped_kernel(
     const bool a_role = !SPLIT || wave < NWA;
     const int wa = wave, wb = SPLIT ? wave - NWA : wave;
     const int rl = lane / G::CPR, slot = lane % G::CPR;
+    // A loads whose rows all lie past the expert's last row are not issued (split roles only: there an A wave's load count per stage
+    // is its own, and its waits count its live loads); their LDS rows keep
+    // stale values, which reach only accumulator rows the epilogue skips
+    const int live_groups = (min(row_end - m0, BM) + G::RPI - 1) / G::RPI;
+    const int a_live = SPLIT ? __builtin_amdgcn_readfirstlane(
+                                   min(AL, max(0, (live_groups - wa + NWA - 1) / NWA)))
+                             : AL;
     const uint16_t *lp[LW];
     auto a_ptr = [&](int q) {
         const int row = (wa + NWA * q) * G::RPI + rl;
@@ -203,7 +221,8 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void grouped_kernel(
     auto issue_a = [&](int kt, int q0) __attribute__((always_inline)) {  // A stage kt from lp[q0 ..]
         uint8_t *st = ring_a + (kt % SA) * ASTAGE;
 #pragma unroll
-        for (int q = 0; q < AL; ++q) load_lds16(lp[q0 + q] + kt * BK, st + (wa + NWA * q) * 1024);
+        for (int q = 0; q < AL; ++q)
+            if (q < a_live) load_lds16(lp[q0 + q] + kt * BK, st + (wa + NWA * q) * 1024);
     };
     auto issue_b = [&](int kt, int q0) __attribute__((always_inline)) {
         uint8_t *st = ring_b + (kt % SB) * BSTAGE;
@@ -243,14 +262,18 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void grouped_kernel(
     auto kloop = [&](auto live, auto role_c) __attribute__((always_inline)) {
         constexpr int L = decltype(live)::value;
         constexpr int ROLE = decltype(role_c)::value;
-        constexpr int KK = BK / 16;
+        // a stage of BK is consumed in SUB fragment steps of BKF = 32 (two
+        // MFMA K steps each), so the fragment registers do not grow with BK
+        constexpr int BKF = BK < 32 ? BK : 32;
+        constexpr int SUB = BK / BKF;
+        constexpr int KK = BKF / 16;
         bf16x8_t af[2][KK][MB], bfr[2][KK][NB];
-        auto read_frags = [&](int kt, int buf) __attribute__((always_inline)) {
+        auto read_frags = [&](int kt, int sub, int buf) __attribute__((always_inline)) {
             const uint8_t *sa = ring_a + (kt % SA) * ASTAGE;
             const uint8_t *sb = ring_b + (kt % SB) * BSTAGE;
 #pragma unroll
             for (int kk = 0; kk < KK; ++kk) {
-                const int c = kk * 2 + lhalf;
+                const int c = (sub * KK + kk) * 2 + lhalf;
 #pragma unroll
                 for (int i = 0; i < L; ++i)
                     af[buf][kk][i] = *reinterpret_cast<const bf16x8_t *>(sa + G::off(rblk(i) + lrow, c));
@@ -274,7 +297,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void grouped_kernel(
 #pragma unroll
             for (int s0 = 0; s0 < SA; ++s0)
                 if (s0 < KT) issue_a(s0, 0);
-            wait_stage<SA + 1, AL>(min(SA - 1, KT - 1));
+            wait_vm_rt(min(SA - 1, KT - 1) * a_live);
         } else if constexpr (ROLE == 2) {
 #pragma unroll
             for (int s0 = 0; s0 < SB; ++s0)
@@ -290,7 +313,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void grouped_kernel(
             wait_stage<SA + 1, AL + BL>(min(SA - 1, KT - 1));
         }
         ring_barrier();
-        if constexpr (L > 0) read_frags(0, 0);
+        if constexpr (L > 0) read_frags(0, 0, 0);
         // one pipeline step consuming stage kt from fragment buffer CUR:
         // wait for stage kt+1 of this wave's ring(s), synchronise the block
         // (every wave has then also finished reading stage kt, whose
@@ -301,12 +324,23 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void grouped_kernel(
         // path joins the loop header, and the compiler's wait analysis would
         // make this stage's MFMAs wait for the next stage's fragment reads.
         auto step = [&](int kt, auto cur_c, auto steady_c) __attribute__((always_inline)) {
-            constexpr int CUR = decltype(cur_c)::value;
+            constexpr int CUR0 = decltype(cur_c)::value;
             constexpr bool STEADY = decltype(steady_c)::value;
+            // the stage's sub-steps before its last: read the next sub-step's
+            // fragments, run this one's MFMAs (no wait: the stage has landed)
+#pragma unroll
+            for (int sub = 0; sub + 1 < SUB; ++sub) {
+                const int cb = CUR0 ^ (sub & 1);
+                if constexpr (L > 0) read_frags(kt, sub + 1, cb ^ 1);
+                __builtin_amdgcn_sched_barrier(0);
+                if constexpr (L > 0) mfmas(cb);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            constexpr int CUR = CUR0 ^ ((SUB - 1) & 1);
             if (STEADY || kt + 1 < KT) {
                 if constexpr (ROLE == 1) {
-                    if constexpr (STEADY) wait_stage<SA, AL>(SA - 2);
-                    else wait_stage<SA, AL>(min(SA - 2, KT - 2 - kt));
+                    if constexpr (STEADY) wait_vm_rt((SA - 2) * a_live);
+                    else wait_vm_rt(min(SA - 2, KT - 2 - kt) * a_live);
                 } else if constexpr (ROLE == 2) {
                     if constexpr (STEADY) wait_stage<SB, BL>(SB - 2);
                     else wait_stage<SB, BL>(min(SB - 2, KT - 2 - kt));
@@ -326,7 +360,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void grouped_kernel(
                         issue_b(kt + SA, AL);
                     }
                 }
-                if constexpr (L > 0) read_frags(kt + 1, CUR ^ 1);
+                if constexpr (L > 0) read_frags(kt + 1, 0, CUR ^ 1);
             }
             __builtin_amdgcn_sched_barrier(0);  // keep the next stage's reads ahead of these MFMAs
             if constexpr (L > 0) mfmas(CUR);
@@ -336,19 +370,20 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void grouped_kernel(
             __builtin_amdgcn_sched_barrier(0);
         };
         using C0 = std::integral_constant<int, 0>;
-        using C1 = std::integral_constant<int, 1>;
         using Steady = std::true_type;
         using Tail = std::false_type;
         // unrolled by two so the fragment buffers are indexed statically
         int kt = 0;
         constexpr int SMAX = SA > SB ? SA : SB;
+        // the buffer of a stage's first sub-step alternates with SUB odd
+        using CN = std::integral_constant<int, SUB & 1>;
         for (; kt + 1 + SMAX < KT; kt += 2) {
             step(kt, C0{}, Steady{});
-            step(kt + 1, C1{}, Steady{});
+            step(kt + 1, CN{}, Steady{});
         }
         for (; kt + 1 < KT; kt += 2) {
             step(kt, C0{}, Tail{});
-            step(kt + 1, C1{}, Tail{});
+            step(kt + 1, CN{}, Tail{});
         }
         if (kt < KT) step(kt, C0{}, Tail{});
     };
@@ -453,10 +488,10 @@ int grouped_entry(int phase, const void *x, const int32_t *perm_token, const int
         return launch_grouped<128, 256, 64, 2, 4, 3, 3>(phase, xp, perm_token, offsets, sel, nsel, tile_start, max_tiles,
                                                  sp, H, I, (uint16_t *)h_ws, (uint16_t *)y, s);
     case 256:
-        return launch_grouped<256, 256, 32, 2, 4, 3, 7>(phase, xp, perm_token, offsets, sel, nsel, tile_start, max_tiles,
+        return launch_grouped<256, 256, 32, 2, 4, 4, 6>(phase, xp, perm_token, offsets, sel, nsel, tile_start, max_tiles,
                                                  sp, H, I, (uint16_t *)h_ws, (uint16_t *)y, s);
     case 384:
-        return launch_grouped<384, 128, 32, 4, 2, 4, 8, true>(phase, xp, perm_token, offsets, sel, nsel, tile_start,
+        return launch_grouped<384, 128, 64, 4, 2, 2, 4, true>(phase, xp, perm_token, offsets, sel, nsel, tile_start,
                                                        max_tiles, sp, H, I, (uint16_t *)h_ws, (uint16_t *)y, s);
     default:
         return fail(kEInval, "grouped: block_m must be 32, 64, 128, 256 or 384");
