@@ -231,6 +231,8 @@ def run_prefill(T, steps, warmup, n_layers, device, seed0):
             ev[1].record(stream)
         ops.swiglu_grouped_down(ws.h_ws, packed.offsets, sel_d, ts_d, (n + bmd - 1) // bmd + E, bmd, slots, H, I,
                                 ws.y)
+        if ev is not None:
+            ev[2].record(stream)
         ops.merge(ws.y, packed.row_of, w, ws.out[:T])
 
     # experts touched per layer (for algorithmic bytes)
@@ -241,19 +243,52 @@ def run_prefill(T, steps, warmup, n_layers, device, seed0):
         touched.append(int((ws.counts > 0).sum().item()))
     for i in range(warmup):
         step(i)
-    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    events = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(3)) for _ in range(steps)]
     torch.cuda.synchronize(device)
     t0 = time.perf_counter()
     for i in range(steps):
         step(i, events[i])
     torch.cuda.synchronize(device)
     wall = time.perf_counter() - t0
-    gateup_ms = [a.elapsed_time(b) for a, b in events]
+    gateup_ms = [a.elapsed_time(b) for a, b, _ in events]
+    down_ms = [b.elapsed_time(c) for _, b, c in events]
     mean_touched = sum(touched[i % n_layers] for i in range(steps)) / steps
+    bmm = vendor_bmm_ms(n // E, device) if n % E == 0 and n // E >= 128 else None
     return dict(T=T, wall_s=wall, ms_per_step=wall / steps * 1e3, tok_s=T * steps / wall,
                 gateup_ms_mean=statistics.mean(gateup_ms), gateup_ms_median=statistics.median(gateup_ms),
+                down_ms_median=statistics.median(down_ms), vendor_bmm=bmm,
                 touched=mean_touched, block_m=ops.grouped_block_m(n // E), layers=n_layers,
                 first_layer=layers[0], first_x=xs[0], ws=ws)
+
+
+def vendor_bmm_ms(rows, device, reps=20):
+    """The layer's expert GEMMs as the BLAS library runs them at their mean
+    size: torch.bmm over E experts of `rows` rows each, gate|up
+    ([rows, H] x [H, 2I]) and down ([rows, I] x [I, H]), contiguous operands.
+    A library reference for the two grouped launches (which also gather the
+    routed rows, apply SwiGLU and cover ragged per-expert row counts)."""
+    import torch
+    a = torch.randn(E, rows, H, dtype=torch.bfloat16, device=device)
+    w1 = torch.randn(E, H, 2 * I, dtype=torch.bfloat16, device=device)
+    h = torch.randn(E, rows, I, dtype=torch.bfloat16, device=device)
+    w2 = torch.randn(E, I, H, dtype=torch.bfloat16, device=device)
+    out = {}
+    for name, fn in (("gateup", lambda: torch.bmm(a, w1)), ("down", lambda: torch.bmm(h, w2))):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize(device)
+        ms = []
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize(device)
+            ms.append(e0.elapsed_time(e1))
+        out[f"{name}_ms"] = statistics.median(ms)
+    del a, w1, h, w2
+    out["what"] = f"torch.bmm over {E} experts x {rows} rows (BLAS), gate|up then down"
+    return out
 
 
 def run_decode(steps, warmup, n_layers, device, seed0):
@@ -316,13 +351,97 @@ def run_decode(steps, warmup, n_layers, device, seed0):
         raise AssertionError("a bounded wait of the fused decode kernel gave up")
     g3 = capture(False)
     _, _, layer_ms3 = timed(g3, steps, warmup)
+    chain = run_decode_chain(layers, device, seed0, reps=max(20, steps // n_layers // 4)) if fused else None
+    read_ms = plain_read_ms(K_TOP * EXPERT_BYTES + ROUTER_BYTES, n_layers, device)
     kernel = ("decode_layer_kernel (route + top-k + gate/up + down/merge in one launch), "
               f"{n_layers} layers per hipGraph" if fused else
               f"route_gemv + decode_gateup + decode_down, {n_layers} layers per hipGraph")
     return dict(T=1, wall_s=wall, ms_per_step=wall / n_steps * 1e3, tok_s=n_steps / wall, kernel=kernel,
                 layer_ms_mean=statistics.mean(layer_ms), layer_ms_median=statistics.median(layer_ms),
-                three_launch_layer_ms=statistics.median(layer_ms3), steps_run=n_steps,
-                layers=n_layers, first_layer=layers[0], first_x=xs[0], ws=wss[0])
+                three_launch_layer_ms=statistics.median(layer_ms3), steps_run=n_steps, chain=chain,
+                plain_read_layer_ms=read_ms, layers=n_layers, first_layer=layers[0], first_x=xs[0], ws=wss[0])
+
+
+def run_decode_chain(layers, device, seed0, reps):
+    """The same layers chained as a decode step runs them, in one hipGraph:
+    layer l takes the previous output plus the residual stream
+    (x_eff = bf16(x + resid)) and predicts layer l+1's experts from its own
+    input (the gate-fallback predictor, fused into the launch).  Returns the
+    per-layer time and how many predicted experts layer l+1 then selected."""
+    import torch
+    from pdscope_amd import ops, synthetic
+    n = len(layers)
+    x0 = synthetic.make_tokens(1, H, seed=seed0 + 11, device=device)
+    r0 = synthetic.make_tokens(1, H, seed=seed0 + 12, device=device)
+    bufs = [dict(out=torch.empty((1, H), dtype=torch.bfloat16, device=device),
+                 x_out=torch.empty((1, H), dtype=torch.bfloat16, device=device),
+                 logits=torch.empty((1, E), dtype=torch.bfloat16, device=device),
+                 ids=torch.empty((1, K_TOP), dtype=torch.int32, device=device),
+                 weights=torch.empty((1, K_TOP), dtype=torch.bfloat16, device=device),
+                 h_ws=torch.empty(K_TOP * I, dtype=torch.bfloat16, device=device),
+                 pred=torch.full((K_TOP,), -1, dtype=torch.int32, device=device)) for _ in range(n)]
+
+    def step():
+        x, r = x0, r0
+        for l, (lay, slots) in enumerate(layers):
+            b = bufs[l]
+            extra = dict(next_gate=layers[l + 1][0].gate, pred_out=b["pred"]) if l + 1 < n else {}
+            ops.decode_layer(x, lay.gate, slots, I, K_TOP, True, out=b["out"], logits=b["logits"], ids=b["ids"],
+                             weights=b["weights"], h_ws=b["h_ws"], resid=r, x_out=b["x_out"], **extra)
+            x, r = b["out"], b["x_out"]
+
+    stream = torch.cuda.current_stream(device)
+    side = torch.cuda.Stream(device)
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        step()
+    stream.wait_stream(side)
+    torch.cuda.synchronize(device)
+    eager = [b["out"].clone() for b in bufs]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    g.replay()
+    torch.cuda.synchronize(device)
+    if not all(torch.equal(b["out"], e) for b, e in zip(bufs, eager)):
+        raise AssertionError("chained decode graph replay differs from eager execution")
+    hits = sum(len(set(bufs[l]["pred"].tolist()) & set(bufs[l + 1]["ids"][0].tolist())) for l in range(n - 1))
+    for _ in range(5):
+        g.replay()
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+    torch.cuda.synchronize(device)
+    events[0].record(stream)
+    for k in range(reps):
+        g.replay()
+        events[k + 1].record(stream)
+    torch.cuda.synchronize(device)
+    layer_ms = [events[k].elapsed_time(events[k + 1]) / n for k in range(reps)]
+    return dict(layer_ms_median=statistics.median(layer_ms), predictor_hits=hits, predictor_total=K_TOP * (n - 1),
+                what="residual sum + next-layer gate-fallback prediction fused into each layer's launch")
+
+
+def plain_read_ms(nbytes, n_regions, device, reps=30):
+    """Time of a vendor GEMV reading `nbytes` once: torch.mv of a [nbytes / 4096, 2048]
+    bf16 matrix (the BLAS library's matrix-vector kernel), over distinct
+    matrices, one per layer copy, so that the 256 MB Infinity Cache holds
+    none of them: a library reference for one launch streaming that many bytes."""
+    import torch
+    rows = nbytes // (2 * H)
+    mats = torch.empty((n_regions, rows, H), dtype=torch.bfloat16, device=device).normal_()
+    v = torch.ones(H, dtype=torch.bfloat16, device=device)
+    for r in range(3):
+        torch.mv(mats[r], v)
+    torch.cuda.synchronize(device)
+    ms = []
+    for k in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        torch.mv(mats[k % n_regions], v)
+        e1.record()
+        torch.cuda.synchronize(device)
+        ms.append(e0.elapsed_time(e1))
+    del mats
+    return statistics.median(ms[3:])
 
 
 def run_zipf_staged(steps, warmup, n_layers, device, seed0):
@@ -736,6 +855,7 @@ def prefill_record(res):
     layer_s = res["ms_per_step"] / 1e3
     return dict(tok_s=res["tok_s"], ms_per_step=res["ms_per_step"], kernel="grouped_kernel<gateup>",
                 kernel_ms_mean=res["gateup_ms_mean"], kernel_ms_median=res["gateup_ms_median"],
+                down_ms_median=res["down_ms_median"], vendor_bmm=res["vendor_bmm"],
                 kernel_bytes=gateup_bytes, kernel_flops=gateup_flops, experts_touched=touched,
                 block_m=res["block_m"], layers_rotated=res["layers"], hbm=hbm, mfma=mfma,
                 layer_hbm_gbs=layer_bytes / layer_s / 1e9, layer_mfma_tflops=layer_flops / layer_s / 1e12)
@@ -746,11 +866,16 @@ def decode_record(res):
     t = res["layer_ms_mean"] / 1e3
     hbm = dict(bound="hbm", achieved=layer_bytes / t / 1e9, peak=HBM_PEAK_GBS, unit="GB/s")
     hbm["frac"] = hbm["achieved"] / hbm["peak"]
+    read_ms = res["plain_read_layer_ms"]
     return dict(tok_s=res["tok_s"], ms_per_step=res["ms_per_step"], kernel=res["kernel"],
                 kernel_ms_mean=res["layer_ms_mean"], kernel_ms_median=res["layer_ms_median"],
                 three_launch_layer_ms=res["three_launch_layer_ms"],
                 kernel_bytes=layer_bytes, layers_rotated=res["layers"], hbm=hbm,
-                layer_hbm_gbs=layer_bytes / (res["ms_per_step"] / 1e3) / 1e9)
+                layer_hbm_gbs=layer_bytes / (res["ms_per_step"] / 1e3) / 1e9,
+                vendor_gemv=dict(ms=read_ms, gbs=layer_bytes / (read_ms / 1e3) / 1e9,
+                                 layer_over_gemv=res["layer_ms_mean"] / read_ms,
+                                 what="torch.mv (BLAS GEMV) reading the layer's byte count once, one launch"),
+                chained_step=res["chain"])
 
 
 def main():
