@@ -79,3 +79,23 @@ def test_resident_graph_costs_closed_form(tmp_path):
     for bad in (("eager_bound", 0.0), ("other", 0.1)):
         with pytest.raises(ValueError):
             ResidentGraphCosts(base, bad[1], bad[0])
+
+
+def test_decode_error_word_raises_and_is_cleared():
+    """The runtime's check of the fused decode kernel's sticky error word, on
+    the CPU: a zero word passes, a set word raises for that call and is
+    cleared, so the next call reports only its own."""
+    from pdscope_amd.pdscope_runtime import PDScopeCudaRuntime
+    word = torch.zeros(1, dtype=torch.int32)
+
+    class Holder:
+        def _decode_error_word(self):
+            return word
+
+    h = Holder()
+    PDScopeCudaRuntime._raise_if_decode_gave_up(h, 0)
+    word[0] = 1
+    with pytest.raises(RuntimeError, match="bounded internal wait gave up"):
+        PDScopeCudaRuntime._raise_if_decode_gave_up(h, int(word[0]))
+    assert int(word[0]) == 0
+    PDScopeCudaRuntime._raise_if_decode_gave_up(h, int(word[0]))
