@@ -380,3 +380,61 @@ def test_chained_argument_checks(pd):
                          ids=torch.empty((1, 2), dtype=torch.int32, device=DEV),
                          weights=torch.empty((1, 2), dtype=torch.bfloat16, device=DEV),
                          h_ws=torch.empty(128, dtype=torch.bfloat16, device=DEV))
+
+
+def test_chained_graph_replay(pd):
+    """A four-layer chained step captured once and replayed with new inputs:
+    every replay equals the eager chain (outputs, residuals, predictions), with
+    eager work and synchronisations between the replays, and the workspace
+    stays clean."""
+    ops, layer, synthetic = pd
+    H, I, E, k = 2048, 768, 128, 8
+    layers = [synthetic.make_layer(**dict(synthetic.QWEN, seed=70 + l), device=DEV) for l in range(4)]
+    slots = [ops.slot_table([ly.experts[e] for e in range(E)], DEV) for ly in layers]
+    xin = synthetic.make_tokens(1, H, seed=300, device=DEV)
+    rin = synthetic.make_tokens(1, H, seed=301, device=DEV)
+    bufs = [dict(out=torch.empty((1, H), dtype=torch.bfloat16, device=DEV),
+                 x_out=torch.empty((1, H), dtype=torch.bfloat16, device=DEV),
+                 logits=torch.empty((1, E), dtype=torch.bfloat16, device=DEV),
+                 ids=torch.empty((1, k), dtype=torch.int32, device=DEV),
+                 weights=torch.empty((1, k), dtype=torch.bfloat16, device=DEV),
+                 h_ws=torch.empty(k * I, dtype=torch.bfloat16, device=DEV),
+                 pred=torch.full((k,), -1, dtype=torch.int32, device=DEV)) for _ in layers]
+
+    def step():
+        x, r = xin, rin
+        for l, ly in enumerate(layers):
+            b = bufs[l]
+            extra = dict(next_gate=layers[l + 1].gate, pred_out=b["pred"]) if l + 1 < len(layers) else {}
+            ops.decode_layer(x, ly.gate, slots[l], I, k, True, out=b["out"], logits=b["logits"], ids=b["ids"],
+                             weights=b["weights"], h_ws=b["h_ws"], resid=r, x_out=b["x_out"], merge="reference",
+                             **extra)
+            x, r = b["out"], b["x_out"]
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    torch.cuda.synchronize()
+    for seed in range(310, 316):
+        xin.copy_(synthetic.make_tokens(1, H, seed=seed, device=DEV))
+        rin.copy_(synthetic.make_tokens(1, H, seed=seed + 100, device=DEV))
+        step()
+        torch.cuda.synchronize()
+        eager = [{n: t.clone() for n, t in b.items() if n != "h_ws"} for b in bufs]
+        for b in bufs:
+            for t in b.values():
+                t.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        for l, (b, e) in enumerate(zip(bufs, eager)):
+            for n, want in e.items():
+                if n == "pred" and l + 1 == len(layers):
+                    continue
+                assert torch.equal(b[n], want), (seed, l, n)
+    _assert_sync_clean(ops, H)
