@@ -195,8 +195,9 @@ __global__ __launch_bounds__(256, 2) void decode_layer_kernel(
     const uint16_t *__restrict__ x, const uint16_t *__restrict__ resid, uint16_t *__restrict__ x_out,
     const uint16_t *__restrict__ gate, const float *__restrict__ bias, int H, int E, int k, int normalize,
     int merge_mode, const uint16_t *const *__restrict__ slots, int I, const uint16_t *__restrict__ next_gate,
-    int32_t *__restrict__ pred_out, uint16_t *__restrict__ logits, int32_t *__restrict__ ids, uint16_t *__restrict__ weights, float *__restrict__ probs,
-    uint16_t *__restrict__ h_ws, uint16_t *__restrict__ out, uint32_t *ws) {
+    int32_t *__restrict__ pred_out, uint16_t *__restrict__ logits, int32_t *__restrict__ ids,
+    uint16_t *__restrict__ weights, float *__restrict__ probs, uint16_t *__restrict__ h_ws,
+    uint16_t *__restrict__ out, uint32_t *ws) {
     extern __shared__ uint4 s_h[];       // k * I bf16
     __shared__ float s_logit[kDecodeMaxE];
     __shared__ uint32_t s_pub[16];
@@ -219,7 +220,8 @@ __global__ __launch_bounds__(256, 2) void decode_layer_kernel(
     const int e_route = (routes ? (int)blockIdx.x : (int)blockIdx.x - RB) * 4 + wave;
     uint4 wv[NCH];
     if (routes || predicts) {
-        const uint4 *wrow = reinterpret_cast<const uint4 *>((routes ? gate : next_gate) + (size_t)min(e_route, E - 1) * H);
+        const uint16_t *src = routes ? gate : next_gate;
+        const uint4 *wrow = reinterpret_cast<const uint4 *>(src + (size_t)min(e_route, E - 1) * H);
 #pragma unroll
         for (int j = 0; j < NCH; ++j) wv[j] = wrow[min(lane + 64 * j, C - 1)];
     }
