@@ -115,6 +115,76 @@ __global__ __launch_bounds__(512) void route_partial_kernel(const uint16_t *__re
     }
 }
 
+// route_partial_lds_kernel: the same partials for large T with less
+// traffic.  Block (128 tokens, K chunk ks) stages the 256-element chunk of
+// every router row in LDS once, by direct-to-LDS loads (lane l of a load
+// fills bytes 16 l of a 1 KB piece), and its 4 waves each take 32 tokens
+// against all E experts.  The chunk is read once per 128 tokens instead of
+// once per 32, and the token rows once per block instead of once per wave.
+// LDS row r (512 bytes) holds its logical 16-byte chunk c in slot
+// c ^ (r % 16), so the 16 rows of a fragment read hit 16 distinct bank
+// groups.  Each partial is the same MFMA chain as in route_partial_kernel.
+__global__ __launch_bounds__(256) void route_partial_lds_kernel(const uint16_t *__restrict__ x,
+                                                                const uint16_t *__restrict__ gate, int T, int H,
+                                                                int E, float *__restrict__ part) {
+    constexpr int STEPS = 16, KC = 16 * STEPS;  // K elements per chunk
+    constexpr int ROWB = KC * 2;                // 512 bytes per router row
+    __shared__ __attribute__((aligned(1024))) uint8_t s_gate[256 * ROWB];  // E <= 256 rows
+    const int lane = lane_id(), wave = threadIdx.x >> 6;
+    const int ks = blockIdx.y;
+    const int t0 = blockIdx.x * 128 + wave * 32;
+    const int kbase = ks * KC;
+    // the router chunk: E/2 pieces of 1 KB (two rows each), E/8 per wave;
+    // lane l writes slot l % 32 of row 2 p + l / 32, i.e. logical chunk
+    // (l % 32) ^ (row % 16)
+    for (int pc = wave; pc < E / 2; pc += 4) {
+        const int row = 2 * pc + (lane >> 5);
+        const int c = (lane & 31) ^ (row & 15);
+        const uint16_t *src = gate + (size_t)row * H + kbase + c * 8;
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(uintptr_t)src,
+                                         (__attribute__((address_space(3))) void *)(uint32_t)(uintptr_t)(
+                                             s_gate + pc * 1024),
+                                         16, 0, 0);
+    }
+    // this wave's token rows
+    const int trow = min(t0 + (lane & 31), T - 1);
+    const uint16_t *xa = x + (size_t)trow * H + kbase + (lane >> 5) * 8;
+    bf16x8_t a[STEPS];
+#pragma unroll
+    for (int st = 0; st < STEPS; ++st) a[st] = *reinterpret_cast<const bf16x8_t *>(xa + 16 * st);
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's chunk pieces and token rows have landed
+    __syncthreads();
+    const int ET = E / 32;
+    f32x16_t acc[8];
+#pragma unroll
+    for (int et = 0; et < 8; ++et) acc[et] = f32x16_t{};
+#pragma unroll
+    for (int st = 0; st < STEPS; ++st) {
+        const int c = st * 2 + (lane >> 5);
+#pragma unroll
+        for (int et = 0; et < 8; ++et) {
+            if (et < ET) {
+                const int row = et * 32 + (lane & 31);
+                const bf16x8_t b =
+                    *reinterpret_cast<const bf16x8_t *>(s_gate + row * ROWB + ((c ^ (row & 15)) << 4));
+                acc[et] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[st], b, acc[et], 0, 0, 0);
+            }
+        }
+    }
+    // lane holds expert column et*32 + (lane & 31), token rows (r/4)*8 + (lane/32)*4 + r%4
+    float *dst = part + (size_t)ks * T * E;
+#pragma unroll
+    for (int et = 0; et < 8; ++et) {
+        if (et >= ET) continue;
+        const int e = et * 32 + (lane & 31);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int t = t0 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+            if (t < T) dst[(size_t)t * E + e] = acc[et][r];
+        }
+    }
+}
+
 // route_finish_kernel: one wave per token sums the KS partials in chunk
 // order, rounds to the bf16 logit and runs the softmax / top-k / renorm.
 // The partials are loaded eight chunks at a time before they are added (one
@@ -162,6 +232,9 @@ __global__ __launch_bounds__(256) void route_finish_kernel(const float *__restri
     wave_lds_sync();
     topk_token<J>(s_logit[wave], bias, E, k, normalize, t, ids, weights, probs, &s_tk[wave]);
 }
+
+// Token count from which the partial logits use the LDS-staged kernel.
+constexpr int kRouteStagedMinT = 2048;
 
 // K chunk of the split-K router: 256 elements (16 MFMA steps) when H allows.
 static int route_kchunk(int H) {
@@ -229,6 +302,13 @@ PD_API int pdscope_route_topk(const void *x, const void *gate, const float *bias
     float *part = reinterpret_cast<float *>(static_cast<char *>(workspace) + 256);
     const dim3 g1((T + 31) / 32, KS);
     const int threads = (E / 32) * 64;
+    // large T: 128 tokens per block over an LDS-staged router chunk
+    // (needs the 256-element chunk)
+    const bool staged = T >= kRouteStagedMinT && kc == 256;
+    if (staged) {
+        const dim3 gs((T + 127) / 128, KS);
+        route_partial_lds_kernel<<<gs, 256, 0, s>>>((const uint16_t *)x, (const uint16_t *)gate, T, H, E, part);
+    } else {
     switch (kc / 16) {
 #define PD_RP(ST)                                                                                           \
     case ST:                                                                                                \
@@ -239,7 +319,8 @@ PD_API int pdscope_route_topk(const void *x, const void *gate, const float *bias
     default:
         return fail(kEInval, "route: unsupported K chunk");
     }
-    int rc = check_launch("route_partial_kernel");
+    }
+    int rc = check_launch(staged ? "route_partial_lds_kernel" : "route_partial_kernel");
     if (rc) return rc;
     const int g2 = (T + 3) / 4;
     if (E <= 64)

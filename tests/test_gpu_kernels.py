@@ -61,7 +61,7 @@ def test_route_small_T_qwen(orc, pd, qwen, T):
     _route_check(orc, ops, x, qwen.gate, 8, True)
 
 
-@pytest.mark.parametrize("T", [9, 33, 512, 4096])
+@pytest.mark.parametrize("T", [9, 33, 512, 2100, 4096])
 def test_route_mfma_qwen(orc, pd, qwen, T):
     ops, _, synthetic = pd
     x = synthetic.make_tokens(T, 2048, seed=200 + T)
@@ -126,6 +126,22 @@ def test_route_probability_collisions(orc, pd, T):
     x = (torch.rand((T, H), generator=gen, device=DEV) + 0.5).to(torch.bfloat16)
     _, ik, _ = _route_check(orc, ops, x, gate, 8, True)
     assert (ik[:, :3] == [100, 50, 7]).all() and (ik[:, 3:] == [0, 1, 2, 3, 4]).all()
+
+
+@pytest.mark.parametrize("E,k", [(64, 6), (128, 8), (256, 16)])
+def test_route_staged_partials_equal_unstaged(pd, E, k):
+    """From 2048 tokens the partial logits come from the LDS-staged kernel
+    (128 tokens per block); below, from the 32-token kernel.  Both add the
+    same MFMA chains, so the first 2047 tokens route bit for bit alike."""
+    ops, _, synthetic = pd
+    gen = torch.Generator(device=DEV).manual_seed(17 + E)
+    gate = (torch.randn((E, 2048), generator=gen, device=DEV) * 0.02).to(torch.bfloat16)
+    x = synthetic.make_tokens(2048, 2048, seed=500 + E)
+    la, ia, wa, _ = ops.route_topk(x, gate, k, True)
+    lb, ib, wb, _ = ops.route_topk(x[:2047].contiguous(), gate, k, True)
+    torch.cuda.synchronize()
+    assert torch.equal(la[:2047].view(torch.int16), lb.view(torch.int16))
+    assert torch.equal(ia[:2047], ib) and torch.equal(wa[:2047].view(torch.int16), wb.view(torch.int16))
 
 
 def test_route_hist(orc, pd):
