@@ -216,21 +216,20 @@ def run_prefill(T, steps, warmup, n_layers, device, seed0):
         logits, ids, w = layer.route(x, lay.gate, ws)
         ops.pack(ids, E, out=packed, workspace=ws.pack_ws)
         bm = ops.grouped_block_m(n // E)
-        ops.schedule(packed.counts, ws.sel_all, bm, out=ws.tile_start, order=ws.sel_order)
         max_tiles = (n + bm - 1) // bm + E
-        # the down launch has its own row tile (layer.down_block_m)
+        # the down launch has its own row tile (layer.down_block_m); one launch schedules both
         bmd = layer.down_block_m(bm, H, I)
-        sel_d, ts_d = (ws.sel_order_down, ws.tile_start_down) if bmd != bm else (ws.sel_order, ws.tile_start)
-        if bmd != bm:
-            ops.schedule(packed.counts, ws.sel_all, bmd, out=ts_d, order=sel_d)
+        ts_d = ws.tile_start_down if bmd != bm else ws.tile_start
+        ops.schedule(packed.counts, ws.sel_all, bm, out=ws.tile_start, order=ws.sel_order,
+                     **(dict(block_m2=bmd, out2=ts_d) if bmd != bm else {}))
         if ev is not None:
             ev[0].record(stream)
         ops.swiglu_grouped_gateup(x, packed.perm_token, packed.offsets, ws.sel_order, ws.tile_start, max_tiles, bm,
                                   slots, H, I, ws.h_ws)
         if ev is not None:
             ev[1].record(stream)
-        ops.swiglu_grouped_down(ws.h_ws, packed.offsets, sel_d, ts_d, (n + bmd - 1) // bmd + E, bmd, slots, H, I,
-                                ws.y)
+        ops.swiglu_grouped_down(ws.h_ws, packed.offsets, ws.sel_order, ts_d, (n + bmd - 1) // bmd + E, bmd, slots,
+                                H, I, ws.y)
         if ev is not None:
             ev[2].record(stream)
         ops.merge(ws.y, packed.row_of, w, ws.out[:T])
@@ -532,12 +531,11 @@ def zipf_gemm(lay, x, bias, device, reps=20):
     _, _, _, packed = ws.views(T)
     ops.pack(ids, E, out=packed, workspace=ws.pack_ws)
     bm = ops.grouped_block_m((T * K_TOP) // E, int(ws.counts.max().item()))
-    ops.schedule(packed.counts, ws.sel_all, bm, out=ws.tile_start, order=ws.sel_order)
     max_tiles = (T * K_TOP + bm - 1) // bm + E
     bmd = layer.down_block_m(bm, H, I)
-    sel_d, ts_d = (ws.sel_order_down, ws.tile_start_down) if bmd != bm else (ws.sel_order, ws.tile_start)
-    if bmd != bm:
-        ops.schedule(packed.counts, ws.sel_all, bmd, out=ts_d, order=sel_d)
+    ts_d = ws.tile_start_down if bmd != bm else ws.tile_start
+    ops.schedule(packed.counts, ws.sel_all, bm, out=ws.tile_start, order=ws.sel_order,
+                 **(dict(block_m2=bmd, out2=ts_d) if bmd != bm else {}))
     max_tiles_d = (T * K_TOP + bmd - 1) // bmd + E
     stream = torch.cuda.current_stream(device)
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(reps + 2)]
@@ -546,7 +544,7 @@ def zipf_gemm(lay, x, bias, device, reps=20):
         ops.swiglu_grouped_gateup(x, packed.perm_token, packed.offsets, ws.sel_order, ws.tile_start, max_tiles, bm,
                                   slots, H, I, ws.h_ws)
         ev[r][1].record(stream)
-        ops.swiglu_grouped_down(ws.h_ws, packed.offsets, sel_d, ts_d, max_tiles_d, bmd, slots, H, I, ws.y)
+        ops.swiglu_grouped_down(ws.h_ws, packed.offsets, ws.sel_order, ts_d, max_tiles_d, bmd, slots, H, I, ws.y)
         ev[r][2].record(stream)
     torch.cuda.synchronize(device)
     gu = statistics.mean(ev[r][0].elapsed_time(ev[r][1]) for r in range(2, reps + 2))

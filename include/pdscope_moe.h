@@ -122,6 +122,15 @@ int pdscope_schedule(const int32_t *counts, const int32_t *sel, int nsel, int bl
 int pdscope_schedule_balanced(const int32_t *counts, const int32_t *sel, int nsel, int block_m,
                               int32_t *order, int32_t *tile_start, void *stream);
 
+/*
+ * pdscope_schedule_balanced for a gate/up and a down launch whose row tiles
+ * differ, in one launch: the order depends on the rows only, so both
+ * launches take `order`; tile_start is its m-tile prefix for block_m and
+ * tile_start2 for block_m2.  No counterpart in the reference.
+ */
+int pdscope_schedule_balanced_pair(const int32_t *counts, const int32_t *sel, int nsel, int block_m, int block_m2,
+                                   int32_t *order, int32_t *tile_start, int32_t *tile_start2, void *stream);
+
 /* Row tile (32, 64, 128, 256 or 384) for `rows_hint` average rows per
  * selected expert: <= 16 rows 32, <= 64 rows 64, <= 124 rows 128, <= 192 rows
  * 256, <= 320 rows 384 (one tile holds a typical expert, so its weights

@@ -292,10 +292,13 @@ __global__ __launch_bounds__(256) void schedule_kernel(const int32_t *__restrict
 // and small experts (similar work) and starts with its largest ones, so the
 // short tiles run last.  order[i] is the expert at position i of that list,
 // tile_start its m-tile prefix (as schedule_kernel over `order`).  nsel <= 256.
+// With tile_start2, the same order's m-tile prefix for a second row tile bm2
+// (the order depends on the rows only, not on the tile).
 __global__ __launch_bounds__(256) void schedule_balanced_kernel(const int32_t *__restrict__ counts,
                                                                 const int32_t *__restrict__ sel, int nsel, int bm,
                                                                 int32_t *__restrict__ order,
-                                                                int32_t *__restrict__ tile_start) {
+                                                                int32_t *__restrict__ tile_start, int bm2,
+                                                                int32_t *__restrict__ tile_start2) {
     __shared__ __align__(16) int s_rows[256];  // -1 past nsel: never ranks above a real expert
     __shared__ int s_at[256];  // list position -> sel position
     __shared__ int s_wsum[4];
@@ -323,15 +326,21 @@ __global__ __launch_bounds__(256) void schedule_balanced_kernel(const int32_t *_
         s_at[before + rd] = i;
     }
     __syncthreads();
-    int tiles = 0;
+    int tiles = 0, tiles2 = 0;
     if (i < nsel) {
         const int si = s_at[i];
         order[i] = sel[si];
         tiles = (s_rows[si] + bm - 1) / bm;
+        if (tile_start2) tiles2 = (s_rows[si] + bm2 - 1) / bm2;
     }
     const int incl = block_scan256(tiles, s_wsum);
     if (i == 0) tile_start[0] = 0;
     if (i < nsel) tile_start[i + 1] = incl;
+    if (tile_start2) {  // uniform: the whole block takes this branch
+        const int incl2 = block_scan256(tiles2, s_wsum);
+        if (i == 0) tile_start2[0] = 0;
+        if (i < nsel) tile_start2[i + 1] = incl2;
+    }
 }
 
 }  // namespace pd
@@ -444,6 +453,19 @@ PD_API int pdscope_schedule_balanced(const int32_t *counts, const int32_t *sel, 
     if (block_m != 32 && block_m != 64 && block_m != 128 && block_m != 256 && block_m != 384)
         return fail(kEInval, "schedule_balanced: block_m must be 32, 64, 128, 256 or 384");
     schedule_balanced_kernel<<<1, 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(counts, sel, nsel, block_m, order,
-                                                                                   tile_start);
+                                                                                   tile_start, 0, nullptr);
+    return check_launch("schedule_balanced_kernel");
+}
+
+PD_API int pdscope_schedule_balanced_pair(const int32_t *counts, const int32_t *sel, int nsel, int block_m,
+                                          int block_m2, int32_t *order, int32_t *tile_start, int32_t *tile_start2,
+                                          void *stream) {
+    if (!counts || !sel || !order || !tile_start || !tile_start2 || nsel < 0 || nsel > 256)
+        return fail(kEInval, "schedule_balanced_pair: bad arguments (nsel must be 0..256)");
+    for (int b : {block_m, block_m2})
+        if (b != 32 && b != 64 && b != 128 && b != 256 && b != 384)
+            return fail(kEInval, "schedule_balanced_pair: block sizes must be 32, 64, 128, 256 or 384");
+    schedule_balanced_kernel<<<1, 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(counts, sel, nsel, block_m, order,
+                                                                                   tile_start, block_m2, tile_start2);
     return check_launch("schedule_balanced_kernel");
 }

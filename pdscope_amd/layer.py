@@ -35,7 +35,6 @@ class MoEWorkspace:
         self.tile_start = torch.empty(E + 1, **i32)
         self.sel_order = torch.empty(E, **i32)  # balanced expert order of the grouped launch
         self.tile_start_down = torch.empty(E + 1, **i32)  # the down launch's own tiling (down_block_m)
-        self.sel_order_down = torch.empty(E, **i32)
         self.sel_all = torch.arange(E, **i32)
         rows = 1 if route_only else max(n, 1)
         self.h_ws = torch.empty(rows * I, dtype=BF16, device=device)
@@ -155,15 +154,16 @@ def grouped_ffn(x, packed, sel, bm, max_tiles, slots, ws: MoEWorkspace, *, max_t
     perm = packed.perm_token if perm is None else perm
     nsel = sel.numel()
     tile_start, order = ws.tile_start[:nsel + 1], ws.sel_order[:nsel]
-    ops.schedule(packed.counts, sel, bm, out=tile_start, order=order)
     bmd = down_block_m(bm, H, I)
     if bmd == bm:
+        ops.schedule(packed.counts, sel, bm, out=tile_start, order=order)
         ops.swiglu_grouped(x, perm, packed.offsets, order, tile_start, max_tiles, bm, slots, H, I, ws.h_ws, ws.y)
         return
-    tile_down, order_down = ws.tile_start_down[:nsel + 1], ws.sel_order_down[:nsel]
-    ops.schedule(packed.counts, sel, bmd, out=tile_down, order=order_down)
+    # one launch schedules both: the balanced order depends on the rows only
+    tile_down = ws.tile_start_down[:nsel + 1]
+    ops.schedule(packed.counts, sel, bm, out=tile_start, order=order, block_m2=bmd, out2=tile_down)
     ops.swiglu_grouped_gateup(x, perm, packed.offsets, order, tile_start, max_tiles, bm, slots, H, I, ws.h_ws)
-    ops.swiglu_grouped_down(ws.h_ws, packed.offsets, order_down, tile_down, max_tiles_down, bmd, slots, H, I, ws.y)
+    ops.swiglu_grouped_down(ws.h_ws, packed.offsets, order, tile_down, max_tiles_down, bmd, slots, H, I, ws.y)
 
 
 def moe_forward(x, gate, slots, ws: MoEWorkspace, *, normalize=True, bias=None, block_m=None, fused_decode=True,

@@ -171,13 +171,25 @@ def grouped_block_m(rows_hint: int, max_rows: int | None = None) -> int:
     return int(_lib.load().pdscope_grouped_block_m_max(int(rows_hint), int(max_rows)))
 
 
-def schedule(counts, sel, block_m, out=None, order=None):
+def schedule(counts, sel, block_m, out=None, order=None, *, block_m2=None, out2=None):
     """Tile prefix over `sel` (order=None), or, with an int32 [nsel] `order`
     buffer, the balanced order of pdscope_schedule_balanced and the prefix
-    over it: the grouped launch must then take `order` as its sel."""
+    over it: the grouped launch must then take `order` as its sel.  With
+    block_m2 and out2 (balanced only), out2 receives the same order's prefix
+    for a second row tile, from the same launch."""
     _need(counts, "counts", torch.int32, 1)
     _need(sel, "sel", torch.int32, 1, counts.device)
     tile_start = out if out is not None else torch.empty(sel.numel() + 1, dtype=torch.int32, device=counts.device)
+    if block_m2 is not None:
+        if order is None or out2 is None:
+            raise ValueError("a second row tile needs the balanced order and an out2 buffer")
+        _need(order, "order", torch.int32, 1, counts.device)
+        _need(out2, "out2", torch.int32, 1, counts.device)
+        if order.numel() < sel.numel() or out2.numel() < sel.numel() + 1:
+            raise ValueError("order / out2 buffers smaller than sel")
+        _lib.call("pdscope_schedule_balanced_pair", _p(counts), _p(sel), sel.numel(), block_m, block_m2, _p(order),
+                  _p(tile_start), _p(out2), _stream(counts.device))
+        return tile_start
     if order is None:
         _lib.call("pdscope_schedule", _p(counts), _p(sel), sel.numel(), block_m, _p(tile_start),
                   _stream(counts.device))

@@ -374,6 +374,31 @@ def test_schedule_balanced_order_and_same_outputs(pd, nsel, bm):
     assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
 
 
+@pytest.mark.parametrize("nsel,bm,bm2", [(128, 384, 256), (61, 64, 128), (1, 32, 384), (256, 256, 32)])
+def test_schedule_balanced_pair_equals_two_schedules(pd, nsel, bm, bm2):
+    """The paired launch writes the order and both tile prefixes of two
+    separate balanced schedules, and the gate/up + down launches over them
+    equal the one-tile grouped launch (bitwise)."""
+    ops, layer, synthetic = pd
+    g = torch.Generator().manual_seed(nsel * 7 + bm2)
+    E = max(nsel, 8)
+    rows = (torch.rand(E, generator=g) ** 3 * 700).to(torch.int32)
+    rows[torch.randperm(E, generator=g)[:E // 4]] = 0
+    sel = torch.tensor(sorted(torch.randperm(E, generator=g)[:nsel].tolist()), dtype=torch.int32, device=DEV)
+    counts = rows.to(DEV)
+    order1, order2 = (torch.full((nsel,), -1, dtype=torch.int32, device=DEV) for _ in range(2))
+    ts1 = ops.schedule(counts, sel, bm, order=order1)
+    ts2 = ops.schedule(counts, sel, bm2, order=order2)
+    order = torch.full((nsel,), -1, dtype=torch.int32, device=DEV)
+    out1, out2 = (torch.full((nsel + 1,), -1, dtype=torch.int32, device=DEV) for _ in range(2))
+    ops.schedule(counts, sel, bm, out=out1, order=order, block_m2=bm2, out2=out2)
+    torch.cuda.synchronize()
+    assert torch.equal(order, order1) and torch.equal(order, order2)
+    assert torch.equal(out1, ts1) and torch.equal(out2, ts2)
+    with pytest.raises(ValueError):
+        ops.schedule(counts, sel, bm, out=out1, block_m2=bm2, out2=out2)
+
+
 def test_decode_qwen(orc, pd, qwen, qwen_host):
     ops, layer, synthetic = pd
     ws = layer.MoEWorkspace(1, 2048, 768, 128, 8, DEV)
