@@ -54,6 +54,11 @@ __device__ __forceinline__ void load_lds16(const uint16_t *src, uint8_t *dst) {
     __builtin_amdgcn_global_load_lds((g_void_t *)(uintptr_t)src, (lds_void_t *)(uint32_t)(uintptr_t)dst, 16, 0, AUX);
 }
 
+// Hides a per-lane load offset from loop-invariant code motion, so each
+// 64-bit address (uniform base + offset) is formed next to its load instead
+// of being hoisted out of the K loop as a live register pair per load.
+__device__ __forceinline__ void opaque(uint32_t &v) { asm volatile("" : "+v"(v)); }
+
 // Wait until at most n vector-memory operations of this wave are in flight
 // (n is a compile-time constant in every use).
 template <int N>
@@ -188,46 +193,62 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void grouped_kernel(
     const int a_live = SPLIT ? __builtin_amdgcn_readfirstlane(
                                    min(AL, max(0, (live_groups - wa + NWA - 1) / NWA)))
                              : AL;
-    const uint16_t *lp[LW];
-    auto a_ptr = [&](int q) {
+    // Load sources as 32-bit offsets in 16-byte units from a wave-uniform base
+    // (A: a_src, B: the expert's block; every row start and chunk is 16-byte
+    // aligned, and 2^32 units cover 64 GiB), one register per load instead
+    // of a 64-bit pointer.
+    uint32_t lp[LW];
+    auto a_off = [&](int q) {
         const int row = (wa + NWA * q) * G::RPI + rl;
-        const int cs = slot ^ G::key(row);
+        const uint32_t cs = (uint32_t)(slot ^ G::key(row));
         const int gr = min(m0 + row, row_end - 1);
-        return GATEUP ? a_src + (size_t)perm_token[gr] * H + cs * 8 : a_src + (size_t)gr * I + cs * 8;
+        return GATEUP ? (uint32_t)perm_token[gr] * (uint32_t)(H / 8) + cs : (uint32_t)gr * (uint32_t)(I / 8) + cs;
     };
-    auto b_ptr = [&](int q) {
+    auto b_off = [&](int q) {
         const int rb = (wb + NWB * q) * G::RPI + rl;
-        const int cs = slot ^ G::key(rb);
+        const uint32_t cs = (uint32_t)(slot ^ G::key(rb));
         if (GATEUP) {
-            const int i = n0 + (rb < BN / 2 ? rb : rb - BN / 2);
-            return base + (rb < BN / 2 ? 0 : IH) + (size_t)i * H + cs * 8;
+            const uint32_t i = (uint32_t)(n0 + (rb < BN / 2 ? rb : rb - BN / 2));
+            return (rb < BN / 2 ? 0u : (uint32_t)(IH / 8)) + i * (uint32_t)(H / 8) + cs;
         }
-        return base + 2 * IH + (size_t)(n0 + rb) * I + cs * 8;
+        return (uint32_t)(IH / 4) + (uint32_t)(n0 + rb) * (uint32_t)(I / 8) + cs;
     };
     if constexpr (SPLIT) {
         if (a_role) {
 #pragma unroll
-            for (int q = 0; q < AL; ++q) lp[q] = a_ptr(q);
+            for (int q = 0; q < AL; ++q) lp[q] = a_off(q);
         } else {
 #pragma unroll
-            for (int q = 0; q < BL; ++q) lp[q] = b_ptr(q);
+            for (int q = 0; q < BL; ++q) lp[q] = b_off(q);
         }
     } else {
 #pragma unroll
-        for (int q = 0; q < AL; ++q) lp[q] = a_ptr(q);
+        for (int q = 0; q < AL; ++q) lp[q] = a_off(q);
 #pragma unroll
-        for (int q = 0; q < BL; ++q) lp[AL + q] = b_ptr(q);
+        for (int q = 0; q < BL; ++q) lp[AL + q] = b_off(q);
     }
+    const uint8_t *const a_base = reinterpret_cast<const uint8_t *>(a_src);
+    const uint8_t *const b_base = reinterpret_cast<const uint8_t *>(base);
     auto issue_a = [&](int kt, int q0) __attribute__((always_inline)) {  // A stage kt from lp[q0 ..]
         uint8_t *st = ring_a + (kt % SA) * ASTAGE;
+        const uint8_t *b = a_base + kt * (BK * 2);
 #pragma unroll
         for (int q = 0; q < AL; ++q)
-            if (q < a_live) load_lds16(lp[q0 + q] + kt * BK, st + (wa + NWA * q) * 1024);
+            if (q < a_live) {
+                uint32_t o = lp[q0 + q];
+                opaque(o);
+                load_lds16(reinterpret_cast<const uint16_t *>(b + (size_t)o * 16), st + (wa + NWA * q) * 1024);
+            }
     };
     auto issue_b = [&](int kt, int q0) __attribute__((always_inline)) {
         uint8_t *st = ring_b + (kt % SB) * BSTAGE;
+        const uint8_t *b = b_base + kt * (BK * 2);
 #pragma unroll
-        for (int q = 0; q < BL; ++q) load_lds16<kDeviceScope>(lp[q0 + q] + kt * BK, st + (wb + NWB * q) * 1024);
+        for (int q = 0; q < BL; ++q) {
+            uint32_t o = lp[q0 + q];
+            opaque(o);
+            load_lds16<kDeviceScope>(reinterpret_cast<const uint16_t *>(b + (size_t)o * 16), st + (wb + NWB * q) * 1024);
+        }
     };
 
     const int wm = wave / WN, wn = wave % WN;
