@@ -141,7 +141,6 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void grouped_kernel(
     constexpr int NWA = SPLIT ? NW / 2 : NW, NWB = SPLIT ? NW / 2 : NW;  // waves loading A / B
     constexpr int AL = BM / G::RPI / NWA, BL = BN / G::RPI / NWB;  // 1 KB loads per loading wave per stage
     static_assert(AL >= 1 && BL >= 1 && AL * G::RPI * NWA == BM && BL * G::RPI * NWB == BN, "tile / load shape");
-    constexpr int LW = SPLIT ? (AL > BL ? AL : BL) : AL + BL;  // load pointers per wave
     static_assert(!SPLIT || (SA - 1) * AL <= 24, "A-wave waits count live loads up to wait_vm_rt's range");
     constexpr int ASTAGE = BM * G::RB, BSTAGE = BN * G::RB;
     __shared__ __attribute__((aligned(1024))) uint8_t smem[SA * ASTAGE + SB * BSTAGE];
@@ -180,7 +179,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void grouped_kernel(
     // ---- per-lane source rows: load q of A-wave wa covers A rows
     // RPI(wa + NWA q) .. +RPI-1 (B likewise with wb, NWB); lane l takes row
     // +l/CPR and the logical chunk that belongs in slot l % CPR of that row
-    // (the swizzle).  Unified roles: lp[0, AL) are A loads, lp[AL, AL+BL) B.
+    // (the swizzle).
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const bool a_role = !SPLIT || wave < NWA;
@@ -193,61 +192,62 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void grouped_kernel(
     const int a_live = SPLIT ? __builtin_amdgcn_readfirstlane(
                                    min(AL, max(0, (live_groups - wa + NWA - 1) / NWA)))
                              : AL;
-    // Load sources as 32-bit offsets in 16-byte units from a wave-uniform base
-    // (A: a_src, B: the expert's block; every row start and chunk is 16-byte
-    // aligned, and 2^32 units cover 64 GiB), one register per load instead
-    // of a 64-bit pointer.
-    uint32_t lp[LW];
-    auto a_off = [&](int q) {
-        const int row = (wa + NWA * q) * G::RPI + rl;
-        const uint32_t cs = (uint32_t)(slot ^ G::key(row));
-        const int gr = min(m0 + row, row_end - 1);
-        return GATEUP ? (uint32_t)perm_token[gr] * (uint32_t)(H / 8) + cs : (uint32_t)gr * (uint32_t)(I / 8) + cs;
-    };
-    auto b_off = [&](int q) {
-        const int rb = (wb + NWB * q) * G::RPI + rl;
-        const uint32_t cs = (uint32_t)(slot ^ G::key(rb));
-        if (GATEUP) {
-            const uint32_t i = (uint32_t)(n0 + (rb < BN / 2 ? rb : rb - BN / 2));
-            return (rb < BN / 2 ? 0u : (uint32_t)(IH / 8)) + i * (uint32_t)(H / 8) + cs;
+    // Load addresses.  Load q of a wave covers rows (w + NW q) RPI .. + RPI-1 of
+    // its tile, and NW RPI is a multiple of the swizzle period (16 rows), so
+    // a lane's row within the group and its swizzled chunk are the same for
+    // every q: a per-lane byte offset plus a wave-uniform part per q.  Only the
+    // gathered gate/up activation rows need a register per load (their token
+    // offsets, in 16-byte units from a_src: 2^32 units cover 64 GiB).
+    static_assert((NWA * G::RPI) % 16 == 0 && (NWB * G::RPI) % 16 == 0, "swizzle period");
+    const uint32_t a_cs = (uint32_t)(slot ^ G::key(wa * G::RPI + rl));
+    const uint32_t b_cs = (uint32_t)(slot ^ G::key(wb * G::RPI + rl));
+    uint32_t lp[GATEUP ? AL : 1];
+    if (GATEUP && a_role) {
+#pragma unroll
+        for (int q = 0; q < AL; ++q) {
+            const int gr = min(m0 + (wa + NWA * q) * G::RPI + rl, row_end - 1);
+            lp[q] = (uint32_t)perm_token[gr] * (uint32_t)(H / 8) + a_cs;
         }
-        return (uint32_t)(IH / 4) + (uint32_t)(n0 + rb) * (uint32_t)(I / 8) + cs;
-    };
-    if constexpr (SPLIT) {
-        if (a_role) {
-#pragma unroll
-            for (int q = 0; q < AL; ++q) lp[q] = a_off(q);
-        } else {
-#pragma unroll
-            for (int q = 0; q < BL; ++q) lp[q] = b_off(q);
-        }
-    } else {
-#pragma unroll
-        for (int q = 0; q < AL; ++q) lp[q] = a_off(q);
-#pragma unroll
-        for (int q = 0; q < BL; ++q) lp[AL + q] = b_off(q);
     }
+    // B: the lane's row and chunk in bytes from the first row of its load group
+    const uint32_t b_lane = (uint32_t)rl * (uint32_t)(K * 2) + b_cs * 16u;
+    // B: byte offset of load q's first row in the expert's block
+    auto b_row0 = [&](int q) __attribute__((always_inline)) {
+        const int rb = (wb + NWB * q) * G::RPI;
+        if (GATEUP)
+            return rb < BN / 2 ? (size_t)(n0 + rb) * H * 2 : (size_t)IH * 2 + (size_t)(n0 + rb - BN / 2) * H * 2;
+        return (size_t)IH * 4 + (size_t)(n0 + rb) * I * 2;
+    };
     const uint8_t *const a_base = reinterpret_cast<const uint8_t *>(a_src);
     const uint8_t *const b_base = reinterpret_cast<const uint8_t *>(base);
-    auto issue_a = [&](int kt, int q0) __attribute__((always_inline)) {  // A stage kt from lp[q0 ..]
+    auto issue_a = [&](int kt) __attribute__((always_inline)) {
         uint8_t *st = ring_a + (kt % SA) * ASTAGE;
         const uint8_t *b = a_base + kt * (BK * 2);
 #pragma unroll
         for (int q = 0; q < AL; ++q)
             if (q < a_live) {
-                uint32_t o = lp[q0 + q];
-                opaque(o);
-                load_lds16(reinterpret_cast<const uint16_t *>(b + (size_t)o * 16), st + (wa + NWA * q) * 1024);
+                if (GATEUP) {
+                    uint32_t o = lp[GATEUP ? q : 0];
+                    opaque(o);
+                    load_lds16(reinterpret_cast<const uint16_t *>(b + (size_t)o * 16), st + (wa + NWA * q) * 1024);
+                } else {
+                    // h rows in grouped order; rows past the expert's end (all
+                    // of a dead group's, with unified roles) repeat its last row
+                    const int gr = min(m0 + (wa + NWA * q) * G::RPI + rl, row_end - 1);
+                    uint32_t o = (uint32_t)gr * (uint32_t)(I / 8) + a_cs;
+                    opaque(o);
+                    load_lds16(reinterpret_cast<const uint16_t *>(b + (size_t)o * 16), st + (wa + NWA * q) * 1024);
+                }
             }
     };
-    auto issue_b = [&](int kt, int q0) __attribute__((always_inline)) {
+    auto issue_b = [&](int kt) __attribute__((always_inline)) {
         uint8_t *st = ring_b + (kt % SB) * BSTAGE;
         const uint8_t *b = b_base + kt * (BK * 2);
 #pragma unroll
         for (int q = 0; q < BL; ++q) {
-            uint32_t o = lp[q0 + q];
+            uint32_t o = b_lane;
             opaque(o);
-            load_lds16<kDeviceScope>(reinterpret_cast<const uint16_t *>(b + (size_t)o * 16), st + (wb + NWB * q) * 1024);
+            load_lds16<kDeviceScope>(reinterpret_cast<const uint16_t *>(b + b_row0(q) + o), st + (wb + NWB * q) * 1024);
         }
     };
 
@@ -317,19 +317,19 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void grouped_kernel(
         if constexpr (ROLE == 1) {
 #pragma unroll
             for (int s0 = 0; s0 < SA; ++s0)
-                if (s0 < KT) issue_a(s0, 0);
+                if (s0 < KT) issue_a(s0);
             wait_vm_rt(min(SA - 1, KT - 1) * a_live);
         } else if constexpr (ROLE == 2) {
 #pragma unroll
             for (int s0 = 0; s0 < SB; ++s0)
-                if (s0 < KT) issue_b(s0, 0);
+                if (s0 < KT) issue_b(s0);
             wait_stage<SB + 1, BL>(min(SB - 1, KT - 1));
         } else {
 #pragma unroll
             for (int s0 = 0; s0 < SA; ++s0)
                 if (s0 < KT) {
-                    issue_a(s0, 0);
-                    issue_b(s0, AL);
+                    issue_a(s0);
+                    issue_b(s0);
                 }
             wait_stage<SA + 1, AL + BL>(min(SA - 1, KT - 1));
         }
@@ -372,13 +372,13 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void grouped_kernel(
                 ring_barrier();
                 // into stage kt's slots, read out before the barrier
                 if constexpr (ROLE == 1) {
-                    if (STEADY || kt + SA < KT) issue_a(kt + SA, 0);
+                    if (STEADY || kt + SA < KT) issue_a(kt + SA);
                 } else if constexpr (ROLE == 2) {
-                    if (STEADY || kt + SB < KT) issue_b(kt + SB, 0);
+                    if (STEADY || kt + SB < KT) issue_b(kt + SB);
                 } else {
                     if (STEADY || kt + SA < KT) {
-                        issue_a(kt + SA, 0);
-                        issue_b(kt + SA, AL);
+                        issue_a(kt + SA);
+                        issue_b(kt + SA);
                     }
                 }
                 if constexpr (L > 0) read_frags(kt + 1, 0, CUR ^ 1);
