@@ -53,6 +53,15 @@ class MoEWorkspace:
             self.shared_offsets = torch.zeros(2, **i32)
             self.shared_tiles = torch.zeros(2, **i32)
             self.shared_sel = torch.zeros(1, **i32)
+            self._shared_key = None    # (T, row tile) the two tables above hold
+            self._side = None
+
+    def side_stream(self):
+        """A second stream on the workspace's device (default priority) for
+        the shared experts, which run beside the routed ones."""
+        if self._side is None:
+            self._side = torch.cuda.Stream(device=self.device)
+        return self._side
 
     def pregathered(self, n: int) -> torch.Tensor:
         """[n, H] bf16 buffer for activation rows gathered into grouped order."""
@@ -107,17 +116,20 @@ def shared_forward(x, shared_slot, ws: MoEWorkspace):
     T = x.shape[0]
     H, Is = ws.H, ws.shared_I
     bm = shared_block_m(T, Is)
-    ws.shared_offsets[1:].fill_(T)
-    ws.shared_tiles[1:].fill_((T + bm - 1) // bm)
+    if ws._shared_key != (T, bm):   # the one-expert tables depend only on T and the row tile
+        ws.shared_offsets[1:].fill_(T)
+        ws.shared_tiles[1:].fill_((T + bm - 1) // bm)
+        ws._shared_key = (T, bm)
     ops.swiglu_grouped(x, ws.shared_rows[:T], ws.shared_offsets, ws.shared_sel, ws.shared_tiles,
                        (T + bm - 1) // bm, bm, shared_slot, H, Is, ws.h_shared, ws.y_shared)
     return ws.y_shared[:T]
 
 
 def experts_resident(x, ids, weights, slots, ws: MoEWorkspace, out=None, *, block_m=None, add_in=None,
-                     merge="fused"):
+                     merge="fused", before_merge=None):
     """K4 (T == 1) or K2+K3+K5 (T > 1) over experts that are all addressable in `slots`.
-    add_in [T, H] bf16 (shared-expert output) is added unweighted in the merge.
+    add_in [T, H] bf16 (shared-expert output) is added unweighted in the merge;
+    before_merge() runs right before the merge is enqueued (to order add_in's producer).
     merge: 'fused' (fp32 sum, one rounding) or 'reference' (bf16 adds in
     ascending expert id, the reference runtime's default merge)."""
     T = x.shape[0]
@@ -132,6 +144,8 @@ def experts_resident(x, ids, weights, slots, ws: MoEWorkspace, out=None, *, bloc
     bmd = down_block_m(bm, H, I)
     grouped_ffn(x, packed, ws.sel_all, bm, (T * k + bm - 1) // bm + E, slots, ws,
                 max_tiles_down=(T * k + bmd - 1) // bmd + E)
+    if before_merge is not None:
+        before_merge()
     ops.merge(ws.y, packed.row_of, weights, out, add_in=add_in, mode=merge)
     return out
 
@@ -186,9 +200,17 @@ def moe_forward(x, gate, slots, ws: MoEWorkspace, *, normalize=True, bias=None, 
     if shared_slot is not None:
         if not ws.shared_I:
             raise ValueError("shared experts need a workspace built with shared_I")
+        # the shared experts need only x: they run on a side stream beside the
+        # routing and the routed experts (a one-expert launch alone does not
+        # fill the device) and join before the merge adds their output
+        cur = torch.cuda.current_stream(x.device)
+        side = ws.side_stream()
+        side.wait_stream(cur)
+        with torch.cuda.stream(side):
+            y_shared = shared_forward(x, shared_slot, ws)
         logits, ids, weights = route(x, gate, ws, normalize=normalize, bias=bias)
-        y_shared = shared_forward(x, shared_slot, ws)
-        out = experts_resident(x, ids, weights, slots, ws, block_m=block_m, add_in=y_shared, merge=merge)
+        out = experts_resident(x, ids, weights, slots, ws, block_m=block_m, add_in=y_shared, merge=merge,
+                               before_merge=lambda: cur.wait_stream(side))
         return out, logits, ids, weights
     fused = (T == 1 and fused_decode and ws.k <= 8 and shared_slot is None
              and ops.decode_layer_supported(ws.H, ws.I, ws.E, ws.k, x.device))
