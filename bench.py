@@ -214,14 +214,14 @@ def run_prefill(T, steps, warmup, n_layers, device, seed0):
         lay, slots = layers[i % n_layers]
         x = xs[i % n_layers]
         logits, ids, w = layer.route(x, lay.gate, ws)
-        ops.pack(ids, E, out=packed, workspace=ws.pack_ws)
         bm = ops.grouped_block_m(n // E)
         max_tiles = (n + bm - 1) // bm + E
-        # the down launch has its own row tile (layer.down_block_m); one launch schedules both
+        # the down launch has its own row tile (layer.down_block_m); the pack
+        # launch writes the balanced schedule for both
         bmd = layer.down_block_m(bm, H, I)
         ts_d = ws.tile_start_down if bmd != bm else ws.tile_start
-        ops.schedule(packed.counts, ws.sel_all, bm, out=ws.tile_start, order=ws.sel_order,
-                     **(dict(block_m2=bmd, out2=ts_d) if bmd != bm else {}))
+        ops.pack(ids, E, out=packed, workspace=ws.pack_ws,
+                 schedule=(ws.sel_all, bm, ws.sel_order, ws.tile_start) + ((bmd, ts_d) if bmd != bm else ()))
         if ev is not None:
             ev[0].record(stream)
         ops.swiglu_grouped_gateup(x, packed.perm_token, packed.offsets, ws.sel_order, ws.tile_start, max_tiles, bm,

@@ -131,6 +131,18 @@ int pdscope_schedule_balanced(const int32_t *counts, const int32_t *sel, int nse
 int pdscope_schedule_balanced_pair(const int32_t *counts, const int32_t *sel, int nsel, int block_m, int block_m2,
                                    int32_t *order, int32_t *tile_start, int32_t *tile_start2, void *stream);
 
+/*
+ * pdscope_pack followed by the balanced schedule of `sel` over the counts it
+ * produces (pdscope_schedule_balanced, or _pair when block_m2 != 0 with
+ * tile_start2), computed inside the pack launch by a block that already holds
+ * the counts, so the schedule costs no launch of its own.  Outputs as the two
+ * calls give them.  No counterpart in the reference.
+ */
+int pdscope_pack_schedule_balanced(const int32_t *ids, int T, int k, int E, int32_t *counts, int32_t *offsets,
+                                   int32_t *perm_token, int32_t *perm_pos, int32_t *row_of, void *workspace,
+                                   const int32_t *sel, int nsel, int block_m, int block_m2, int32_t *order,
+                                   int32_t *tile_start, int32_t *tile_start2, void *stream);
+
 /* Row tile (32, 64, 128, 256 or 384) for `rows_hint` average rows per
  * selected expert: <= 16 rows 32, <= 64 rows 64, <= 124 rows 128, <= 192 rows
  * 256, <= 320 rows 384 (one tile holds a typical expert, so its weights

@@ -30,6 +30,8 @@ SIGNATURES = {
     "pdscope_schedule": ([_vp, _vp, _i32, _i32, _vp, _vp], _i32),
     "pdscope_schedule_balanced": ([_vp, _vp, _i32, _i32, _vp, _vp, _vp], _i32),
     "pdscope_schedule_balanced_pair": ([_vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp], _i32),
+    "pdscope_pack_schedule_balanced": ([_vp, _i32, _i32, _i32] + [_vp] * 6 + [_vp, _i32, _i32, _i32] + [_vp] * 4,
+                                       _i32),
     "pdscope_grouped_block_m": ([_i32], _i32),
     "pdscope_grouped_block_m_max": ([_i32, _i32], _i32),
     "pdscope_swiglu_grouped": ([_vp, _vp, _vp, _vp, _i32, _vp, _i32, _i32, _vp, _i32, _i32, _vp, _vp, _vp], _i32),

@@ -47,6 +47,54 @@ __device__ int block_scan256(int v, int *s_wsum) {
     return v + add;
 }
 
+// The balanced order and tile prefixes, computed by threads 0..255 of the
+// calling block (every thread of the block must call it: it synchronises).
+// rows[e]: rows of expert e (global or LDS); s_rows / s_at: 256 ints of LDS
+// each (s_rows 16-byte aligned), s_wsum: 4 ints.
+__device__ void balanced_schedule(const int32_t *rows, const int32_t *__restrict__ sel, int nsel, int bm,
+                                  int32_t *__restrict__ order, int32_t *__restrict__ tile_start, int bm2,
+                                  int32_t *__restrict__ tile_start2, int *s_rows, int *s_at, int *s_wsum) {
+    const int i = threadIdx.x;
+    if (i < 256) s_rows[i] = i < nsel ? rows[sel[i]] : -1;  // -1 past nsel: never ranks above a real expert
+    __syncthreads();
+    if (i < nsel) {
+        const int c = s_rows[i];
+        int r = 0;
+        // four rows per LDS read (broadcast)
+        for (int j = 0; j < nsel; j += 4) {
+            const int4 q = *reinterpret_cast<const int4 *>(s_rows + j);
+            r += (q.x > c) | ((q.x == c) & (j < i));
+            r += (q.y > c) | ((q.y == c) & (j + 1 < i));
+            r += (q.z > c) | ((q.z == c) & (j + 2 < i));
+            r += (q.w > c) | ((q.w == c) & (j + 3 < i));
+        }
+        const int full = nsel >> 3, rem = nsel & 7;
+        const int rd = r >> 3, w = r & 7;
+        const int g = (rd & 1) ? 7 - w : w;
+        // groups before g: `full` members each, plus one if the last (partial)
+        // round reaches them (round `full` deals to 0.. upward when even, 7.. downward when odd)
+        int before = g * full;
+        if (rem) before += (full & 1) ? max(0, g - (8 - rem)) : min(g, rem);
+        s_at[before + rd] = i;
+    }
+    __syncthreads();
+    int tiles = 0, tiles2 = 0;
+    if (i < nsel) {
+        const int si = s_at[i];
+        order[i] = sel[si];
+        tiles = (s_rows[si] + bm - 1) / bm;
+        if (tile_start2) tiles2 = (s_rows[si] + bm2 - 1) / bm2;
+    }
+    const int incl = block_scan256(tiles, s_wsum);
+    if (i == 0) tile_start[0] = 0;
+    if (i < nsel) tile_start[i + 1] = incl;
+    if (tile_start2) {  // uniform: the whole block takes this branch
+        const int incl2 = block_scan256(tiles2, s_wsum);
+        if (i == 0) tile_start2[0] = 0;
+        if (i < nsel) tile_start2[i + 1] = incl2;
+    }
+}
+
 constexpr int kPackRC = 32;  // 64-id chunks per wave held in registers
 
 // Load up to kPackRC chunks of the wave's segment (expert id, or -1 outside
@@ -72,11 +120,30 @@ __device__ __forceinline__ void pack_load(const int32_t *__restrict__ ids, int T
     }
 }
 
+// Balanced schedule requested together with a pack (order == nullptr: none).
+struct PackSchedule {
+    const int32_t *sel;
+    int nsel, bm, bm2;
+    int32_t *order, *tile_start, *tile_start2;
+};
+
+// The schedule from the per-expert totals `tot` held by threads e < E.
+__device__ void pack_then_schedule(const PackSchedule &ps, int E, int tot) {
+    __shared__ __align__(16) int s_tot[kPackMaxE];
+    __shared__ __align__(16) int s_rows[256];
+    __shared__ int s_at[256];
+    __shared__ int s_ws2[4];
+    if (threadIdx.x < E) s_tot[threadIdx.x] = tot;
+    __syncthreads();
+    balanced_schedule(s_tot, ps.sel, ps.nsel, ps.bm, ps.order, ps.tile_start, ps.bm2, ps.tile_start2, s_rows, s_at,
+                      s_ws2);
+}
+
 __global__ __launch_bounds__(1024) void pack_kernel(const int32_t *__restrict__ ids, int T, int k, int E,
                                                     int32_t *__restrict__ counts, int32_t *__restrict__ offsets,
                                                     int32_t *__restrict__ perm_token,
                                                     int32_t *__restrict__ perm_pos,
-                                                    int32_t *__restrict__ row_of) {
+                                                    int32_t *__restrict__ row_of, PackSchedule ps) {
     __shared__ int32_t s_cnt[kPackWaves][kPackMaxE];
     __shared__ int s_wsum[4];
     const int n = T * k;
@@ -117,6 +184,7 @@ __global__ __launch_bounds__(1024) void pack_kernel(const int32_t *__restrict__ 
             run += c;
         }
     }
+    if (ps.order) pack_then_schedule(ps, E, tot);  // uniform over the block
     __syncthreads();
     // pass 2: stable scatter
     for (int sc = beg; sc < end; sc += kPackRC * 64) {
@@ -208,7 +276,7 @@ __global__ __launch_bounds__(1024) void pack_scatter_kernel(const int32_t *__res
                                                             int32_t *__restrict__ offsets,
                                                             int32_t *__restrict__ perm_token,
                                                             int32_t *__restrict__ perm_pos,
-                                                            int32_t *__restrict__ row_of) {
+                                                            int32_t *__restrict__ row_of, PackSchedule ps) {
     __shared__ int32_t s_cnt[kPackWaves][kPackMaxE];
     __shared__ int s_wsum[4];
     const int n = T * k;
@@ -245,6 +313,8 @@ __global__ __launch_bounds__(1024) void pack_scatter_kernel(const int32_t *__res
             run += c;
         }
     }
+    // every block holds the totals; the last one (the shortest chunk) schedules
+    if (ps.order && (int)blockIdx.x == nchunk - 1) pack_then_schedule(ps, E, tot);
     __syncthreads();
 #pragma unroll
     for (int c = 0; c < kChunkRC; ++c) {
@@ -299,48 +369,10 @@ __global__ __launch_bounds__(256) void schedule_balanced_kernel(const int32_t *_
                                                                 int32_t *__restrict__ order,
                                                                 int32_t *__restrict__ tile_start, int bm2,
                                                                 int32_t *__restrict__ tile_start2) {
-    __shared__ __align__(16) int s_rows[256];  // -1 past nsel: never ranks above a real expert
+    __shared__ __align__(16) int s_rows[256];
     __shared__ int s_at[256];  // list position -> sel position
     __shared__ int s_wsum[4];
-    const int i = threadIdx.x;
-    s_rows[i] = i < nsel ? counts[sel[i]] : -1;
-    __syncthreads();
-    if (i < nsel) {
-        const int c = s_rows[i];
-        int r = 0;
-        // four rows per LDS read (broadcast)
-        for (int j = 0; j < nsel; j += 4) {
-            const int4 q = *reinterpret_cast<const int4 *>(s_rows + j);
-            r += (q.x > c) | ((q.x == c) & (j < i));
-            r += (q.y > c) | ((q.y == c) & (j + 1 < i));
-            r += (q.z > c) | ((q.z == c) & (j + 2 < i));
-            r += (q.w > c) | ((q.w == c) & (j + 3 < i));
-        }
-        const int full = nsel >> 3, rem = nsel & 7;
-        const int rd = r >> 3, w = r & 7;
-        const int g = (rd & 1) ? 7 - w : w;
-        // groups before g: `full` members each, plus one if the last (partial)
-        // round reaches them (round `full` deals to 0.. upward when even, 7.. downward when odd)
-        int before = g * full;
-        if (rem) before += (full & 1) ? max(0, g - (8 - rem)) : min(g, rem);
-        s_at[before + rd] = i;
-    }
-    __syncthreads();
-    int tiles = 0, tiles2 = 0;
-    if (i < nsel) {
-        const int si = s_at[i];
-        order[i] = sel[si];
-        tiles = (s_rows[si] + bm - 1) / bm;
-        if (tile_start2) tiles2 = (s_rows[si] + bm2 - 1) / bm2;
-    }
-    const int incl = block_scan256(tiles, s_wsum);
-    if (i == 0) tile_start[0] = 0;
-    if (i < nsel) tile_start[i + 1] = incl;
-    if (tile_start2) {  // uniform: the whole block takes this branch
-        const int incl2 = block_scan256(tiles2, s_wsum);
-        if (i == 0) tile_start2[0] = 0;
-        if (i < nsel) tile_start2[i + 1] = incl2;
-    }
+    balanced_schedule(counts, sel, nsel, bm, order, tile_start, bm2, tile_start2, s_rows, s_at, s_wsum);
 }
 
 }  // namespace pd
@@ -357,8 +389,9 @@ PD_API size_t pdscope_pack_workspace_size(int T, int k, int E) {
     return (size_t)((n + kChunkIds - 1) / kChunkIds) * (size_t)E * sizeof(int32_t);
 }
 
-PD_API int pdscope_pack(const int32_t *ids, int T, int k, int E, int32_t *counts, int32_t *offsets,
-                        int32_t *perm_token, int32_t *perm_pos, int32_t *row_of, void *workspace, void *stream) {
+static int pack_launch(const int32_t *ids, int T, int k, int E, int32_t *counts, int32_t *offsets,
+                       int32_t *perm_token, int32_t *perm_pos, int32_t *row_of, void *workspace, PackSchedule ps,
+                       void *stream) {
     if (!ids || !counts || !offsets || !perm_token || !perm_pos || !row_of)
         return fail(kEInval, "pack: null pointer");
     if (T < 1 || k < 1 || E < 1 || E > kPackMaxE) return fail(kEInval, "pack: need T,k >= 1 and 1 <= E <= 256");
@@ -366,7 +399,7 @@ PD_API int pdscope_pack(const int32_t *ids, int T, int k, int E, int32_t *counts
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int n = T * k;
     if (n <= kPackMultiMin) {
-        pack_kernel<<<1, 1024, 0, s>>>(ids, T, k, E, counts, offsets, perm_token, perm_pos, row_of);
+        pack_kernel<<<1, 1024, 0, s>>>(ids, T, k, E, counts, offsets, perm_token, perm_pos, row_of, ps);
         return check_launch("pack_kernel");
     }
     if (!workspace) return fail(kEInval, "pack: T*k above the single-block size needs pdscope_pack_workspace_size bytes");
@@ -376,8 +409,28 @@ PD_API int pdscope_pack(const int32_t *ids, int T, int k, int E, int32_t *counts
     int rc = check_launch("pack_count_kernel");
     if (rc) return rc;
     pack_scatter_kernel<<<nchunk, 1024, 0, s>>>(ids, T, k, E, hist, nchunk, counts, offsets, perm_token, perm_pos,
-                                                row_of);
+                                                row_of, ps);
     return check_launch("pack_scatter_kernel");
+}
+
+PD_API int pdscope_pack(const int32_t *ids, int T, int k, int E, int32_t *counts, int32_t *offsets,
+                        int32_t *perm_token, int32_t *perm_pos, int32_t *row_of, void *workspace, void *stream) {
+    return pack_launch(ids, T, k, E, counts, offsets, perm_token, perm_pos, row_of, workspace,
+                       PackSchedule{nullptr, 0, 0, 0, nullptr, nullptr, nullptr}, stream);
+}
+
+PD_API int pdscope_pack_schedule_balanced(const int32_t *ids, int T, int k, int E, int32_t *counts,
+                                          int32_t *offsets, int32_t *perm_token, int32_t *perm_pos,
+                                          int32_t *row_of, void *workspace, const int32_t *sel, int nsel,
+                                          int block_m, int block_m2, int32_t *order, int32_t *tile_start,
+                                          int32_t *tile_start2, void *stream) {
+    if (!sel || !order || !tile_start || nsel < 0 || nsel > 256 || (block_m2 != 0) != (tile_start2 != nullptr))
+        return fail(kEInval, "pack_schedule_balanced: bad schedule arguments (nsel 0..256; block_m2 with tile_start2)");
+    for (int b : {block_m, block_m2 ? block_m2 : block_m})
+        if (b != 32 && b != 64 && b != 128 && b != 256 && b != 384)
+            return fail(kEInval, "pack_schedule_balanced: block sizes must be 32, 64, 128, 256 or 384");
+    return pack_launch(ids, T, k, E, counts, offsets, perm_token, perm_pos, row_of, workspace,
+                       PackSchedule{sel, nsel, block_m, block_m2, order, tile_start, tile_start2}, stream);
 }
 
 // ---------------------------------------------------------------- no-allocation variant

@@ -139,11 +139,13 @@ def experts_resident(x, ids, weights, slots, ws: MoEWorkspace, out=None, *, bloc
         ops.swiglu_decode(x, ids, weights, slots, H, I, ws.h_ws, out, merge=merge)
         return out
     _, _, _, packed = ws.views(T)
-    ops.pack(ids, E, out=packed, workspace=ws.pack_ws)
     bm = block_m or ops.grouped_block_m((T * k) // E)
     bmd = down_block_m(bm, H, I)
+    # the balanced schedule of all experts comes out of the pack launch
+    sched = (ws.sel_all, bm, ws.sel_order, ws.tile_start) + ((bmd, ws.tile_start_down) if bmd != bm else ())
+    ops.pack(ids, E, out=packed, workspace=ws.pack_ws, schedule=sched)
     grouped_ffn(x, packed, ws.sel_all, bm, (T * k + bm - 1) // bm + E, slots, ws,
-                max_tiles_down=(T * k + bmd - 1) // bmd + E)
+                max_tiles_down=(T * k + bmd - 1) // bmd + E, scheduled=True)
     if before_merge is not None:
         before_merge()
     ops.merge(ws.y, packed.row_of, weights, out, add_in=add_in, mode=merge)
@@ -159,23 +161,28 @@ def down_block_m(bm: int, H: int, I: int) -> int:
     return 256 if bm == 384 and H % 256 == 0 and I % 128 == 0 else bm
 
 
-def grouped_ffn(x, packed, sel, bm, max_tiles, slots, ws: MoEWorkspace, *, max_tiles_down, perm=None):
+def grouped_ffn(x, packed, sel, bm, max_tiles, slots, ws: MoEWorkspace, *, max_tiles_down, perm=None,
+                scheduled=False):
     """Grouped SwiGLU over the experts in `sel` (int32 device): gate/up on
     bm-row tiles into ws.h_ws, down on down_block_m(bm, H, I)-row tiles into ws.y.
     max_tiles / max_tiles_down bound the two launches' tile counts.  perm
-    (default packed.perm_token) maps grouped rows to rows of x."""
+    (default packed.perm_token) maps grouped rows to rows of x.  scheduled:
+    ws.sel_order / ws.tile_start (/ ws.tile_start_down) already hold the
+    balanced schedule of `sel` (written by the pack launch)."""
     H, I = ws.H, ws.I
     perm = packed.perm_token if perm is None else perm
     nsel = sel.numel()
     tile_start, order = ws.tile_start[:nsel + 1], ws.sel_order[:nsel]
     bmd = down_block_m(bm, H, I)
     if bmd == bm:
-        ops.schedule(packed.counts, sel, bm, out=tile_start, order=order)
+        if not scheduled:
+            ops.schedule(packed.counts, sel, bm, out=tile_start, order=order)
         ops.swiglu_grouped(x, perm, packed.offsets, order, tile_start, max_tiles, bm, slots, H, I, ws.h_ws, ws.y)
         return
     # one launch schedules both: the balanced order depends on the rows only
     tile_down = ws.tile_start_down[:nsel + 1]
-    ops.schedule(packed.counts, sel, bm, out=tile_start, order=order, block_m2=bmd, out2=tile_down)
+    if not scheduled:
+        ops.schedule(packed.counts, sel, bm, out=tile_start, order=order, block_m2=bmd, out2=tile_down)
     ops.swiglu_grouped_gateup(x, perm, packed.offsets, order, tile_start, max_tiles, bm, slots, H, I, ws.h_ws)
     ops.swiglu_grouped_down(ws.h_ws, packed.offsets, order, tile_down, max_tiles_down, bmd, slots, H, I, ws.y)
 

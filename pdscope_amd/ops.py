@@ -125,7 +125,11 @@ def pack_workspace_size(T: int, k: int, E: int) -> int:
     return int(_lib.load().pdscope_pack_workspace_size(int(T), int(k), int(E)))
 
 
-def pack(ids, E, out: Packed | None = None, workspace=None) -> Packed:
+def pack(ids, E, out: Packed | None = None, workspace=None, *, schedule=None) -> Packed:
+    """K2 grouping.  schedule=(sel, block_m, order, tile_start[, block_m2,
+    tile_start2]) also writes the balanced schedule of `sel` over the
+    resulting counts (as schedule(..., order=...)) from inside the pack
+    launch (pdscope_pack_schedule_balanced)."""
     _need(ids, "ids", torch.int32, 2)
     T, k = ids.shape
     dev = ids.device
@@ -137,8 +141,23 @@ def pack(ids, E, out: Packed | None = None, workspace=None) -> Packed:
     need = pack_workspace_size(T, k, E)
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = torch.empty(need, dtype=torch.uint8, device=dev)
-    _lib.call("pdscope_pack", _p(ids), T, k, E, _p(out.counts), _p(out.offsets), _p(out.perm_token),
-              _p(out.perm_pos), _p(out.row_of), _p(workspace) if need else None, _stream(dev))
+    args = (_p(ids), T, k, E, _p(out.counts), _p(out.offsets), _p(out.perm_token), _p(out.perm_pos), _p(out.row_of),
+            _p(workspace) if need else None)
+    if schedule is None:
+        _lib.call("pdscope_pack", *args, _stream(dev))
+        return out
+    sel, block_m, order, tile_start, *second = schedule
+    block_m2, tile_start2 = second if second else (0, None)
+    for t, name, size in ((sel, "sel", 0), (order, "order", sel.numel()), (tile_start, "tile_start", sel.numel() + 1)):
+        _need(t, name, torch.int32, 1, dev)
+        if t.numel() < size:
+            raise ValueError(f"{name} smaller than sel needs")
+    if tile_start2 is not None:
+        _need(tile_start2, "tile_start2", torch.int32, 1, dev)
+        if tile_start2.numel() < sel.numel() + 1:
+            raise ValueError("tile_start2 smaller than sel needs")
+    _lib.call("pdscope_pack_schedule_balanced", *args, _p(sel), sel.numel(), block_m, block_m2, _p(order),
+              _p(tile_start), _p(tile_start2), _stream(dev))
     return out
 
 

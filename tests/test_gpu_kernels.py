@@ -399,6 +399,39 @@ def test_schedule_balanced_pair_equals_two_schedules(pd, nsel, bm, bm2):
         ops.schedule(counts, sel, bm, out=out1, block_m2=bm2, out2=out2)
 
 
+@pytest.mark.parametrize("T,k,E,nsel,bm,bm2", [(5, 8, 128, 128, 64, 0), (256, 8, 128, 128, 64, 0),
+                                                (512, 8, 128, 128, 64, 0), (4096, 8, 128, 128, 384, 256),
+                                                (1304, 6, 64, 40, 128, 0), (3000, 8, 256, 256, 256, 32),
+                                                (700, 4, 32, 17, 32, 384)])
+def test_pack_with_schedule_equals_pack_then_schedule(pd, T, k, E, nsel, bm, bm2):
+    """pdscope_pack_schedule_balanced: the grouping bit-exact with
+    pdscope_pack and the order / tile prefixes with pdscope_schedule_balanced
+    (_pair) over the counts it produced, on the single-block (T*k <= 2048)
+    and multi-block paths, over all experts and over subsets."""
+    ops, layer, synthetic = pd
+    g = torch.Generator().manual_seed(T * 7 + E + nsel)
+    ids = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)]).to(torch.int32).to(DEV)
+    sel = torch.tensor(sorted(torch.randperm(E, generator=g)[:nsel].tolist()), dtype=torch.int32, device=DEV)
+    ref = ops.pack(ids, E)
+    o1 = torch.empty(nsel, dtype=torch.int32, device=DEV)
+    t1 = torch.empty(nsel + 1, dtype=torch.int32, device=DEV)
+    t2 = torch.empty(nsel + 1, dtype=torch.int32, device=DEV)
+    if bm2:
+        ops.schedule(ref.counts, sel, bm, out=t1, order=o1, block_m2=bm2, out2=t2)
+    else:
+        ops.schedule(ref.counts, sel, bm, out=t1, order=o1)
+    order = torch.full((nsel,), -1, dtype=torch.int32, device=DEV)
+    ts = torch.full((nsel + 1,), -1, dtype=torch.int32, device=DEV)
+    ts2 = torch.full((nsel + 1,), -1, dtype=torch.int32, device=DEV)
+    got = ops.pack(ids, E, schedule=(sel, bm, order, ts) + ((bm2, ts2) if bm2 else ()))
+    torch.cuda.synchronize()
+    for name in ("counts", "offsets", "perm_token", "perm_pos", "row_of"):
+        assert torch.equal(getattr(got, name), getattr(ref, name)), name
+    assert torch.equal(order, o1) and torch.equal(ts, t1)
+    if bm2:
+        assert torch.equal(ts2, t2)
+
+
 def test_decode_qwen(orc, pd, qwen, qwen_host):
     ops, layer, synthetic = pd
     ws = layer.MoEWorkspace(1, 2048, 768, 128, 8, DEV)
