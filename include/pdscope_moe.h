@@ -134,9 +134,10 @@ int pdscope_schedule_balanced_pair(const int32_t *counts, const int32_t *sel, in
 /*
  * pdscope_pack followed by the balanced schedule of `sel` over the counts it
  * produces (pdscope_schedule_balanced, or _pair when block_m2 != 0 with
- * tile_start2), computed inside the pack launch by a block that already holds
- * the counts, so the schedule costs no launch of its own.  Outputs as the two
- * calls give them.  No counterpart in the reference.
+ * tile_start2), computed inside the pack launch by one extra workgroup (it
+ * counts the ids itself, or sums the per-chunk counts of the multi-block path)
+ * beside the scatter, so the schedule costs no launch of its own.  Outputs as
+ * the two calls give them.  No counterpart in the reference.
  */
 int pdscope_pack_schedule_balanced(const int32_t *ids, int T, int k, int E, int32_t *counts, int32_t *offsets,
                                    int32_t *perm_token, int32_t *perm_pos, int32_t *row_of, void *workspace,

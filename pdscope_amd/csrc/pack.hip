@@ -95,7 +95,10 @@ __device__ void balanced_schedule(const int32_t *rows, const int32_t *__restrict
     }
 }
 
-constexpr int kPackRC = 32;  // 64-id chunks per wave held in registers
+// 64-id chunks per wave held in registers: the single-workgroup kernel runs up
+// to 2048 ids (two chunks per wave, one pass); loading more chunks than a
+// wave's segment holds cost 2.7-6 us per call at T*k = 512..2048
+constexpr int kPackRC = 2;
 
 // Load up to kPackRC chunks of the wave's segment (expert id, or -1 outside
 // the segment / outside [0, E)) with every load in flight at once.
@@ -171,6 +174,12 @@ __global__ __launch_bounds__(1024) void pack_kernel(const int32_t *__restrict__ 
     int tot = 0;
     if (threadIdx.x < E)
         for (int w = 0; w < kPackWaves; ++w) tot += s_cnt[w][threadIdx.x];
+    // a second workgroup (launched with a schedule only) counts as well and
+    // writes the schedule while the first scatters
+    if (blockIdx.x == 1) {
+        pack_then_schedule(ps, E, tot);
+        return;
+    }
     const int incl = block_scan256(threadIdx.x < 256 ? tot : 0, s_wsum);
     if (threadIdx.x < E) {
         const int e = threadIdx.x;
@@ -184,7 +193,6 @@ __global__ __launch_bounds__(1024) void pack_kernel(const int32_t *__restrict__ 
             run += c;
         }
     }
-    if (ps.order) pack_then_schedule(ps, E, tot);  // uniform over the block
     __syncthreads();
     // pass 2: stable scatter
     for (int sc = beg; sc < end; sc += kPackRC * 64) {
@@ -279,6 +287,15 @@ __global__ __launch_bounds__(1024) void pack_scatter_kernel(const int32_t *__res
                                                             int32_t *__restrict__ row_of, PackSchedule ps) {
     __shared__ int32_t s_cnt[kPackWaves][kPackMaxE];
     __shared__ int s_wsum[4];
+    if ((int)blockIdx.x == nchunk) {
+        // the extra workgroup of a launch with a schedule: totals from the
+        // per-chunk counts, then the schedule, beside the scatter
+        int tot = 0;
+        if (threadIdx.x < E)
+            for (int b = 0; b < nchunk; ++b) tot += hist[(size_t)b * E + threadIdx.x];
+        pack_then_schedule(ps, E, tot);
+        return;
+    }
     const int n = T * k;
     const int wave = threadIdx.x >> 6, lane = lane_id();
     const int beg = min((int)blockIdx.x * kChunkIds + wave * 64 * kChunkRC, n);
@@ -313,8 +330,6 @@ __global__ __launch_bounds__(1024) void pack_scatter_kernel(const int32_t *__res
             run += c;
         }
     }
-    // every block holds the totals; the last one (the shortest chunk) schedules
-    if (ps.order && (int)blockIdx.x == nchunk - 1) pack_then_schedule(ps, E, tot);
     __syncthreads();
 #pragma unroll
     for (int c = 0; c < kChunkRC; ++c) {
@@ -399,7 +414,7 @@ static int pack_launch(const int32_t *ids, int T, int k, int E, int32_t *counts,
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int n = T * k;
     if (n <= kPackMultiMin) {
-        pack_kernel<<<1, 1024, 0, s>>>(ids, T, k, E, counts, offsets, perm_token, perm_pos, row_of, ps);
+        pack_kernel<<<ps.order ? 2 : 1, 1024, 0, s>>>(ids, T, k, E, counts, offsets, perm_token, perm_pos, row_of, ps);
         return check_launch("pack_kernel");
     }
     if (!workspace) return fail(kEInval, "pack: T*k above the single-block size needs pdscope_pack_workspace_size bytes");
@@ -408,7 +423,7 @@ static int pack_launch(const int32_t *ids, int T, int k, int E, int32_t *counts,
     pack_count_kernel<<<nchunk, 1024, 0, s>>>(ids, T, k, E, hist);
     int rc = check_launch("pack_count_kernel");
     if (rc) return rc;
-    pack_scatter_kernel<<<nchunk, 1024, 0, s>>>(ids, T, k, E, hist, nchunk, counts, offsets, perm_token, perm_pos,
+    pack_scatter_kernel<<<nchunk + (ps.order ? 1 : 0), 1024, 0, s>>>(ids, T, k, E, hist, nchunk, counts, offsets, perm_token, perm_pos,
                                                 row_of, ps);
     return check_launch("pack_scatter_kernel");
 }
