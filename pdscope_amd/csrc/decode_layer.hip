@@ -204,6 +204,8 @@ __global__ __launch_bounds__(256, 2) void decode_layer_kernel(
     __shared__ float s_y[kDecodeMaxK * 4];
     __shared__ const uint16_t *s_slot[kDecodeMaxE];
     __shared__ TopkScratch s_tk;
+    __shared__ TopkScratch s_tk2;  // the exact routing when the logit-key one fails its check
+    __shared__ int s_redo;
     __shared__ uint32_t s_epoch;
 
     const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
@@ -295,58 +297,117 @@ __global__ __launch_bounds__(256, 2) void decode_layer_kernel(
         }
     }
     __syncthreads();
+    // Without a logit bias the experts are picked first by their bf16 logits
+    // (topk_by_logit_keys: the rows below start streaming ~0.5 us earlier),
+    // and wave 0 checks the pick against the probabilities while its rows
+    // stream; when the check fails (distinct logits with equal
+    // probabilities), the exact routing is computed and the rows whose
+    // expert it changes are computed again before h is published.
+    const bool pub = blockIdx.x == 0;
+    const bool by_keys = bias == nullptr;
+    int rk[4];
     if (wave == 0) {
-        const bool pub = blockIdx.x == 0;
-        if (E <= 128)
+        if (by_keys) {
+            if (E <= 128)
+                topk_by_logit_keys<2>(s_logit, E, k, &s_tk, rk);
+            else
+                topk_by_logit_keys<4>(s_logit, E, k, &s_tk, rk);
+        } else if (E <= 128) {
             topk_token<2>(s_logit, bias, E, k, normalize, 0, pub ? ids : nullptr, pub ? weights : nullptr,
                           pub ? probs : nullptr, &s_tk);
-        else
+        } else {
             topk_token<4>(s_logit, bias, E, k, normalize, 0, pub ? ids : nullptr, pub ? weights : nullptr,
                           pub ? probs : nullptr, &s_tk);
+        }
     }
     __syncthreads();
 
     // ---- 3. the gate/up rows this wave computes
     uint4 gv[P][NCH], uv[P][NCH];
     bool has[P];
+    auto issue_rows = [&](const TopkScratch &tk) __attribute__((always_inline)) {
 #pragma unroll
-    for (int p = 0; p < P; ++p) {
-        const int q = min(q0 + p, KI - 1);
-        const int sl = q / I, i = q - sl * I;
-        const uint16_t *base = s_slot[s_tk.seli[sl]];
-        // an expert without a ready copy reads the activation row instead
-        // (H elements, in bounds) and contributes h = 0
-        has[p] = base != nullptr;
-        const uint16_t *grow = base ? base + (size_t)i * H : x;
-        const uint16_t *urow = base ? base + (size_t)(I + i) * H : x;
+        for (int p = 0; p < P; ++p) {
+            const int q = min(q0 + p, KI - 1);
+            const int sl = q / I, i = q - sl * I;
+            const uint16_t *base = s_slot[tk.seli[sl]];
+            // an expert without a ready copy reads the activation row instead
+            // (H elements, in bounds) and contributes h = 0
+            has[p] = base != nullptr;
+            const uint16_t *grow = base ? base + (size_t)i * H : x;
+            const uint16_t *urow = base ? base + (size_t)(I + i) * H : x;
 #pragma unroll
-        for (int j = 0; j < NCH; ++j) {
-            gv[p][j] = ld_nt(grow + 8 * min(lane + 64 * j, C - 1));
-            uv[p][j] = ld_nt(urow + 8 * min(lane + 64 * j, C - 1));
+            for (int j = 0; j < NCH; ++j) {
+                gv[p][j] = ld_nt(grow + 8 * min(lane + 64 * j, C - 1));
+                uv[p][j] = ld_nt(urow + 8 * min(lane + 64 * j, C - 1));
+            }
         }
+    };
+    // ---- 4. gate/up -> h
+    // h = bf16(silu(bf16(g)) * bf16(u)), lane 0 for the wave's P rows.  (One
+    // lane per row would publish earlier, but then the down rows below start
+    // earlier too and slow the blocks whose gate/up rows are still streaming:
+    // the last block's h, which every block waits for, comes later.)
+    auto finish_rows = [&]() __attribute__((always_inline)) {
+        float g[P], u[P];
+        gate_up_dots<P, NCH>(gv, uv, xv, C, lane, g, u);
+        if (lane == 0) {
+#pragma unroll
+            for (int p = 0; p < P; ++p) {
+                const float a = bf16_round(silu_f32(bf16_round(g[p])));
+                const uint32_t hb = has[p] ? f2bf(a * bf16_round(u[p])) : 0u;
+                s_pub[wave * P + p] = (epoch << 16) | hb;
+            }
+        }
+    };
+    issue_rows(s_tk);
+    if (wave == 0) {
+        bool exact = true;
+        if (by_keys) {
+            exact = E <= 128 ? topk_verify_finish<2>(s_logit, E, k, normalize, 0, pub ? ids : nullptr,
+                                                     pub ? weights : nullptr, pub ? probs : nullptr, &s_tk, rk)
+                             : topk_verify_finish<4>(s_logit, E, k, normalize, 0, pub ? ids : nullptr,
+                                                     pub ? weights : nullptr, pub ? probs : nullptr, &s_tk, rk);
+            if (!exact) {
+                if (E <= 128)
+                    topk_token<2>(s_logit, nullptr, E, k, normalize, 0, pub ? ids : nullptr, pub ? weights : nullptr,
+                                  pub ? probs : nullptr, &s_tk2);
+                else
+                    topk_token<4>(s_logit, nullptr, E, k, normalize, 0, pub ? ids : nullptr, pub ? weights : nullptr,
+                                  pub ? probs : nullptr, &s_tk2);
+            }
+        }
+        if (lane == 0) s_redo = exact ? 0 : 1;
     }
     if (has_resid && !add_now) {
 #pragma unroll
         for (int j = 0; j < NCH; ++j) xv[j] = add_bf16x8(xv[j], rv[j]);
     }
-    // ---- 4. gate/up -> h
-    float g[P], u[P];
-    gate_up_dots<P, NCH>(gv, uv, xv, C, lane, g, u);
-    // h = bf16(silu(bf16(g)) * bf16(u)), lane 0 for the wave's P rows.  (One
-    // lane per row would publish earlier, but then the down rows below start
-    // earlier too and slow the blocks whose gate/up rows are still streaming:
-    // the last block's h, which every block waits for, comes later.)
-    if (lane == 0) {
+    finish_rows();
+    __syncthreads();
+    if (s_redo) {
+        // the exact routing replaces the logit-key pick: rows of a changed
+        // slot are loaded and computed again (block-uniform branch)
+        bool changed = false;
 #pragma unroll
         for (int p = 0; p < P; ++p) {
-            const float a = bf16_round(silu_f32(bf16_round(g[p])));
-            const uint32_t hb = has[p] ? f2bf(a * bf16_round(u[p])) : 0u;
-            s_pub[wave * P + p] = (epoch << 16) | hb;
+            const int sl = min(q0 + p, KI - 1) / I;
+            changed |= s_tk2.seli[sl] != s_tk.seli[sl];
         }
+        if (changed) {
+            issue_rows(s_tk2);
+            finish_rows();
+        }
+        __syncthreads();
+        if (tid < k) {
+            s_tk.seli[tid] = s_tk2.seli[tid];
+            s_tk.selp[tid] = s_tk2.selp[tid];
+            s_tk.selw[tid] = s_tk2.selw[tid];
+        }
+        __syncthreads();
     }
     // the block's 4P words go out as 8-byte writes by the last wave's first
     // 2P threads
-    __syncthreads();
     if (tid >= kPublisher && tid < kPublisher + 2 * P) {
         const int t2 = tid - kPublisher;
         const int qb = blockIdx.x * 4 * P + 2 * t2;

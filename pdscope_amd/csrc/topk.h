@@ -144,6 +144,113 @@ __device__ __forceinline__ void topk_token(const float *lrow, const float *__res
     wave_lds_sync();
 }
 
+// Order-preserving key of a bf16 logit (held as fp32) and its expert id:
+// larger logit first, equal logits lower id first; keys of distinct experts
+// differ.  The bf16 bits map to an unsigned order (sign set: complement;
+// else set the sign), the id fills the low half as 0xffff - e, and the top
+// bit flips so signed integer order is that unsigned order.
+__device__ __forceinline__ int logit_key(float v, int e) {
+    const uint32_t b = __float_as_uint(v) >> 16;
+    const uint32_t o = (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
+    return (int)(((o << 16) | (0xffffu - (uint32_t)e)) ^ 0x80000000u);
+}
+
+// First half of the two-step routing of one token by one wave (no logit
+// bias): the k experts of largest bf16 logit (equal logits: lower id) in
+// that order, by k rounds of a wave-wide max over unique keys (no ballot
+// per round), into sc->seli.  rank[j] receives the rank of expert
+// lane + 64 j, -1 if not taken.  The softmax is increasing in the logit, so
+// this is the probability top-k except where distinct logits give equal
+// probabilities; topk_verify_finish detects exactly those cases.
+template <int J>
+__device__ __forceinline__ void topk_by_logit_keys(const float *lrow, int E, int k, TopkScratch *sc,
+                                                   int (&rank)[4]) {
+    const int lane = lane_id();
+    int key[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int e = lane + 64 * j;
+        key[j] = e < E ? logit_key(lrow[e], e) : (int)0x80000000;
+        rank[j] = -1;
+    }
+    int myid = 0;
+    for (int r = 0; r < k; ++r) {
+        int lm = key[0];
+#pragma unroll
+        for (int j = 1; j < J; ++j) lm = max(lm, key[j]);
+        const int sel = 0xffff - (dpp_max_i32(lm) & 0xffff);
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+            if (lane + 64 * j == sel) {
+                key[j] = (int)0x80000000;
+                rank[j] = r;
+            }
+        if (lane == r) myid = sel;
+    }
+    if (lane < k) sc->seli[lane] = myid;
+    wave_lds_sync();
+}
+
+// Second half: the softmax (probs row t written when non-null), then a check
+// that sc->seli is the top-k of topk_token -- ranks descending in
+// (probability, -id), and the last one above every expert not taken in that
+// order.  If so, the probabilities and weights go to sc->selp / selw (and
+// ids / weights row t when non-null) with topk_token's arithmetic (the
+// renormalising sum in rank order) and it returns true; else it writes
+// nothing more and returns false, and the caller runs topk_token.
+template <int J>
+__device__ __forceinline__ bool topk_verify_finish(const float *lrow, int E, int k, int normalize, int t,
+                                                   int32_t *__restrict__ ids, uint16_t *__restrict__ weights,
+                                                   float *__restrict__ probs, TopkScratch *sc,
+                                                   const int (&rank)[4]) {
+#pragma clang fp contract(off)
+    const int lane = lane_id();
+    float p[J];
+    softmax_wave<J>(lrow, nullptr, E, t, probs, p);
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+        if (rank[j] >= 0) sc->selp[rank[j]] = p[j];
+    wave_lds_sync();
+    bool bad = false;
+    if (lane + 1 < k) {
+        const float a = sc->selp[lane], b = sc->selp[lane + 1];
+        bad = !(a > b || (a == b && sc->seli[lane] < sc->seli[lane + 1]));
+    }
+    // the largest probability not taken (bit patterns: p >= 0), -1 if none
+    int um = -1;
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+        if (lane + 64 * j < E && rank[j] < 0) um = max(um, (int)__float_as_uint(p[j]));
+    const int M = dpp_max_i32(um);
+    const int last = (int)__float_as_uint(sc->selp[k - 1]);
+    if (last < M) {
+        bad = true;
+    } else if (last == M) {
+        // the lowest expert id not taken with that probability must come after
+        int emin = 0x7fffffff;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const unsigned long long bm =
+                __ballot(lane + 64 * j < E && rank[j] < 0 && (int)__float_as_uint(p[j]) == M);
+            if (bm && emin == 0x7fffffff) emin = 64 * j + __ffsll(bm) - 1;
+        }
+        if (sc->seli[k - 1] > emin) bad = true;
+    }
+    if (__ballot(bad)) return false;
+    float denom = 0.0f;
+    if (normalize)
+        for (int r = 0; r < k; ++r) denom = denom + sc->selp[r];
+    if (lane < k) {
+        const float myp = sc->selp[lane];
+        const uint16_t wb = (uint16_t)f2bf(normalize ? myp / denom : myp);
+        sc->selw[lane] = wb;
+        if (ids) ids[(size_t)t * k + lane] = sc->seli[lane];
+        if (weights) weights[(size_t)t * k + lane] = wb;
+    }
+    wave_lds_sync();
+    return true;
+}
+
 // Block-level wrapper for one token: wave 0 routes, the block waits.  Must
 // be reached by the whole block; sc is then valid for every thread.
 template <int J>

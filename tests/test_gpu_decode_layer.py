@@ -113,6 +113,44 @@ def test_fused_matches_oracle_qwen(orc, pd):
     _assert_sync_clean(ops)
 
 
+@pytest.mark.parametrize("merge", ["fused", "reference"])
+def test_fused_routing_where_logit_order_and_probability_order_differ(orc, pd, merge):
+    """The fused kernel picks experts by their bf16 logits first and checks
+    the pick against the probabilities.  Here three experts get logits near
+    +5 and the others distinct logits far below (their probabilities
+    underflow to 0 and tie), so the probability top-k takes the five lowest
+    ids among the tied experts while the logit order would take the five
+    largest logits: the check must fail and the exact routing (and the rows
+    it changes) must win.  Ids and weights against the oracle, everything
+    bitwise against the three-launch path."""
+    ops, layer, synthetic = pd
+    H, I, E, k = 2048, 768, 128, 8
+    if not ops.decode_layer_supported(H, I, E, k, DEV):
+        pytest.skip("shape not resident on this device")
+    lay = synthetic.make_layer(H, I, E, k, True, seed=4242, device=DEV)
+    slots = ops.slot_table([lay.experts[e] for e in range(E)], DEV)
+    x = synthetic.make_tokens(1, H, seed=77, device=DEV)
+    xf = x.float()[0]
+    big = [101, 7, 64]
+    target = torch.tensor([-130.0 - (e * 37) % 97 for e in range(E)])
+    target[big] = torch.tensor([5.0, 4.5, 4.0])
+    gate = (target[:, None].to(DEV) * xf[None, :] / (xf @ xf)).to(torch.bfloat16).contiguous()
+    a = _three_launch(ops, x, gate, slots, I, k, True, merge=merge)
+    b = _fused(ops, x, gate, slots, I, k, True, merge=merge)
+    torch.cuda.synchronize()
+    for name, u, v in zip(("logits", "ids", "weights", "out"), a, b[:4]):
+        assert torch.equal(u.view(torch.int16) if u.dtype == torch.bfloat16 else u,
+                           v.view(torch.int16) if v.dtype == torch.bfloat16 else v), name
+    oi, ow = orc.route_from_logits(u16(b[0]), k, True, None)
+    assert np.array_equal(b[1].cpu().numpy(), oi) and np.array_equal(u16(b[2]), ow)
+    ids = b[1].cpu().numpy()[0].tolist()
+    assert ids[:3] == big
+    assert ids[3:] == [e for e in range(E) if e not in big][:5], ids
+    lg = u16(b[0])[0].astype(np.int32)
+    assert len(set(lg[[e for e in range(E) if e not in big]].tolist())) > 5, "the tied experts' logits must differ"
+    _assert_sync_clean(ops, H)
+
+
 def test_fused_zipf_bias_and_missing_copies(pd):
     """Router bias (Zipf workload) and slots without a ready copy (address 0 ->
     the expert contributes nothing) behave as on the three-launch path."""
