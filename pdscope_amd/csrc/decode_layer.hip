@@ -200,6 +200,7 @@ __global__ __launch_bounds__(256, 2) void decode_layer_kernel(
     uint16_t *__restrict__ out, uint32_t *ws) {
     extern __shared__ uint4 s_h[];       // k * I bf16
     __shared__ float s_logit[kDecodeMaxE];
+    __shared__ float s_plogit[CHAIN ? kDecodeMaxE : 1];  // the next layer's predictor logits (last block)
     __shared__ uint32_t s_pub[16];
     __shared__ float s_y[kDecodeMaxK * 4];
     __shared__ const uint16_t *s_slot[kDecodeMaxE];
@@ -442,6 +443,21 @@ __global__ __launch_bounds__(256, 2) void decode_layer_kernel(
     // ---- 5. collect h (the other waves), then down + merge
     if (tid < kPublisher)
         collect<8>(ws + kWsH, KI, tid, kPublisher, epoch, err, budget, reinterpret_cast<uint16_t *>(s_h));
+    // meanwhile the last block's publisher wave routes the next layer from
+    // the predictor logits (published early in the launch) into pred_out
+    if (CHAIN && next_gate && blockIdx.x == gridDim.x - 1 && tid >= kPublisher) {
+        for (int j = lane; j < 2 * RB; j += 64) {
+            const uint32_t *w = ws + kWsPLogit + (j >> 1) * 32 + (j & 1) * 2;
+            const uint64_t v = poll_pair(w, epoch, err, budget);
+            if (2 * j < E) s_plogit[2 * j] = bf2f((uint32_t)v & 0xffffu);
+            if (2 * j + 1 < E) s_plogit[2 * j + 1] = bf2f((uint32_t)(v >> 32) & 0xffffu);
+        }
+        wave_lds_sync();
+        if (E <= 128)
+            topk_token<2>(s_plogit, nullptr, E, k, normalize, 0, pred_out, nullptr, nullptr, &s_tk2);
+        else
+            topk_token<4>(s_plogit, nullptr, E, k, normalize, 0, pred_out, nullptr, nullptr, &s_tk2);
+    }
     __syncthreads();
     // y[s][c] = bf16(h_s . down_s[col c]), each half-wave its own slot: the
     // slot's h chunks are read once, and the four column chains (each in
@@ -509,24 +525,6 @@ __global__ __launch_bounds__(256, 2) void decode_layer_kernel(
     if (CHAIN && !next_gate && blockIdx.x == 0 && tid < 2 * RB)
         __hip_atomic_store(reinterpret_cast<uint64_t *>(ws + kWsPLogit + (tid >> 1) * 32 + (tid & 1) * 2), 0ull,
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // the last block routes the next layer from the predictor logits (all
-    // published early in the launch) into pred_out
-    if (CHAIN && next_gate && blockIdx.x == gridDim.x - 1) {
-        __syncthreads();
-        if (wave == 0) {
-            for (int j = lane; j < 2 * RB; j += 64) {
-                const uint32_t *w = ws + kWsPLogit + (j >> 1) * 32 + (j & 1) * 2;
-                const uint64_t v = poll_pair(w, epoch, err, budget);
-                if (2 * j < E) s_logit[2 * j] = bf2f((uint32_t)v & 0xffffu);
-                if (2 * j + 1 < E) s_logit[2 * j + 1] = bf2f((uint32_t)(v >> 32) & 0xffffu);
-            }
-        }
-        __syncthreads();
-        if (E <= 128)
-            topk_block<2>(s_logit, nullptr, E, k, normalize, pred_out, nullptr, nullptr, &s_tk);
-        else
-            topk_block<4>(s_logit, nullptr, E, k, normalize, pred_out, nullptr, nullptr, &s_tk);
-    }
     if (tid == 0) __hip_atomic_store(ws + kWsEpoch + blockIdx.x, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
