@@ -348,6 +348,50 @@ def test_chained_equals_plain_launch_on_the_residual_sum(pd, shape, merge):
     _assert_sync_clean(ops, H)
 
 
+def _colliding_gate(x_eff, E, big, scores):
+    """Router rows whose logits on x_eff are about `scores` for the experts in
+    `big` and distinct values far below for the rest (probabilities 0)."""
+    xf = x_eff.float()[0]
+    target = torch.tensor([-130.0 - (e * 37) % 97 for e in range(E)])
+    target[big] = torch.tensor(scores)
+    return (target[:, None].to(DEV) * xf[None, :] / (xf @ xf)).to(torch.bfloat16).contiguous()
+
+
+@pytest.mark.parametrize("merge", ["fused", "reference"])
+def test_chained_routing_where_logit_order_and_probability_order_differ(pd, merge):
+    """The chained kernel on logits whose probabilities tie at 0 below the
+    top three (the logit-key pick fails its check and the exact routing and
+    its rows replace it), with the next gate built the same way: every output
+    bitwise that of the plain launch on x_eff, pred_out the exact routing of
+    the next gate."""
+    ops, layer, synthetic = pd
+    H, I, E, k = 2048, 768, 128, 8
+    if not ops.decode_layer_supported(H, I, E, k, DEV):
+        pytest.skip("shape not resident on this device")
+    lay = synthetic.make_layer(H, I, E, k, True, seed=4343, device=DEV)
+    slots = ops.slot_table([lay.experts[e] for e in range(E)], DEV)
+    x = synthetic.make_tokens(1, H, seed=78, device=DEV)
+    resid = synthetic.make_tokens(1, H, seed=79, device=DEV)
+    x_eff = x + resid
+    gate = _colliding_gate(x_eff, E, [30, 99, 2], [5.0, 4.5, 4.0])
+    nxt = _colliding_gate(x_eff, E, [12, 127], [3.0, 2.5])
+    base = _fused(ops, x_eff, gate, slots, I, k, True, merge=merge)
+    nids = _route_ids(ops, x_eff, nxt, k, True)
+    c = _chained(ops, x, gate, slots, I, k, True, resid=resid, next_gate=nxt, merge=merge)
+    torch.cuda.synchronize()
+    for name, want in (("logits", base[0]), ("ids", base[1]), ("weights", base[2]), ("out", base[3]),
+                       ("probs", base[4]), ("x_out", x_eff)):
+        got = c[name]
+        eq = torch.equal(got.view(torch.int16), want.view(torch.int16)) if got.dtype == torch.bfloat16 \
+            else torch.equal(got.view(torch.int32), want.view(torch.int32))
+        assert eq, name
+    ids = c["ids"].cpu().numpy()[0].tolist()
+    assert ids == [30, 99, 2] + [e for e in range(E) if e not in (30, 99, 2)][:5], ids
+    assert torch.equal(c["pred_out"], nids[0])
+    assert c["pred_out"].cpu().tolist() == [12, 127] + [e for e in range(E) if e not in (12, 127)][:6]
+    _assert_sync_clean(ops, H)
+
+
 def test_chain_of_layers_equals_layer_by_layer(pd):
     """Four layers chained the way a decode step runs them: each launch takes
     the previous output and residual and predicts the next layer's experts.
