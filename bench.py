@@ -910,10 +910,12 @@ def main():
     for wl in order:
         kind, T, nl = plan[wl]
         main_leg = wl == args.workload
-        steps = args.steps if main_leg else {"prefill512": 200, "decode": 2000, "prefill4096": 50, "prefill4096_zipf": 20,
-                                                       "dsv2_mixed": 100}[wl]
-        warmup = args.warmup if main_leg else {"prefill512": 20, "decode": 200, "prefill4096": 5, "prefill4096_zipf": 2,
-                                                        "dsv2_mixed": 10}[wl]
+        # extra legs: enough warm-up for the weight pages of every layer copy
+        # to be mapped, and steps enough for a stable mean (a few seconds each)
+        steps = args.steps if main_leg else {"prefill512": 400, "decode": 2000, "prefill4096": 200, "prefill4096_zipf": 20,
+                                                       "dsv2_mixed": 300}[wl]
+        warmup = args.warmup if main_leg else {"prefill512": 100, "decode": 200, "prefill4096": 50, "prefill4096_zipf": 2,
+                                                        "dsv2_mixed": 50}[wl]
         if kind == "decode":
             steps = max(steps, 1)
         log(f"[bench] {wl}: T={T} layers={nl} steps={steps} warmup={warmup}")
