@@ -70,6 +70,26 @@ class ExpertKey:
         _require_int(self.expert, "expert")
         if not isinstance(self.representation, str) or not self.representation:
             raise CacheError("an expert key names its representation")
+        # the ledger hashes and compares keys on every transition: the field
+        # tuple and its hash are computed once (the record is immutable)
+        t = (self.layer, self.expert, self.representation)
+        object.__setattr__(self, "_t", t)
+        object.__setattr__(self, "_h", hash(t))
+
+    def __eq__(self, other):
+        if self is other:
+            return True
+        if other.__class__ is self.__class__:
+            return self._t == other._t
+        return NotImplemented
+
+    def __hash__(self):
+        return self._h
+
+    def __reduce__(self):
+        # rebuilt through __init__, so the cached hash is recomputed where the
+        # key is loaded (string hashes differ between processes)
+        return (ExpertKey, (self.layer, self.expert, self.representation))
 
 
 @dataclass(frozen=True)
@@ -93,6 +113,24 @@ class LoadTicket:
     key: ExpertKey
     pool: str            # "cache" or "demand_staging"
     slot: int | None     # staging slot index
+
+    def __post_init__(self):
+        # tickets key the executor's copy and transfer tables: hash once
+        object.__setattr__(self, "_h", hash((self.owner, self.generation, self.key, self.pool, self.slot)))
+
+    def __eq__(self, other):
+        if self is other:
+            return True
+        if other.__class__ is self.__class__:
+            return (self._h == other._h and self.generation == other.generation and self.owner == other.owner
+                    and self.key == other.key and self.pool == other.pool and self.slot == other.slot)
+        return NotImplemented
+
+    def __hash__(self):
+        return self._h
+
+    def __reduce__(self):
+        return (LoadTicket, (self.owner, self.generation, self.key, self.pool, self.slot))
 
 
 @dataclass(frozen=True)
@@ -169,14 +207,26 @@ class _Reveal:
     open_keys: set
 
 
+def _order(key):
+    """ExpertKey order as a plain tuple (the dataclass orders by these fields
+    in this order): sorting and bisecting on it compares in C."""
+    return key._t
+
+
+def _order_item(item):
+    return _order(item[0])
+
+
 class _Ranking:
-    """Keys ordered by (rank, key): one sorted bucket of keys per rank value
-    and the sorted list of ranks that have a non-empty bucket."""
+    """Keys ordered by (rank, key): one sorted bucket per rank value (holding
+    the keys' field tuples) and the sorted list of ranks that have a
+    non-empty bucket."""
 
     def __init__(self):
         self._rank_of = {}
         self._buckets = {}
         self._ranks = []
+        self._key_of = {}
 
     def __contains__(self, key):
         return key in self._rank_of
@@ -192,7 +242,9 @@ class _Ranking:
         if bucket is None:
             bucket = self._buckets[rank] = []
             bisect.insort(self._ranks, rank)
-        bisect.insort(bucket, key)
+        t = _order(key)
+        bisect.insort(bucket, t)
+        self._key_of[t] = key
         self._rank_of[key] = rank
 
     def discard(self, key):
@@ -200,19 +252,23 @@ class _Ranking:
         if rank is None:
             return
         bucket = self._buckets[rank]
-        del bucket[bisect.bisect_left(bucket, key)]
+        t = _order(key)
+        del bucket[bisect.bisect_left(bucket, t)]
+        del self._key_of[t]
         if not bucket:
             del self._buckets[rank]
             del self._ranks[bisect.bisect_left(self._ranks, rank)]
 
     def ascending(self):
         for rank in list(self._ranks):
-            yield from list(self._buckets.get(rank, ()))
+            for t in list(self._buckets.get(rank, ())):
+                yield self._key_of[t]
 
     def clear(self):
         self._rank_of.clear()
         self._buckets.clear()
         self._ranks.clear()
+        self._key_of.clear()
 
 
 class ExpertCache:
@@ -272,7 +328,7 @@ class ExpertCache:
 
     def _copy_for(self, ticket):
         copy = self._copies.get(ticket.key)
-        if copy is None or copy.ticket != ticket:
+        if copy is None or (copy.ticket is not ticket and copy.ticket != ticket):
             raise CacheError("the ticket belongs to no live copy of this ledger")
         return copy
 
@@ -303,7 +359,7 @@ class ExpertCache:
 
     @property
     def unfinished_demand_keys(self):
-        return () if self._reveal is None else tuple(sorted(self._reveal.open_keys))
+        return () if self._reveal is None else tuple(sorted(self._reveal.open_keys, key=_order))
 
     @property
     def retention_hint(self):
@@ -469,7 +525,7 @@ class ExpertCache:
             raise CacheError("only a true routing reveals demand")
         if not isinstance(token_counts, Mapping):
             raise CacheError("token counts must be a mapping expert -> tokens")
-        counts = tuple(sorted(dict(token_counts).items()))
+        counts = tuple(sorted(dict(token_counts).items(), key=_order_item))
         if not counts:
             raise CacheError("an empty demand cannot be revealed")
         for key, n in counts:
@@ -656,7 +712,8 @@ class ExpertCache:
             raise CacheError("no ready copy to compute with (a loading copy is not a hit)")
         handle = UseHandle(c.ticket, next(self._serials))
         c.holders.add(handle.serial)
-        self._reindex(key)
+        # an open expert is in no ranking (the reveal took it out and only a
+        # closed one goes back), so holding it changes no ranking
         return handle
 
     def release(self, handle):

@@ -137,6 +137,12 @@ class PDScopeCudaRuntime:
         self.device = self.executor.device
         self.pending = {}
         self.transient = set()
+        # the masters' own key objects: the ledger's tables are keyed by them,
+        # so lookups with these hit on identity
+        self._keys = {}
+        for mk in masters:
+            if mk.representation == "bf16":
+                self._keys.setdefault(mk.layer, [None] * self.E)[mk.expert] = mk
         self.forecasts = {}
         self.prediction_counts = {p: dict(hits=0, total=0) for p in ("prefill", "decode")}
         self._ws = {}
@@ -175,7 +181,16 @@ class PDScopeCudaRuntime:
         return ws
 
     def _key(self, layer, e):
-        return ExpertKey(layer, e, "bf16")
+        # one key object per expert, built once (a key is an immutable record)
+        keys = self._keys.get(layer)
+        if keys is None:
+            keys = self._keys[layer] = [None] * self.E
+        if not 0 <= e < self.E:
+            return ExpertKey(layer, e, "bf16")
+        k = keys[e]
+        if k is None:
+            k = keys[e] = ExpertKey(layer, e, "bf16")
+        return k
 
     def poll(self, wait=False):
         for key, ticket in list(self.pending.items()):

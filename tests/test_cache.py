@@ -297,3 +297,39 @@ def test_retention_hint_lasts_one_reveal_and_expire_prefetch():
     t5 = c.begin_load(K(1, 5), origin="prefetch")
     assert c.expire_prefetch(t5) and c.lookup(K(1, 5)) is None and t5 in c.take_retired()
     assert t not in c.take_retired()
+
+
+def test_expert_key_record_contract():
+    """ExpertKey stays a frozen, ordered dataclass record: field equality and
+    hash, order by (layer, expert, representation), replace/asdict, and a
+    pickle round trip that rebuilds its hash in the loading process."""
+    import dataclasses
+    import pickle
+    a, b, c = ExpertKey(1, 2, "bf16"), ExpertKey(1, 2, "bf16"), ExpertKey(1, 10, "bf16")
+    assert a == b and a is not b and hash(a) == hash(b) and len({a, b, c}) == 2
+    assert a != c and a < c and sorted([c, ExpertKey(0, 99, "bf16"), a])[0] == ExpertKey(0, 99, "bf16")
+    assert ExpertKey(1, 2, "a") < ExpertKey(1, 2, "b") and a != (1, 2, "bf16")
+    assert dataclasses.replace(a, expert=10) == c
+    assert dataclasses.asdict(a) == dict(layer=1, expert=2, representation="bf16")
+    r = pickle.loads(pickle.dumps(a))
+    assert r == a and hash(r) == hash(a) and {a: 1}[r] == 1
+    with pytest.raises(dataclasses.FrozenInstanceError):
+        a.layer = 3
+    with pytest.raises(CacheError):
+        ExpertKey(1, -1, "bf16")
+
+
+def test_load_ticket_record_contract():
+    """LoadTicket equality and hash follow its fields, also across a pickle
+    round trip and for distinct but equal key objects."""
+    import dataclasses
+    import pickle
+    from pdscope_amd.cache import LoadTicket
+    a = LoadTicket("owner", 3, ExpertKey(1, 2, "bf16"), "cache", None)
+    b = LoadTicket("owner", 3, ExpertKey(1, 2, "bf16"), "cache", None)
+    assert a == b and hash(a) == hash(b) and {a: 1}[b] == 1
+    for field, value in (("owner", "x"), ("generation", 4), ("key", ExpertKey(1, 3, "bf16")),
+                         ("pool", "demand_staging"), ("slot", 0)):
+        assert dataclasses.replace(a, **{field: value}) != a, field
+    r = pickle.loads(pickle.dumps(a))
+    assert r == a and hash(r) == hash(a)
