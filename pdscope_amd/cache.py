@@ -349,6 +349,15 @@ class ExpertCache:
         return EntryView(key, c.nbytes, c.ticket.pool, c.state, c.ticket, c.phase != RESERVED, len(c.holders),
                          c.origin, c.used, c.expired)
 
+    def ready_in_cache(self, key):
+        """Whether lookup(key) would show state 'ready' (landed, not held) in
+        pool 'cache', without building the view."""
+        c = self._copies.get(key)
+        if c is None:
+            self._registered(key)
+            return False
+        return not c.holders and c.phase == READY and c.ticket.pool == "cache"
+
     @property
     def resident_payload_bytes(self):
         return self._cache_charged

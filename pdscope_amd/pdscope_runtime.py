@@ -213,11 +213,8 @@ class PDScopeCudaRuntime:
         self.executor.reclaim()
 
     def _layer_fully_resident(self, layer):
-        for e in range(self.E):
-            v = self.cache.lookup(self._key(layer, e))
-            if v is None or v.state != "ready" or v.pool != "cache":
-                return False
-        return True
+        ready = self.cache.ready_in_cache
+        return all(ready(self._key(layer, e)) for e in range(self.E))
 
     # ------------------------------------------------------------ forward
 

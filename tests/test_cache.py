@@ -333,3 +333,32 @@ def test_load_ticket_record_contract():
         assert dataclasses.replace(a, **{field: value}) != a, field
     r = pickle.loads(pickle.dumps(a))
     assert r == a and hash(r) == hash(a)
+
+
+def test_ready_in_cache_agrees_with_lookup():
+    """ready_in_cache(key) is lookup's (state == 'ready' and pool == 'cache')
+    through a lifecycle: hot copies, a held copy, a staged miss."""
+    sizes = {ExpertKey(0, e, "bf16"): 10 for e in range(4)}
+    cache = ExpertCache(sizes, 20, [10], policy="LRU", initial_hotset=[ExpertKey(0, 0, "bf16"), ExpertKey(0, 1, "bf16")])
+    for k in cache.initial_hotset:
+        t = cache.begin_load(k, origin="initial")
+        cache.submit(t)
+        cache.complete_load(t)
+
+    def agree():
+        for k in sizes:
+            v = cache.lookup(k)
+            assert cache.ready_in_cache(k) == (v is not None and v.state == "ready" and v.pool == "cache"), k
+    agree()
+    cache.on_demand(DemandID("r", 0, 0), {ExpertKey(0, 0, "bf16"): 1, ExpertKey(0, 2, "bf16"): 1})
+    h = cache.acquire(ExpertKey(0, 0, "bf16"))
+    agree()
+    t = cache.begin_load(ExpertKey(0, 2, "bf16"), origin="demand", admit=False)
+    cache.submit(t)
+    agree()
+    cache.complete_load(t)
+    agree()
+    cache.release(h)
+    agree()
+    with pytest.raises(CacheError):
+        cache.ready_in_cache(ExpertKey(0, 9, "bf16"))
