@@ -574,8 +574,11 @@ class ExpertCache:
                 self._times_demanded[o.key] += 1
                 self._last_tick[o.key] = self._tick
         self._reveal = _Reveal(identity, counts, valid, observations, set(physical))
+        # open experts cannot be evicted: they leave both rankings (what
+        # _reindex does for a key that is not evictable)
         for key in physical:
-            self._reindex(key)  # open experts cannot be evicted
+            self._unprotected.discard(key)
+            self._protected_rank.discard(key)
         return observations
 
     def _observe(self, key, tokens, valid_tokens):
