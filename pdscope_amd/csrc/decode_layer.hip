@@ -244,6 +244,7 @@ __global__ __launch_bounds__(256, 2) void decode_layer_kernel(
         s_epoch = ep ? ep : 1u;
     }
     for (int e = tid; e < E; e += blockDim.x) s_slot[e] = slots[e];
+    if (tid < 16) s_tk.seli[tid] = -1;  // no expert picked yet (see the rows below)
     __syncthreads();
     const uint32_t epoch = s_epoch;
     // the residual sum: now where the router dot needs it, else while the
@@ -321,17 +322,25 @@ __global__ __launch_bounds__(256, 2) void decode_layer_kernel(
                           pub ? probs : nullptr, &s_tk);
         }
     }
-    __syncthreads();
+    // with the logit-key pick each wave waits (below) only for the ranks of its
+    // own rows, which wave 0 stores round by round: a block whose rows belong
+    // to an early rank starts streaming before the pick is complete
+    if (!by_keys) __syncthreads();
 
     // ---- 3. the gate/up rows this wave computes
     uint4 gv[P][NCH], uv[P][NCH];
     bool has[P];
-    auto issue_rows = [&](const TopkScratch &tk) __attribute__((always_inline)) {
+    auto issue_rows = [&](TopkScratch &tk) __attribute__((always_inline)) {
 #pragma unroll
         for (int p = 0; p < P; ++p) {
             const int q = min(q0 + p, KI - 1);
             const int sl = q / I, i = q - sl * I;
-            const uint16_t *base = s_slot[tk.seli[sl]];
+            int e = __hip_atomic_load(&tk.seli[sl], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            while (e < 0) {  // rank sl not picked yet (logit-key pick in progress)
+                __builtin_amdgcn_s_sleep(1);
+                e = __hip_atomic_load(&tk.seli[sl], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
+            const uint16_t *base = s_slot[e];
             // an expert without a ready copy reads the activation row instead
             // (H elements, in bounds) and contributes h = 0
             has[p] = base != nullptr;

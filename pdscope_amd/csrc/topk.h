@@ -158,8 +158,10 @@ __device__ __forceinline__ int logit_key(float v, int e) {
 // First half of the two-step routing of one token by one wave (no logit
 // bias): the k experts of largest bf16 logit (equal logits: lower id) in
 // that order, by k rounds of a wave-wide max over unique keys (no ballot
-// per round), into sc->seli.  rank[j] receives the rank of expert
-// lane + 64 j, -1 if not taken.  The softmax is increasing in the logit, so
+// per round), into sc->seli.  Each round's expert is stored at once with
+// workgroup-scope release, so other waves of the block may wait for just the
+// ranks they need (sc->seli[r] < 0 until then, when the caller cleared it).
+// rank[j] receives the rank of expert lane + 64 j, -1 if not taken.  The softmax is increasing in the logit, so
 // this is the probability top-k except where distinct logits give equal
 // probabilities; topk_verify_finish detects exactly those cases.
 template <int J>
@@ -173,7 +175,6 @@ __device__ __forceinline__ void topk_by_logit_keys(const float *lrow, int E, int
         key[j] = e < E ? logit_key(lrow[e], e) : (int)0x80000000;
         rank[j] = -1;
     }
-    int myid = 0;
     for (int r = 0; r < k; ++r) {
         int lm = key[0];
 #pragma unroll
@@ -185,9 +186,8 @@ __device__ __forceinline__ void topk_by_logit_keys(const float *lrow, int E, int
                 key[j] = (int)0x80000000;
                 rank[j] = r;
             }
-        if (lane == r) myid = sel;
+        if (lane == 0) __hip_atomic_store(&sc->seli[r], sel, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
-    if (lane < k) sc->seli[lane] = myid;
     wave_lds_sync();
 }
 
