@@ -10,10 +10,15 @@
 // every block is resident at once (checked against the occupancy of this
 // kernel on the current device).  Phases:
 //   1. blocks 0 .. E/4-1: one wave per router row -> bf16 logit;
-//   2. wave 0 of every block collects the E logits and runs softmax / top-k
-//      itself, so no further hop publishes the routing;
+//   2. wave 0 of every block collects the E logits and picks the experts
+//      itself, so no further hop publishes the routing: without a logit bias
+//      by unique bf16-logit keys, each rank stored as soon as it is known,
+//      then checked against the softmax probabilities while the rows stream
+//      (on a mismatch the exact top-k replaces the pick and the rows it
+//      changes are computed again); with a bias, the exact softmax / top-k;
 //   3. every wave issues the loads of its P (gate, up) row pairs of the
-//      routed experts (16-byte non-temporal loads);
+//      routed experts (16-byte non-temporal loads) once the rank of its rows
+//      is picked;
 //   4. gate/up dot products -> h; then the wave issues its down-projection
 //      rows (two slots x four output columns), which land while h is
 //      handed between blocks;
