@@ -341,7 +341,17 @@ __global__ __launch_bounds__(256, 2) void decode_layer_kernel(
             const int q = min(q0 + p, KI - 1);
             const int sl = q / I, i = q - sl * I;
             int e = __hip_atomic_load(&tk.seli[sl], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
-            while (e < 0) {  // rank sl not picked yet (logit-key pick in progress)
+            // rank sl not picked yet (logit-key pick in progress): wave 0 stores
+            // every rank after its bounded polls, so this ends; the wait still
+            // spends the thread's poll budget, and an exhausted budget sets the
+            // error word and reads expert 0 (in bounds)
+            while (e < 0) {
+                if (budget == 0) {
+                    __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    e = 0;
+                    break;
+                }
+                --budget;
                 __builtin_amdgcn_s_sleep(1);
                 e = __hip_atomic_load(&tk.seli[sl], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
             }
