@@ -113,27 +113,32 @@ def test_fused_matches_oracle_qwen(orc, pd):
     _assert_sync_clean(ops)
 
 
+COLLIDE_SHAPES = [dict(H=2048, I=768, E=128, k=8, big=[101, 7, 64]),
+                  dict(H=2048, I=512, E=256, k=8, big=[200, 3, 129]),
+                  dict(H=1024, I=512, E=64, k=4, big=[40, 9])]
+
+
 @pytest.mark.parametrize("merge", ["fused", "reference"])
-def test_fused_routing_where_logit_order_and_probability_order_differ(orc, pd, merge):
+@pytest.mark.parametrize("shape", COLLIDE_SHAPES, ids=lambda s: f"E{s['E']}_k{s['k']}")
+def test_fused_routing_where_logit_order_and_probability_order_differ(orc, pd, merge, shape):
     """The fused kernel picks experts by their bf16 logits first and checks
-    the pick against the probabilities.  Here three experts get logits near
-    +5 and the others distinct logits far below (their probabilities
-    underflow to 0 and tie), so the probability top-k takes the five lowest
-    ids among the tied experts while the logit order would take the five
-    largest logits: the check must fail and the exact routing (and the rows
-    it changes) must win.  Ids and weights against the oracle, everything
-    bitwise against the three-launch path."""
+    the pick against the probabilities.  Here two or three experts get
+    logits near +5 and the others distinct logits far below (their
+    probabilities underflow to 0 and tie), so the probability top-k fills
+    the rest with the lowest ids among the tied experts while the logit order
+    would take the largest logits: the check must fail and the exact routing
+    (and the rows it changes) must win.  Shapes cover 64, 128 and 256
+    experts (the pick's two- and four-candidates-per-lane forms).  Ids and weights against
+    the oracle, everything bitwise against the three-launch path."""
     ops, layer, synthetic = pd
-    H, I, E, k = 2048, 768, 128, 8
-    if not ops.decode_layer_supported(H, I, E, k, DEV):
-        pytest.skip("shape not resident on this device")
-    lay = synthetic.make_layer(H, I, E, k, True, seed=4242, device=DEV)
+    H, I, E, k, big = shape["H"], shape["I"], shape["E"], shape["k"], shape["big"]
+    assert ops.decode_layer_supported(H, I, E, k, DEV), "the fused kernel should cover this shape"
+    lay = synthetic.make_layer(H, I, E, k, True, seed=4242 + E, device=DEV)
     slots = ops.slot_table([lay.experts[e] for e in range(E)], DEV)
     x = synthetic.make_tokens(1, H, seed=77, device=DEV)
     xf = x.float()[0]
-    big = [101, 7, 64]
     target = torch.tensor([-130.0 - (e * 37) % 97 for e in range(E)])
-    target[big] = torch.tensor([5.0, 4.5, 4.0])
+    target[big] = torch.tensor([5.0, 4.5, 4.0][:len(big)])
     gate = (target[:, None].to(DEV) * xf[None, :] / (xf @ xf)).to(torch.bfloat16).contiguous()
     a = _three_launch(ops, x, gate, slots, I, k, True, merge=merge)
     b = _fused(ops, x, gate, slots, I, k, True, merge=merge)
@@ -144,8 +149,8 @@ def test_fused_routing_where_logit_order_and_probability_order_differ(orc, pd, m
     oi, ow = orc.route_from_logits(u16(b[0]), k, True, None)
     assert np.array_equal(b[1].cpu().numpy(), oi) and np.array_equal(u16(b[2]), ow)
     ids = b[1].cpu().numpy()[0].tolist()
-    assert ids[:3] == big
-    assert ids[3:] == [e for e in range(E) if e not in big][:5], ids
+    assert ids[:len(big)] == big
+    assert ids[len(big):] == [e for e in range(E) if e not in big][:k - len(big)], ids
     lg = u16(b[0])[0].astype(np.int32)
     assert len(set(lg[[e for e in range(E) if e not in big]].tolist())) > 5, "the tied experts' logits must differ"
     _assert_sync_clean(ops, H)
@@ -357,24 +362,28 @@ def _colliding_gate(x_eff, E, big, scores):
     return (target[:, None].to(DEV) * xf[None, :] / (xf @ xf)).to(torch.bfloat16).contiguous()
 
 
+CHAIN_COLLIDE = [dict(H=2048, I=768, E=128, k=8, big=[30, 99, 2], nbig=[12, 127]),
+                 dict(H=2048, I=512, E=256, k=8, big=[250, 1, 130], nbig=[200, 17])]
+
+
 @pytest.mark.parametrize("merge", ["fused", "reference"])
-def test_chained_routing_where_logit_order_and_probability_order_differ(pd, merge):
+@pytest.mark.parametrize("shape", CHAIN_COLLIDE, ids=lambda s: f"E{s['E']}")
+def test_chained_routing_where_logit_order_and_probability_order_differ(pd, merge, shape):
     """The chained kernel on logits whose probabilities tie at 0 below the
     top three (the logit-key pick fails its check and the exact routing and
     its rows replace it), with the next gate built the same way: every output
     bitwise that of the plain launch on x_eff, pred_out the exact routing of
     the next gate."""
     ops, layer, synthetic = pd
-    H, I, E, k = 2048, 768, 128, 8
-    if not ops.decode_layer_supported(H, I, E, k, DEV):
-        pytest.skip("shape not resident on this device")
-    lay = synthetic.make_layer(H, I, E, k, True, seed=4343, device=DEV)
+    H, I, E, k, big, nbig = shape["H"], shape["I"], shape["E"], shape["k"], shape["big"], shape["nbig"]
+    assert ops.decode_layer_supported(H, I, E, k, DEV), "the fused kernel should cover this shape"
+    lay = synthetic.make_layer(H, I, E, k, True, seed=4343 + E, device=DEV)
     slots = ops.slot_table([lay.experts[e] for e in range(E)], DEV)
     x = synthetic.make_tokens(1, H, seed=78, device=DEV)
     resid = synthetic.make_tokens(1, H, seed=79, device=DEV)
     x_eff = x + resid
-    gate = _colliding_gate(x_eff, E, [30, 99, 2], [5.0, 4.5, 4.0])
-    nxt = _colliding_gate(x_eff, E, [12, 127], [3.0, 2.5])
+    gate = _colliding_gate(x_eff, E, big, [5.0, 4.5, 4.0])
+    nxt = _colliding_gate(x_eff, E, nbig, [3.0, 2.5])
     base = _fused(ops, x_eff, gate, slots, I, k, True, merge=merge)
     nids = _route_ids(ops, x_eff, nxt, k, True)
     c = _chained(ops, x, gate, slots, I, k, True, resid=resid, next_gate=nxt, merge=merge)
@@ -386,9 +395,9 @@ def test_chained_routing_where_logit_order_and_probability_order_differ(pd, merg
             else torch.equal(got.view(torch.int32), want.view(torch.int32))
         assert eq, name
     ids = c["ids"].cpu().numpy()[0].tolist()
-    assert ids == [30, 99, 2] + [e for e in range(E) if e not in (30, 99, 2)][:5], ids
+    assert ids == big + [e for e in range(E) if e not in big][:k - 3], ids
     assert torch.equal(c["pred_out"], nids[0])
-    assert c["pred_out"].cpu().tolist() == [12, 127] + [e for e in range(E) if e not in (12, 127)][:6]
+    assert c["pred_out"].cpu().tolist() == nbig + [e for e in range(E) if e not in nbig][:k - 2]
     _assert_sync_clean(ops, H)
 
 
