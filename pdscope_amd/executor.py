@@ -195,6 +195,8 @@ class ExpertExecutor:
         self.closed = False
         self._host_tables = {}  # layer -> host list of base addresses (0 = no ready copy)
         self._dev_tables = {}   # layer -> device int64 [E]
+        self._table_version = {}  # layer -> count of host table changes
+        self._uploaded = {}       # layer -> (version, stream, event) of the last upload
         self._ring = _PinnedRing(8 * 256)
         # the slot storage was allocated on the current stream, whose queued
         # work may still touch the blocks' previous owners: order both
@@ -276,22 +278,33 @@ class ExpertExecutor:
 
     def _set_entry(self, key, addr):
         host = self._host_tables.get(key.layer)
-        if host is not None and key.expert < len(host):
+        if host is not None and key.expert < len(host) and host[key.expert] != addr:
             host[key.expert] = addr
+            self._table_version[key.layer] = self._table_version.get(key.layer, 0) + 1
 
     def table_entry(self, layer, e):
         host = self._host_tables.get(layer)
         return 0 if host is None or e >= len(host) else host[e]
 
     def upload_table(self, layer, E, stream):
-        """Copy the host mirror of a layer's slot table to the device on `stream`."""
+        """Copy the host mirror of a layer's slot table to the device on `stream`.
+
+        A table whose host mirror has not changed since its last upload is not
+        copied again; a reader on another stream is ordered after that copy."""
         dev, host = self.table(layer, E)
+        ver = self._table_version.get(layer, 0)
+        last = self._uploaded.get(layer)
+        if last is not None and last[0] == ver:
+            if last[1] != stream:
+                stream.wait_event(last[2])
+            return dev
         i, buf = self._ring.take()
         view = buf[:8 * E].view(torch.int64)
         view.copy_(torch.tensor(host, dtype=torch.int64))
         with torch.cuda.stream(stream):
             dev.copy_(view, non_blocking=True)
         self._ring.mark(i, stream)
+        self._uploaded[layer] = (ver, stream, self._ring.events[i])
         return dev
 
     def upload_ints(self, values, stream):
@@ -549,6 +562,8 @@ class ExpertExecutor:
             self.pinned.clear()
             self._host_tables.clear()
             self._dev_tables.clear()
+            self._table_version.clear()
+            self._uploaded.clear()
             self.cache_storage = None
             self.closed = True
 
