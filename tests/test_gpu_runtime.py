@@ -452,6 +452,46 @@ def test_executor_per_expert_hook_matches_oracle(orc):
         ex.shutdown()
 
 
+def test_executor_slot_table_upload_follows_the_host_mirror():
+    """upload_table copies a layer's table again only after an entry changed;
+    every upload, skipped or not, leaves the device table equal to the host
+    mirror as seen from the stream that asked for it."""
+    from pdscope_amd.cache import DemandID, ExpertCache, ExpertKey
+    from pdscope_amd.executor import ExpertExecutor
+    H, I, E, k = 256, 128, 32, 4
+    _, masters = build(1, H, I, E, k, seed=6)
+    sizes = {key: w.nbytes for key, w in masters.items()}
+    size = next(iter(sizes.values()))
+    cache = ExpertCache(sizes, 4 * size, [size, size])
+    ex = ExpertExecutor(cache, masters, 0)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+
+    def device_table(stream):
+        dev = ex.upload_table(0, E, stream)
+        with torch.cuda.stream(stream):
+            snap = dev.clone()
+        stream.synchronize()
+        return snap.cpu().tolist()
+
+    try:
+        assert device_table(s1) == [0] * E
+        copies_before = ex._ring.i
+        assert device_table(s2) == [0] * E          # unchanged: no new copy
+        assert ex._ring.i == copies_before
+        key = ExpertKey(0, 3, "bf16")
+        cache.on_demand(DemandID("r", 1, 0), {key: 1})
+        t = ex.load(key)
+        assert ex.finish_load(t, wait=True)
+        want = [0] * E
+        want[3] = ex.copies[t].data_ptr()
+        assert ex.table(0, E)[1] == want
+        assert device_table(s2) == want             # changed: copied again
+        assert ex._ring.i != copies_before
+        assert device_table(s1) == want             # unchanged, read from the other stream
+    finally:
+        ex.shutdown()
+
+
 class _Pool:
     def __init__(self):
         self.q = []
