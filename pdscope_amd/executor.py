@@ -404,12 +404,27 @@ class ExpertExecutor:
             self._group_stream_ctx = None
 
     def gpu_group(self, keys, launch, *, input_ref=None, wait_for=None):
-        """Acquire `keys`, run `launch()` (one grouped launch) on the compute stream, record one event."""
+        """Acquire `keys`, run `launch()` (one grouped launch) on the compute stream, record one event.
+
+        With launch=None the work reading these copies is already enqueued on
+        `wait_for` (a replay issued before the reveal): the uses are accounted
+        and the event is recorded on that stream, with no compute-stream join."""
         self._open()
         handles = tuple(self.cache.acquire(k) for k in keys)
         for h in handles:
             if h.ticket not in self.copies or h.ticket in self.loads:
                 raise RuntimeError("acquired a copy whose transfer has not been confirmed")
+        if launch is None:
+            for h in handles:
+                ev = self._landed.pop(h.ticket, None)
+                if ev is not None:
+                    self._free_events.append(ev)
+            ev = self._event()
+            ev.record(torch.cuda.current_stream(self.device) if wait_for is None else wait_for)
+            p = PendingCompute(handles, None, ev, input_ref, tuple(keys))
+            self.computes[id(p)] = p
+            self._log(event="compute_submitted", experts=len(keys))
+            return p
         span = self._group_stream_ctx is not None
         ctx = contextlib.nullcontext() if span else torch.cuda.stream(self.compute_stream)
         with ctx:

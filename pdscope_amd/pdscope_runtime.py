@@ -426,8 +426,7 @@ class PDScopeCudaRuntime:
                         self._replay_decode_graph(layer, x, gate, normalize, k, out, ring=ring,
                                                   next_gate=graph_pred)
                 else:
-                    def launch():  # the replay already produced `out`; account the uses it made
-                        pass
+                    launch = None  # the replay on `cur` already produced `out`; account the uses it made
                 tasks.append(ex.gpu_group([key(e) for e in resident], launch, input_ref=x, wait_for=cur))
         elif resident:
             ex.table(layer, E)
