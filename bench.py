@@ -661,23 +661,16 @@ def run_stack(n_layers, device, seed0, T_prefill=2048, n_decode=64, cap_gib=24, 
 
 def copy_engine_gbs(rt, srcs, device):
     """Back-to-back expert copies from pinned host memory into the runtime's
-    staging slots, alternating over two side streams as the executor's loads
-    do: the H2D rate the staging path can reach."""
+    staging slots on a side stream: the H2D rate the staging path can reach."""
     import torch
     from pdscope_amd import ops
     dst = rt.executor.staging
-    cur = torch.cuda.current_stream(device)
-    queues = (torch.cuda.Stream(device), torch.cuda.Stream(device))
+    s = torch.cuda.Stream(device)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize(device)
-    e0.record(cur)
-    for q in queues:
-        q.wait_stream(cur)
+    e0.record(s)
     for j, src in enumerate(srcs):
-        ops.stage_expert(dst[j % len(dst)][:EXPERT_BYTES], src.view(torch.uint8), stream=queues[j % 2])
-    for q in queues:
-        cur.wait_stream(q)
-    e1.record(cur)
+        ops.stage_expert(dst[j % len(dst)][:EXPERT_BYTES], src.view(torch.uint8), stream=s)
+    e1.record(s)
     torch.cuda.synchronize(device)
     return len(srcs) * EXPERT_BYTES / (e0.elapsed_time(e1) / 1e3) / 1e9
 

@@ -4,9 +4,8 @@ Mirrors ExpertExecutor (expertbench/executor.py:165-680) for the GPU path:
 
 * ``load`` reserves a copy in the ledger and stages the expert's whole
   gate|up|down block (one pinned host block, one ``hipMemcpyAsync``) into a
-  cache-pool slot or a demand staging slot, alternating between two load
-  queues (the load stream and a second one), recording one event
-  (executor.py:333-372);
+  cache-pool slot or a demand staging slot on the load stream, recording one
+  event (executor.py:333-372);
 * ``finish_load`` reports completion to the ledger only after that event
   completed (executor.py:374-390);
 * ``gpu_group`` acquires every expert of a launch, runs ONE grouped launch on
@@ -152,13 +151,6 @@ class ExpertExecutor:
                     or any(s.device != self.device for s in streams)):
                 raise ValueError("shared executor streams must be a distinct pair on the same device")
             self.load_stream, self.compute_stream = streams
-        # Expert copies alternate between the load stream and a second one:
-        # two copy queues keep two DMA engines busy (9 MiB pinned blocks back
-        # to back: 57 GB/s against 54 GB/s on one queue).  Each copy records
-        # its own event, and a slot is rewritten only after the ledger retired
-        # its previous copy, so the two queues need no ordering between them.
-        self._load_queues = (self.load_stream, torch.cuda.Stream(device=self.device))
-        self._next_queue = 0
         # ---- device storage: one contiguous cache pool of equal slots, plus staging slots
         nslots = cache.cache_bytes // self.expert_bytes
         if cache_storage is None:
@@ -202,8 +194,7 @@ class ExpertExecutor:
         # work may still touch the blocks' previous owners: order both
         # executor streams after it before they write or read a slot
         cur = torch.cuda.current_stream(self.device)
-        for q in self._load_queues:
-            q.wait_stream(cur)
+        self.load_stream.wait_stream(cur)
         self.compute_stream.wait_stream(cur)
         self._group_stream_ctx = None
         self._cpu_pool = None
@@ -365,9 +356,7 @@ class ExpertExecutor:
         self.copies[ticket] = flat
         self.cache.submit(ticket)
         ev = self._event()
-        queue = self._load_queues[self._next_queue]
-        self._next_queue ^= 1
-        ops.stage_expert(flat, src, event=ev, stream=queue)
+        ops.stage_expert(flat, src, event=ev, stream=self.load_stream)
         self.loads[ticket] = ev
         self._log(event="load_submitted", generation=ticket.generation, pool=ticket.pool,
                   expert_bytes=self.expert_bytes, source_pinned=bool(src.is_pinned()))
@@ -566,8 +555,7 @@ class ExpertExecutor:
             self._cpu_pool.shutdown(wait=True)
             self._cpu_pool = None
         if not self.closed:
-            for q in self._load_queues:
-                q.synchronize()
+            self.load_stream.synchronize()
             self.compute_stream.synchronize()
             self.copies.clear()
             self.loads.clear()
