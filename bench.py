@@ -2,7 +2,7 @@
 """MoE-layer benchmark on one MI355X: Qwen3-30B-A3B-shaped layers, seeded random weights.
 
     python bench.py [--steps K] [--warmup W]
-                    [--workload prefill512|decode|prefill4096|prefill4096_zipf|dsv2_mixed|stack48]
+                    [--workload prefill512|decode|prefill4096|prefill4096_zipf|dsv2_mixed|stack48|runtime_decode]
 
 A step is one MoE layer forward over one batch of synthetic tokens whose
 inputs and weights are already resident in HBM: route (K1) -> pack (K2) ->
@@ -51,7 +51,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=4000)
     ap.add_argument("--warmup", type=int, default=400)
     ap.add_argument("--workload", default="decode",
-                    choices=["prefill512", "decode", "prefill4096", "prefill4096_zipf", "dsv2_mixed", "stack48"])
+                    choices=["prefill512", "decode", "prefill4096", "prefill4096_zipf", "dsv2_mixed", "stack48",
+                             "runtime_decode"])
     ap.add_argument("--no-extra", action="store_true", help="only the main workload")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, cpus) - 1")
@@ -659,6 +660,56 @@ def run_stack(n_layers, device, seed0, T_prefill=2048, n_decode=64, cap_gib=24, 
                 pcie=pcie, steps_run=n_decode)
 
 
+def run_runtime_decode(steps, warmup, n_layers, device, seed0):
+    """Decode through the drop-in runtime with every expert resident: one
+    token per PDScopeCudaRuntime.forward call, each layer replaying its
+    captured single-launch graph (with the next layer's prediction), the
+    routing read back for the ledger's reveal, acquire / release of the
+    routed experts and the trace row.  A step is one layer call, timed by
+    wall clock: the host cost of the runtime around the layer kernel."""
+    import torch
+    from pdscope_amd import synthetic
+    from pdscope_amd.cache import ExpertKey
+    from pdscope_amd.executor import masters_from_block
+    from pdscope_amd.pdscope_runtime import PDScopeCudaRuntime
+    gates, masters, hot = [], {}, []
+    for l in range(n_layers):
+        lay = synthetic.make_layer(H, I, E, K_TOP, True, seed=seed0 + 40000 + 1000 * l, device=device)
+        masters.update(masters_from_block(l, lay.experts, E, H, I))
+        gates.append(lay.gate)
+        hot += [ExpertKey(l, e, "bf16") for e in range(E)]
+        del lay
+    torch.cuda.empty_cache()
+    rt = PDScopeCudaRuntime(masters, hot_keys=hot, speculative_slots=0, demand_slots=8, resident_graphs=True,
+                            device=device, diagnostics=False)
+    x = synthetic.make_tokens(1, H, seed=seed0 + 40999, device=device)
+    try:
+        def pass_(step):
+            for l in range(n_layers):
+                rt.forward(x, gates[l], layer=l, step=step, request="runtime_decode", top_k=K_TOP,
+                           next_gate=gates[l + 1] if l + 1 < n_layers else None)
+        n_warm = max(1, -(-warmup // n_layers))
+        n_timed = max(1, steps // n_layers)
+        for p in range(n_warm):
+            pass_(1 + p)
+        torch.cuda.synchronize(device)
+        t0 = time.perf_counter()
+        for p in range(n_timed):
+            pass_(1 + n_warm + p)
+        torch.cuda.synchronize(device)
+        wall = time.perf_counter() - t0
+    finally:
+        rt.close()
+    calls = n_timed * n_layers
+    t = wall / calls
+    layer_bytes = K_TOP * EXPERT_BYTES + ROUTER_BYTES + 2 * H * 2
+    hbm = dict(bound="hbm", achieved=layer_bytes / t / 1e9, peak=HBM_PEAK_GBS, unit="GB/s")
+    hbm["frac"] = hbm["achieved"] / hbm["peak"]
+    return dict(tok_s=1.0 / t, ms_per_step=t * 1e3, kernel="PDScopeCudaRuntime.forward, T=1, all experts resident",
+                kernel_ms_mean=t * 1e3, host_us_per_layer_call=t * 1e6, layers_rotated=n_layers, hbm=hbm,
+                steps_run=calls)
+
+
 def copy_engine_gbs(rt, srcs, device):
     """Back-to-back expert copies from pinned host memory into the runtime's
     staging slots on a side stream: the H2D rate the staging path can reach."""
@@ -903,9 +954,12 @@ def main():
         return
 
     plan = {"prefill512": ("prefill", 512, 4), "decode": ("decode", 1, 16), "prefill4096": ("prefill", 4096, 2),
-            "prefill4096_zipf": ("zipf", 4096, 2), "dsv2_mixed": ("dsv2", 1304, 4), "stack48": ("stack", 2048, 48)}
-    # the 48-layer stack pins 58 GB of host masters: it runs only when asked for
-    order = [args.workload] + ([] if args.no_extra else [w for w in plan if w not in (args.workload, "stack48")])
+            "prefill4096_zipf": ("zipf", 4096, 2), "dsv2_mixed": ("dsv2", 1304, 4), "stack48": ("stack", 2048, 48),
+            "runtime_decode": ("rtdecode", 1, 4)}
+    # the 48-layer stack pins 58 GB of host masters, and the runtime's host
+    # cost is a separate question: both run only when asked for
+    order = [args.workload] + ([] if args.no_extra else [w for w in plan
+                                                         if w not in (args.workload, "stack48", "runtime_decode")])
     records, raw = {}, {}
     for wl in order:
         kind, T, nl = plan[wl]
@@ -930,6 +984,9 @@ def main():
             rec = dict(res)
         elif kind == "stack":
             res = run_stack(nl, device, 20261011)
+            rec = dict(res)
+        elif kind == "rtdecode":
+            res = run_runtime_decode(steps, warmup, nl, device, 20261011)
             rec = dict(res)
         else:
             res = run_decode(steps, warmup, nl, device, 20261011)
@@ -973,6 +1030,9 @@ def main():
                 "prefill4096": "Qwen3-30B-A3B-shaped MoE layer, prefill T=4096 uniform routing, 128 experts resident",
                 "prefill4096_zipf": "Qwen3-30B-A3B-shaped MoE layer, prefill T=4096 with a Zipf(1.1) router bias, "
                                     "32 experts resident, the rest staged through 8 demand slots",
+                "runtime_decode": "Qwen3-30B-A3B-shaped MoE layers through PDScopeCudaRuntime.forward, decode T=1, "
+                                  "all 128 experts resident, graph replay with next-layer prediction; a step is "
+                                  "one layer call (host cost of the runtime included)",
                 "stack48": "48 Qwen3-30B-A3B-shaped MoE blocks (identity attention + RMSNorm), prefill 2048 then 64 "
                            "decode steps, 24 GiB expert-slot cap, gate-fallback prefetch, decode graph replay; "
                            "value is decode tok/s"}
