@@ -541,9 +541,11 @@ class PDScopeCudaRuntime:
             note = getattr(self.cpu_backend, "note_native_dispatch", None)
             if note is not None:
                 note(len(native_cpu))
-        done = torch.cuda.Event()
-        done.record(ex.compute_stream)
-        cur.wait_event(done)
+        if not (graph_path and not late_replays):
+            # (a replay served before the reveal enqueued nothing on the compute stream)
+            done = torch.cuda.Event()
+            done.record(ex.compute_stream)
+            cur.wait_event(done)
         if graph_path and late_replays:
             # replays after the demand reveal: their error word, read once they completed
             host[err_at:err_at + 1].copy_(self._decode_error_word(), non_blocking=True)
