@@ -558,106 +558,37 @@ def zipf_gemm(lay, x, bias, device, reps=20):
                           frac=achieved / BF16_PEAK_TFLOPS))
 
 
-def rms_residual(out, x, eps=1e-6):
-    """Next-layer activation of the stack: attention is the identity, so the
-    block is h = x + moe(x) followed by RMSNorm (weight 1) in fp32."""
-    import torch
-    h = out.float() + x.float()
-    return (h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + eps)).to(torch.bfloat16)
-
-
 def run_stack(n_layers, device, seed0, T_prefill=2048, n_decode=64, cap_gib=24, hot_per_layer=40, demand_slots=8):
-    """48 Qwen3-30B-A3B-shaped MoE blocks through the drop-in runtime: the
-    expert masters live in pinned host memory (48 x 128 x 9 MiB), HBM holds at
-    most cap_gib of expert slots (a static hot set chosen by calibration
-    routing, speculative prefetch slots and 8 demand staging slots), the
-    gate-fallback predictor (layer l+1 gate on the layer-l activation)
-    prefetches, and decode layers replay their captured single-launch graph
-    over the resident set.  Prefill 2048 tokens, then 64 decode steps."""
-    import torch
-    from pdscope_amd import synthetic
-    from pdscope_amd.cache import ExpertKey
-    from pdscope_amd.executor import masters_from_block
-    from pdscope_amd.pdscope_runtime import PDScopeCudaRuntime
+    """48 Qwen3-30B-A3B-shaped MoE blocks through the drop-in runtime
+    (pdscope_amd.stack): the expert masters live in pinned host memory
+    (48 x 128 x 9 MiB); the process's device memory stays within cap_gib
+    (allocator capped 1 GiB below it, expert slots sized within the cap: a
+    static hot set chosen by calibration routing, speculative prefetch slots
+    and 8 demand staging slots); the gate-fallback predictor (layer l+1 gate
+    on the layer-l activation) prefetches, and decode layers replay their
+    captured single-launch graph over the resident set.  Prefill 2048
+    tokens, then 64 decode steps.  The run raises if the ledger does not
+    close or the device footprint exceeds the cap."""
+    from pdscope_amd import stack
     t_setup = time.perf_counter()
-    gates, masters, hot = [], {}, []
-    calib = synthetic.make_tokens(512, H, seed=seed0 + 30001, device=device)
-    from pdscope_amd import layer as LY
-    cws = LY.MoEWorkspace(512, H, I, E, K_TOP, device, route_only=True)
-    for l in range(n_layers):
-        lay = synthetic.make_layer(H, I, E, K_TOP, True, seed=seed0 + 20000 + 1000 * l, device=device)
-        masters.update(masters_from_block(l, lay.experts, E, H, I))
-        gates.append(lay.gate)
-        # static hot profile: the experts a seeded calibration batch routes to most
-        _, ids, _ = LY.route(calib, lay.gate, cws)
-        cnt = torch.bincount(ids.reshape(-1).long(), minlength=E).cpu().tolist()
-        hot += [ExpertKey(l, e, "bf16") for e in sorted(range(E), key=lambda e: (-cnt[e], e))[:hot_per_layer]]
-        del lay
-    torch.cuda.empty_cache()
-    slot_budget = (cap_gib << 30) // EXPERT_BYTES
-    speculative = slot_budget - demand_slots - len(hot)
-    if speculative < 0:
-        raise ValueError("hot set and staging slots exceed the HBM cap")
-    rt = PDScopeCudaRuntime(masters, hot_keys=hot, speculative_slots=speculative, demand_slots=demand_slots,
-                            resident_graphs=True, device=device, diagnostics=False)
+    model = stack.build_stack(n_layers, device, seed0=seed0, hot_per_layer=hot_per_layer)
+    session = stack.StackSession(model, device, stack.StackBudget(device_total=cap_gib << 30,
+                                                                  demand_slots=demand_slots))
     setup_s = time.perf_counter() - t_setup
     try:
-        def pass_(x, step):
-            rows = []
-            for l in range(n_layers):
-                out, _, row = rt.forward(x, gates[l], layer=l, step=step, request="stack",
-                                         next_gate=gates[l + 1] if l + 1 < n_layers else None, top_k=K_TOP)
-                rows.append(row)
-                x = rms_residual(out, x)
-            return x, rows
-
-        def phase_stats(rows, wall, tokens, before, after):
-            # whole-phase ledger totals: a copy that lands between two layer
-            # calls is completed by the next call's poll, outside any row
-            h2d = after.get("h2d_bytes_submitted", 0) - before.get("h2d_bytes_submitted", 0)
-            demand = sum(len(r["decision"]["on_demand_queue"]) for r in rows)
-            routed = sum(len(r["token_counts"]) for r in rows)
-            return dict(tok_s=tokens / wall, wall_s=wall, h2d_bytes=h2d, h2d_gbs=h2d / wall / 1e9,
-                        routed_experts=routed, demand_misses=demand, resident_hit_rate=1 - demand / max(1, routed),
-                        prefetch_issued=sum(len(r["prefetch_issued"]) for r in rows),
-                        **{kk: after.get(kk, 0) - before.get(kk, 0) for kk in
-                           ("demand_loads_submitted", "prefetch_loads_submitted", "unused_prefetch_evictions",
-                            "fresh_prefetch_hits", "loading_misses", "absent_misses")},
-                        paths=sorted({r.get("decode_path", "grouped") for r in rows}))
-
-        x = synthetic.make_tokens(T_prefill, H, seed=seed0 + 30002, device=device)
-        # the residual block's torch kernels load on their first call (~0.25 s
-        # on a fresh process): call it once outside the timed passes
-        rms_residual(x, x)
-        torch.cuda.synchronize(device)
-        st0 = rt.cache.stats()
-        t0 = time.perf_counter()
-        x, rows_p = pass_(x, 0)
-        torch.cuda.synchronize(device)
-        st1 = rt.cache.stats()
-        prefill = phase_stats(rows_p, time.perf_counter() - t0, T_prefill, st0, st1)
-        rows_d = []
-        t0 = time.perf_counter()
-        for step in range(1, n_decode + 1):
-            tok = synthetic.make_tokens(1, H, seed=seed0 + 30100 + step, device=device)
-            _, rows = pass_(tok, step)
-            rows_d += rows
-        torch.cuda.synchronize(device)
-        decode = phase_stats(rows_d, time.perf_counter() - t0, n_decode, st1, rt.cache.stats())
-        pred = {p: dict(v) for p, v in rt.prediction_counts.items()}
-        copy_gbs = copy_engine_gbs(rt, [masters[ExpertKey(0, e, "bf16")].flat for e in range(E)], device)
-        mem = dict(cache_slots=len(hot) + speculative, hot_slots=len(hot), speculative_slots=speculative,
-                   demand_slots=demand_slots, hbm_expert_bytes=(len(hot) + speculative + demand_slots) * EXPERT_BYTES,
-                   pinned_master_bytes=len(masters) * EXPERT_BYTES)
+        res = session.run(T_prefill, n_decode)
+        copy_gbs = copy_engine_gbs(session.runtime, [model.expert_block(0, e) for e in range(E)], device)
     finally:
-        rt.close()
+        session.close()
+    prefill, decode = res["prefill"], res["decode"]
     pcie = dict(bound="pcie_h2d", achieved=prefill["h2d_gbs"], peak=copy_gbs, unit="GB/s",
                 peak_kind="measured back-to-back expert copies on this host", phase="prefill")
     pcie["frac"] = pcie["achieved"] / pcie["peak"]
+    del model, session
     return dict(tok_s=decode["tok_s"], ms_per_step=1e3 / decode["tok_s"], kernel="48-layer stack through the runtime",
-                kernel_ms_mean=1e3 * decode["wall_s"] / n_decode, prefill=prefill, decode=decode, predictor=pred,
-                memory=mem, layers=n_layers, setup_s=setup_s, tokens_prefill=T_prefill, decode_steps=n_decode,
-                pcie=pcie, steps_run=n_decode)
+                kernel_ms_mean=1e3 * decode["wall_s"] / n_decode, prefill=prefill, decode=decode,
+                predictor=res["predictor"], memory=res["memory"], closure=res["closure"], layers=n_layers,
+                setup_s=setup_s, tokens_prefill=T_prefill, decode_steps=n_decode, pcie=pcie, steps_run=n_decode)
 
 
 def run_runtime_decode(steps, warmup, n_layers, device, seed0):

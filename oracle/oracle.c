@@ -213,24 +213,27 @@ static double silu_d(double g) { return g / (1.0 + exp(-g)); }
 /* qwen.py:87-90 with torch's bf16 output rounding after every op. */
 void orc_expert_forward(const uint16_t *x, int m, const uint16_t *wg, const uint16_t *wu,
                         const uint16_t *wd, int H, int I, uint16_t *y, uint16_t *h) {
-#pragma omp parallel
-    {
-        uint16_t *hrow = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)I);
-#pragma omp for schedule(static)
-        for (int r = 0; r < m; ++r) {
-            const uint16_t *xr = x + (size_t)r * H;
-            for (int i = 0; i < I; ++i) {
-                uint16_t g = orc_f64_to_bf16(dot_bf16_exact(xr, wg + (size_t)i * H, H));
-                uint16_t u = orc_f64_to_bf16(dot_bf16_exact(xr, wu + (size_t)i * H, H));
-                uint16_t a = orc_f64_to_bf16(silu_d(orc_bf16_to_f32(g)));
-                hrow[i] = orc_f64_to_bf16((double)orc_bf16_to_f32(a) * (double)orc_bf16_to_f32(u));
-            }
-            if (h) memcpy(h + (size_t)r * I, hrow, sizeof(uint16_t) * (size_t)I);
-            for (int j = 0; j < H; ++j)
-                y[(size_t)r * H + j] = orc_f64_to_bf16(dot_bf16_exact(hrow, wd + (size_t)j * I, I));
-        }
-        free(hrow);
+    /* Every output element is one exact dot product rounded once, so the
+     * work splits over (row, column) pairs: a single-row call uses every
+     * thread and the result does not depend on the thread count. */
+    uint16_t *hbuf = h ? h : (uint16_t *)malloc(sizeof(uint16_t) * (size_t)m * I);
+    if (!hbuf) return;
+    int64_t ni = (int64_t)m * I, nj = (int64_t)m * H;
+#pragma omp parallel for schedule(static)
+    for (int64_t ri = 0; ri < ni; ++ri) {
+        int64_t r = ri / I, i = ri % I;
+        const uint16_t *xr = x + (size_t)r * H;
+        uint16_t g = orc_f64_to_bf16(dot_bf16_exact(xr, wg + (size_t)i * H, H));
+        uint16_t u = orc_f64_to_bf16(dot_bf16_exact(xr, wu + (size_t)i * H, H));
+        uint16_t a = orc_f64_to_bf16(silu_d(orc_bf16_to_f32(g)));
+        hbuf[ri] = orc_f64_to_bf16((double)orc_bf16_to_f32(a) * (double)orc_bf16_to_f32(u));
     }
+#pragma omp parallel for schedule(static)
+    for (int64_t rj = 0; rj < nj; ++rj) {
+        int64_t r = rj / H, j = rj % H;
+        y[rj] = orc_f64_to_bf16(dot_bf16_exact(hbuf + (size_t)r * I, wd + (size_t)j * I, I));
+    }
+    if (!h) free(hbuf);
 }
 
 /* qwen.py:93-98 reference_fp32: float math with no intermediate rounding. */

@@ -63,6 +63,40 @@ def oracle_layer_given_routing(orc, x_u16, ids, w_u16, experts_u16, H, I):
     return orc.merge(y, p["row_of"], w_u16), y, p
 
 
+def oracle_tokens_given_routing(orc, x_u16, ids, w_u16, tokens, block_of, H, I, add_in=None, merge="fused"):
+    """Oracle layer output of selected tokens for a given routing.
+
+    block_of(e) returns expert e's flat gate|up|down block as uint16.  The
+    rows of one expert go through the oracle in one call.  merge "fused" is
+    the exactly rounded weighted sum, "reference" the reference's bf16
+    index_add_ in ascending expert id (the runtime's default merge).
+    Returns (out [n,H], y [n*k,H]) with y in (token, slot) order."""
+    tokens = np.asarray(tokens)
+    n, k = len(tokens), ids.shape[1]
+    y = np.empty((n * k, H), np.uint16)
+    sel = ids[tokens]
+    IH = I * H
+    for e in np.unique(sel):
+        where = np.argwhere(sel == e)
+        xs = np.ascontiguousarray(x_u16[tokens[where[:, 0]]])
+        blk = block_of(int(e))
+        y[where[:, 0] * k + where[:, 1]] = orc.expert_forward(
+            xs, blk[:IH].reshape(I, H), blk[IH:2 * IH].reshape(I, H), blk[2 * IH:].reshape(H, I))
+    w_t = np.ascontiguousarray(w_u16[tokens])
+    if merge == "fused":
+        row_of = np.arange(n * k, dtype=np.int32).reshape(n, k)
+        return orc.merge(y, row_of, w_t, add_in=add_in), y
+    if merge != "reference":
+        raise ValueError(merge)
+    # merge_ordered adds a token's rows in grouped-row order, which is
+    # ascending expert id: place each token's rows by the rank of their id
+    rank = np.argsort(np.argsort(sel, axis=1, kind="stable"), axis=1, kind="stable")
+    row_of = (np.arange(n)[:, None] * k + rank).astype(np.int32)
+    y_rows = np.empty_like(y)
+    y_rows[row_of.reshape(-1)] = y
+    return orc.merge_ordered(y_rows, row_of, w_t, add_in=add_in), y
+
+
 def assert_layer_close(orc, out, ref_u16):
     m = err_metrics(orc.bf16_to_f32(u16(out)), orc.bf16_to_f32(ref_u16))
     assert m["max_rel"] <= MAX_REL and m["mean_abs"] <= MEAN_ABS, m
