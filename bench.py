@@ -4,19 +4,22 @@
     python bench.py [--steps K] [--warmup W]
                     [--workload prefill512|decode|prefill4096|prefill4096_zipf|dsv2_mixed|stack48|runtime_decode]
 
-A step is one MoE layer forward over one batch of synthetic tokens whose
-inputs and weights are already resident in HBM: route (K1) -> pack (K2) ->
-balanced tile schedule -> grouped SwiGLU gate/up + down (K3) -> merge (K5) for
-prefill, route (K1) -> decode GEMV gate/up + down/merge (K4) for T = 1
-(decode steps replay one hipGraph per layer).  Steps rotate over several
-independently seeded layer copies so the 256 MB Infinity Cache cannot hold
-the streamed weights between steps.
+Inputs and weights are resident in HBM when timing starts.  A prefill step
+is one MoE layer forward over one batch of synthetic tokens: route (K1) ->
+pack with the balanced tile schedule (K2) -> grouped SwiGLU gate/up + down
+(K3) -> merge (K5).  A decode step is one token through 16 layer copies: one
+replay of a hipGraph of 16 single-launch layers (route + top-k + gate/up +
+down + merge in one launch each); its throughput counts the 16 layer
+launches.  Steps rotate over several independently seeded layer copies so the
+256 MB Infinity Cache cannot hold the streamed weights between steps.
 
 The default workload is the T = 1 decode layer (128 experts, top-8, all
 resident), the configuration the metric is quoted on.  The same JSON line
-also carries the T = 512 and T = 4096 prefills (all resident, and the
-T = 4096 Zipf-skewed layer with 32 resident experts and 8 demand staging
-slots through the runtime) and the DeepSeek-V2-Lite mixed-batch results
+also carries the T = 512 prefill (uniform routing), the T = 4096 prefill on
+the Zipf(1.1)-biased routing with every expert resident (the grouped SwiGLU
+the T = 4096 target names; the uniform routing beside it), the T = 4096
+Zipf-skewed layer with 32 resident experts and 8 demand staging slots
+through the runtime, and the DeepSeek-V2-Lite mixed-batch results
 ("workloads"), each with its own roofline figure, and CPU baselines: the
 AVX2 bf16 SwiGLU expert kernel under oracle/ (a stand-in for ktransformers'
 AVX2BF16_MOE, which is not available offline) timed on this host's cores on
@@ -25,7 +28,9 @@ seconds of CPU work.
 
 Roofline: ``achieved`` is algorithmic bytes (or useful flops) of the dominant
 kernel per launch divided by its mean duration, measured with HIP events on
-the launch stream during the timed steps.
+the launch stream during the timed steps (for T = 4096: both grouped
+launches against the layer's useful flops).  ``traffic`` is read from the
+committed rocprofv3 counter summary of the same command under profiles/.
 """
 from __future__ import annotations
 
@@ -48,14 +53,15 @@ CPU_SAMPLE_S = 10.0            # seconds of CPU work per CPU-baseline sample
 def parse():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=4000)
-    ap.add_argument("--warmup", type=int, default=400)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--workload", default="decode",
                     choices=["prefill512", "decode", "prefill4096", "prefill4096_zipf", "dsv2_mixed", "stack48",
                              "runtime_decode"])
     ap.add_argument("--no-extra", action="store_true", help="only the main workload")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, cpus) - 1")
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="0: physical cores of this process's CPUs (at most 16, one GPU's share) - 1")
     ap.add_argument("--cpu-seconds", type=float, default=CPU_SAMPLE_S,
                     help="CPU work per CPU-baseline sample (after two warm-up runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -200,8 +206,11 @@ def build_layers(n, device, seed0):
     return layers
 
 
-def run_prefill(T, steps, warmup, n_layers, device, seed0):
-    """Eager launches; HIP events bracket the grouped gate/up kernel in every timed step."""
+def run_prefill(T, steps, warmup, n_layers, device, seed0, bias=None):
+    """Eager launches; HIP events bracket the grouped gate/up and down kernels
+    in every timed step.  bias: the router's fp32 logit bias (the Zipf
+    workload).  Each layer copy's row tile comes from its own routing's mean
+    and largest expert rows, as the runtime chooses it for a resident launch."""
     import torch
     from pdscope_amd import layer, ops, synthetic
     layers = build_layers(n_layers, device, seed0)
@@ -210,12 +219,13 @@ def run_prefill(T, steps, warmup, n_layers, device, seed0):
     n = T * K_TOP
     _, _, _, packed = ws.views(T)
     stream = torch.cuda.current_stream(device)
+    tiles = {}
 
     def step(i, ev=None):
         lay, slots = layers[i % n_layers]
         x = xs[i % n_layers]
-        logits, ids, w = layer.route(x, lay.gate, ws)
-        bm = ops.grouped_block_m(n // E)
+        logits, ids, w = layer.route(x, lay.gate, ws, bias=bias)
+        bm = tiles.get(i % n_layers, ops.grouped_block_m(n // E))
         max_tiles = (n + bm - 1) // bm + E
         # the down launch has its own row tile (layer.down_block_m); the pack
         # launch writes the balanced schedule for both
@@ -235,12 +245,16 @@ def run_prefill(T, steps, warmup, n_layers, device, seed0):
             ev[2].record(stream)
         ops.merge(ws.y, packed.row_of, w, ws.out[:T])
 
-    # experts touched per layer (for algorithmic bytes)
-    touched = []
+    # experts touched per layer (for algorithmic bytes) and each copy's row tile
+    touched, max_rows = [], []
     for i in range(n_layers):
         step(i)
         torch.cuda.synchronize(device)
-        touched.append(int((ws.counts > 0).sum().item()))
+        counts = ws.counts.cpu()
+        live = counts[counts > 0]
+        touched.append(int(live.numel()))
+        max_rows.append(int(live.max()))
+        tiles[i] = ops.grouped_block_m(int(live.sum()) // int(live.numel()), int(live.max()))
     for i in range(warmup):
         step(i)
     events = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(3)) for _ in range(steps)]
@@ -252,13 +266,16 @@ def run_prefill(T, steps, warmup, n_layers, device, seed0):
     wall = time.perf_counter() - t0
     gateup_ms = [a.elapsed_time(b) for a, b, _ in events]
     down_ms = [b.elapsed_time(c) for _, b, c in events]
+    grouped_ms = [g + d for g, d in zip(gateup_ms, down_ms)]
     mean_touched = sum(touched[i % n_layers] for i in range(steps)) / steps
-    bmm = vendor_bmm_ms(n // E, device) if n % E == 0 and n // E >= 128 else None
+    bmm = vendor_bmm_ms(n // E, device) if bias is None and n % E == 0 and n // E >= 128 else None
     return dict(T=T, wall_s=wall, ms_per_step=wall / steps * 1e3, tok_s=T * steps / wall,
                 gateup_ms_mean=statistics.mean(gateup_ms), gateup_ms_median=statistics.median(gateup_ms),
-                down_ms_median=statistics.median(down_ms), vendor_bmm=bmm,
-                touched=mean_touched, block_m=ops.grouped_block_m(n // E), layers=n_layers,
-                first_layer=layers[0], first_x=xs[0], ws=ws)
+                down_ms_mean=statistics.mean(down_ms), down_ms_median=statistics.median(down_ms),
+                grouped_ms_mean=statistics.mean(grouped_ms), grouped_ms_median=statistics.median(grouped_ms),
+                vendor_bmm=bmm, touched=mean_touched, max_rows=max(max_rows),
+                block_m=sorted(set(tiles.values())), routing="zipf(1.1) bias" if bias is not None else "uniform",
+                layers=n_layers, steps_run=steps, first_layer=layers[0], first_x=xs[0], ws=ws, bias=bias)
 
 
 def vendor_bmm_ms(rows, device, reps=20):
@@ -293,9 +310,12 @@ def vendor_bmm_ms(rows, device, reps=20):
 
 def run_decode(steps, warmup, n_layers, device, seed0):
     """All layer copies captured in ONE hipGraph (as a decode step over a stack
-    of resident layers replays them); HIP events bracket every replay and the
-    per-layer time is the replay time over the layer count.  The same is done
-    for the three-launch path (route + decode GEMV + down/merge) for reference."""
+    of resident layers replays them).  A step is one replay: one token through
+    the n_layers layers.  Exactly `steps` replays are timed after `warmup`
+    untimed ones, with a HIP event on the replay stream after each; the layer
+    time is the events' total over steps * n_layers launches, and both the
+    throughput and the roofline come from it.  The same is done for the
+    three-launch path (route + decode GEMV + down/merge) for reference."""
     import torch
     from pdscope_amd import layer, ops, synthetic
     layers = build_layers(n_layers, device, seed0)
@@ -329,37 +349,43 @@ def run_decode(steps, warmup, n_layers, device, seed0):
         for i in range(n_layers):
             if not torch.equal(wss[i].out[:1], eager[i]):
                 raise AssertionError("decode graph replay differs from eager execution")
-        reps = max(1, nsteps // n_layers)
-        for _ in range(max(1, nwarm // n_layers)):
+        for _ in range(nwarm):
             g.replay()
-        events = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+        # exactly nsteps replays between two synchronisations; an event on the
+        # replay stream after each one
+        events = [torch.cuda.Event(enable_timing=True) for _ in range(nsteps + 1)]
         torch.cuda.synchronize(device)
         t0 = time.perf_counter()
         events[0].record(stream)
-        for r in range(reps):
+        for r in range(nsteps):
             g.replay()
             events[r + 1].record(stream)
         torch.cuda.synchronize(device)
         wall = time.perf_counter() - t0
-        layer_ms = [events[r].elapsed_time(events[r + 1]) / n_layers for r in range(reps)]
-        return reps * n_layers, wall, layer_ms
+        replay_ms = [events[r].elapsed_time(events[r + 1]) for r in range(nsteps)]
+        return wall, replay_ms, events[0].elapsed_time(events[nsteps])
 
     fused = ops.decode_layer_supported(H, I, E, K_TOP, device)
     g = capture(True)
-    n_steps, wall, layer_ms = timed(g, steps, warmup)
+    wall, replay_ms, total_ms = timed(g, steps, warmup)
     if fused and ops.decode_workspace_error(device, H):
         raise AssertionError("a bounded wait of the fused decode kernel gave up")
     g3 = capture(False)
-    _, _, layer_ms3 = timed(g3, steps, warmup)
-    chain = run_decode_chain(layers, device, seed0, reps=max(20, steps // n_layers // 4)) if fused else None
+    _, replay_ms3, _ = timed(g3, min(steps, 200), 20)
+    chain = run_decode_chain(layers, device, seed0, reps=max(20, min(steps, 500) // 4)) if fused else None
     read_ms = plain_read_ms(K_TOP * EXPERT_BYTES + ROUTER_BYTES, n_layers, device)
     kernel = ("decode_layer_kernel (route + top-k + gate/up + down/merge in one launch), "
               f"{n_layers} layers per hipGraph" if fused else
               f"route_gemv + decode_gateup + decode_down, {n_layers} layers per hipGraph")
-    return dict(T=1, wall_s=wall, ms_per_step=wall / n_steps * 1e3, tok_s=n_steps / wall, kernel=kernel,
-                layer_ms_mean=statistics.mean(layer_ms), layer_ms_median=statistics.median(layer_ms),
-                three_launch_layer_ms=statistics.median(layer_ms3), steps_run=n_steps, chain=chain,
-                plain_read_layer_ms=read_ms, layers=n_layers, first_layer=layers[0], first_x=xs[0], ws=wss[0])
+    launches = steps * n_layers
+    layer_ms = [ms / n_layers for ms in replay_ms]
+    return dict(T=1, wall_s=wall, event_s=total_ms / 1e3, ms_per_step=total_ms / steps,
+                tok_s=launches / (total_ms / 1e3), wall_tok_s=launches / wall, kernel=kernel,
+                layer_ms_mean=total_ms / launches, layer_ms_median=statistics.median(layer_ms),
+                layer_ms_min=min(layer_ms), layer_ms_max=max(layer_ms),
+                three_launch_layer_ms=statistics.median(replay_ms3) / n_layers, steps_run=steps,
+                layer_launches=launches, chain=chain, plain_read_layer_ms=read_ms, layers=n_layers,
+                first_layer=layers[0], first_x=xs[0], ws=wss[0])
 
 
 def run_decode_chain(layers, device, seed0, reps):
@@ -713,14 +739,34 @@ def run_dsv2_mixed(steps, warmup, n_layers, device, seed0):
 
 # ----------------------------------------------------------------------------- CPU baseline
 
+CPU_SHARE = 16   # host CPUs one GPU's work may occupy on the GPU box
+
+
+def host_cores():
+    """Logical CPUs this process may run on, the physical cores among them
+    (distinct (package, core) pairs from sysfs) and the CPU model."""
+    try:
+        aff = sorted(os.sched_getaffinity(0))
+    except AttributeError:
+        aff = list(range(os.cpu_count() or 2))
+    cores = set()
+    for c in aff:
+        base = f"/sys/devices/system/cpu/cpu{c}/topology/"
+        try:
+            cores.add((open(base + "physical_package_id").read().strip(), open(base + "core_id").read().strip()))
+        except OSError:
+            cores.add(("?", str(c)))
+    return dict(logical_cpus=len(aff), physical_cores=len(cores), share=CPU_SHARE, model=cpu_model())
+
+
 def cpu_threads(requested):
+    """Worker threads of the CPU baseline: one per physical core of the
+    process's CPUs, within one GPU's share of the box, minus one for the
+    control thread (README.md:142; docs/REPRODUCE.md:38-41 of the reference)."""
     if requested > 0:
         return requested
-    try:
-        avail = len(os.sched_getaffinity(0))
-    except AttributeError:
-        avail = os.cpu_count() or 2
-    return max(1, min(16, avail) - 1)
+    hc = host_cores()
+    return max(1, min(hc["physical_cores"], hc["logical_cpus"], CPU_SHARE) - 1)
 
 
 def cpu_model():
@@ -826,24 +872,36 @@ def cpu_baseline_decode(lay, x, threads, budget_s, copies=8, warm=2):
 # ----------------------------------------------------------------------------- reporting
 
 def prefill_record(res):
+    """Roofline figures of the grouped SwiGLU: `mfma` counts both launches
+    (gate/up + down) against the layer's useful flops 2*T*k*3*I*H (no tile
+    padding); `hbm` is the gate/up launch's algorithmic bytes (the HBM-bound
+    launch at T=512) over its own time."""
     T, touched = res["T"], res["touched"]
     n = T * K_TOP
     gateup_bytes = touched * 2 * I * H * 2 + T * H * 2 + n * I * 2
-    gateup_flops = 2.0 * n * H * 2 * I
-    t = res["gateup_ms_mean"] / 1e3
+    grouped_flops = 2.0 * n * 3 * I * H
+    t_gu = res["gateup_ms_mean"] / 1e3
+    t_grp = res["grouped_ms_mean"] / 1e3
     layer_bytes = touched * EXPERT_BYTES + ROUTER_BYTES + 2 * T * H * 2
-    layer_flops = 2.0 * n * 3 * I * H + 2.0 * T * E * H
-    hbm = dict(bound="hbm", achieved=gateup_bytes / t / 1e9, peak=HBM_PEAK_GBS, unit="GB/s")
+    layer_flops = grouped_flops + 2.0 * T * E * H
+    hbm = dict(bound="hbm", achieved=gateup_bytes / t_gu / 1e9, peak=HBM_PEAK_GBS, unit="GB/s",
+               kernel="grouped_kernel<gateup>")
     hbm["frac"] = hbm["achieved"] / hbm["peak"]
-    mfma = dict(bound="mfma", achieved=gateup_flops / t / 1e12, peak=BF16_PEAK_TFLOPS, unit="TFLOP/s")
+    mfma = dict(bound="mfma", achieved=grouped_flops / t_grp / 1e12, peak=BF16_PEAK_TFLOPS, unit="TFLOP/s",
+                kernel="grouped_kernel<gateup> + grouped_kernel<down>", flops=grouped_flops)
     mfma["frac"] = mfma["achieved"] / mfma["peak"]
+    gu_flops = 2.0 * n * H * 2 * I
     layer_s = res["ms_per_step"] / 1e3
-    return dict(tok_s=res["tok_s"], ms_per_step=res["ms_per_step"], kernel="grouped_kernel<gateup>",
-                kernel_ms_mean=res["gateup_ms_mean"], kernel_ms_median=res["gateup_ms_median"],
-                down_ms_median=res["down_ms_median"], vendor_bmm=res["vendor_bmm"],
-                kernel_bytes=gateup_bytes, kernel_flops=gateup_flops, experts_touched=touched,
-                block_m=res["block_m"], layers_rotated=res["layers"], hbm=hbm, mfma=mfma,
-                layer_hbm_gbs=layer_bytes / layer_s / 1e9, layer_mfma_tflops=layer_flops / layer_s / 1e12)
+    return dict(tok_s=res["tok_s"], ms_per_step=res["ms_per_step"], routing=res["routing"],
+                kernel="grouped_kernel<gateup> + grouped_kernel<down>",
+                kernel_ms_mean=res["grouped_ms_mean"], kernel_ms_median=res["grouped_ms_median"],
+                gateup_ms_mean=res["gateup_ms_mean"], gateup_ms_median=res["gateup_ms_median"],
+                down_ms_mean=res["down_ms_mean"], down_ms_median=res["down_ms_median"],
+                gateup_mfma_frac=gu_flops / t_gu / 1e12 / BF16_PEAK_TFLOPS, vendor_bmm=res["vendor_bmm"],
+                gateup_bytes=gateup_bytes, grouped_flops=grouped_flops, experts_touched=touched,
+                max_rows_per_expert=res["max_rows"], block_m=res["block_m"], layers_rotated=res["layers"],
+                hbm=hbm, mfma=mfma, layer_hbm_gbs=layer_bytes / layer_s / 1e9,
+                layer_mfma_tflops=layer_flops / layer_s / 1e12)
 
 
 def decode_record(res):
@@ -853,10 +911,12 @@ def decode_record(res):
     hbm["frac"] = hbm["achieved"] / hbm["peak"]
     read_ms = res["plain_read_layer_ms"]
     return dict(tok_s=res["tok_s"], ms_per_step=res["ms_per_step"], kernel=res["kernel"],
+                clock="HIP events on the replay stream over the timed replays (throughput and roofline)",
+                wall_tok_s=res["wall_tok_s"], layer_launches=res["layer_launches"],
                 kernel_ms_mean=res["layer_ms_mean"], kernel_ms_median=res["layer_ms_median"],
+                kernel_ms_min=res["layer_ms_min"], kernel_ms_max=res["layer_ms_max"],
                 three_launch_layer_ms=res["three_launch_layer_ms"],
                 kernel_bytes=layer_bytes, layers_rotated=res["layers"], hbm=hbm,
-                layer_hbm_gbs=layer_bytes / (res["ms_per_step"] / 1e3) / 1e9,
                 vendor_gemv=dict(ms=read_ms, gbs=layer_bytes / (read_ms / 1e3) / 1e9,
                                  layer_over_gemv=res["layer_ms_mean"] / read_ms,
                                  what="torch.mv (BLAS GEMV) reading the layer's byte count once per launch, "
@@ -875,7 +935,7 @@ def main():
         return
     import torch
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-    from pdscope_amd import _lib
+    from pdscope_amd import _lib, synthetic
     _lib.load()
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
@@ -897,14 +957,27 @@ def main():
         main_leg = wl == args.workload
         # extra legs: enough warm-up for the weight pages of every layer copy
         # to be mapped, and steps enough for a stable mean (a few seconds each)
-        steps = args.steps if main_leg else {"prefill512": 400, "decode": 2000, "prefill4096": 200, "prefill4096_zipf": 20,
+        steps = args.steps if main_leg else {"prefill512": 400, "decode": 500, "prefill4096": 200, "prefill4096_zipf": 20,
                                                        "dsv2_mixed": 300}[wl]
         warmup = args.warmup if main_leg else {"prefill512": 100, "decode": 200, "prefill4096": 50, "prefill4096_zipf": 2,
                                                         "dsv2_mixed": 50}[wl]
         if kind == "decode":
             steps = max(steps, 1)
         log(f"[bench] {wl}: T={T} layers={nl} steps={steps} warmup={warmup}")
-        if kind == "prefill":
+        if kind == "prefill" and T == 4096:
+            # config 3's layers, tokens and Zipf(1.1) router bias with every
+            # expert resident: the grouped SwiGLU the T=4096 target names;
+            # the uniform routing of the same shape is recorded beside it
+            bias, _ = synthetic.zipf_bias(E, 1.1, seed=20261011, device=device)
+            res = run_prefill(T, steps, warmup, nl, device, 20261011 + 9000, bias=bias)
+            rec = prefill_record(res)
+            uni = run_prefill(T, max(20, steps // 2), max(5, warmup // 2), nl, device, 20261011)
+            rec["uniform_routing"] = {kk: v for kk, v in prefill_record(uni).items()
+                                      if kk in ("tok_s", "kernel_ms_mean", "gateup_ms_mean", "down_ms_mean",
+                                                "gateup_mfma_frac", "mfma", "vendor_bmm", "block_m")}
+            for kk in ("first_layer", "first_x", "ws", "bias"):
+                uni.pop(kk, None)
+        elif kind == "prefill":
             res = run_prefill(T, steps, warmup, nl, device, 20261011)
             rec = prefill_record(res)
         elif kind == "dsv2":
@@ -933,11 +1006,21 @@ def main():
             lay0 = res["first_layer"][0]
             if kind == "decode":
                 cb = cpu_baseline_decode(lay0, res["first_x"], threads, args.cpu_seconds)
-            elif kind == "zipf":
+                # thread sweep (docs/REPRODUCE.md:50-52 of the reference), a short sample per count
+                sweep = []
+                for nt in sorted({1, 2, 4, 8, threads}):
+                    s = cpu_baseline_decode(lay0, res["first_x"], nt, 1.5, warm=1)
+                    sweep.append(dict(threads=nt, tok_s=s["value"], dram_gbs=s["dram_gbs"]))
+                cb["thread_sweep"] = sweep
+            elif res.get("bias") is not None:
                 cb = cpu_baseline_prefill(lay0, res["first_x"], threads, args.cpu_seconds, bias=res["bias"],
                                           what="Zipf(1.1)-biased ")
             else:
                 cb = cpu_baseline_prefill(lay0, res["first_x"], threads, args.cpu_seconds)
+            hc = cb["host"] = host_cores()
+            cb["sample"] += (f"; host: {hc['logical_cpus']} logical CPUs and {hc['physical_cores']} physical cores "
+                             f"in this process's affinity, {threads} workers = min(physical cores, "
+                             f"{CPU_SHARE}-CPU share of one GPU) - 1 for the control thread")
             rec["cpu_baseline"] = cb
             log(f"[bench] {wl}: CPU baseline {cb['value']:.2f} tok/s")
         for k in ("first_layer", "first_x", "ws", "bias"):
@@ -952,13 +1035,19 @@ def main():
         roof = dict(main["pcie"])
     else:
         roof = dict(main["hbm"])
-    roof["kernel"] = main["kernel"]
-    roof["traffic"] = traffic_from_profiles(f"{args.workload}_traffic.md")
+    roof.setdefault("kernel", main["kernel"])
+    traffic_profile = f"{args.workload}_traffic.md"
+    roof["traffic"] = traffic_from_profiles(traffic_profile)
+    roof["traffic_source"] = (f"profiles/{traffic_profile}: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of this "
+                              "workload's command, committed; not measured in this run"
+                              if roof["traffic"] is not None else None)
     cfg_name = {"dsv2_mixed": "DeepSeek-V2-Lite-shaped MoE layer (64 x 1408 routed top-6, 2 shared), mixed batch "
                               "48 decode + 256 + 1000 prefill tokens",
                 "prefill512": "Qwen3-30B-A3B-shaped MoE layer, prefill T=512 uniform routing, 128 experts resident",
-                "decode": "Qwen3-30B-A3B-shaped MoE layer, decode T=1, 128 experts resident (hipGraph per layer)",
-                "prefill4096": "Qwen3-30B-A3B-shaped MoE layer, prefill T=4096 uniform routing, 128 experts resident",
+                "decode": "Qwen3-30B-A3B-shaped MoE layer, decode T=1, 128 experts resident; a step is one token "
+                          "through 16 layer copies (one hipGraph replay of 16 single-launch layers)",
+                "prefill4096": "Qwen3-30B-A3B-shaped MoE layer, prefill T=4096 with a Zipf(1.1) router bias (the "
+                               "T=4096 layer's routing), all 128 experts resident: the grouped SwiGLU",
                 "prefill4096_zipf": "Qwen3-30B-A3B-shaped MoE layer, prefill T=4096 with a Zipf(1.1) router bias, "
                                     "32 experts resident, the rest staged through 8 demand slots",
                 "runtime_decode": "Qwen3-30B-A3B-shaped MoE layers through PDScopeCudaRuntime.forward, decode T=1, "

@@ -125,7 +125,7 @@ __device__ __forceinline__ void wait_stage(int younger) {
 // XCD b % 8): all n-tiles of an m-tile share the gathered activation rows
 // in one L2, and the m-tiles of one expert read the same weight tiles at
 // the same time from one L2.
-template <int BM, int BN, int BK, int WM, int WN, int SA, int SB, bool ILV, bool GATEUP, int OCC>
+template <int BM, int BN, int BK, int WM, int WN, int SA, int SB, bool ILV, bool GATEUP, int OCC, int FK>
 __global__ __launch_bounds__(64 * WM * WN, OCC == 1 ? 1 : OCC * WM * WN / 4) void grouped_kernel(
     const uint16_t *__restrict__ a_src, const int32_t *__restrict__ perm_token,
     const int32_t *__restrict__ offsets, const int32_t *__restrict__ sel, int nsel,
@@ -286,9 +286,11 @@ __global__ __launch_bounds__(64 * WM * WN, OCC == 1 ? 1 : OCC * WM * WN / 4) voi
     auto kloop = [&](auto live, auto role_c) __attribute__((always_inline)) {
         constexpr int L = decltype(live)::value;
         constexpr int ROLE = decltype(role_c)::value;
-        // a stage of BK is consumed in SUB fragment steps of BKF = 32 (two
-        // MFMA K steps each), so the fragment registers do not grow with BK
-        constexpr int BKF = BK < 32 ? BK : 32;
+        // a stage of BK is consumed in SUB fragment steps of BKF = FK (16:
+        // one MFMA K step, 32: two), so the fragment registers do not grow
+        // with BK
+        static_assert(FK == 16 || FK == 32, "fragment step of one or two MFMA K steps");
+        constexpr int BKF = BK < FK ? BK : FK;
         constexpr int SUB = BK / BKF;
         constexpr int KK = BKF / 16;
         bf16x8_t af[2][KK][MB], bfr[2][KK][NB];
@@ -464,7 +466,8 @@ __global__ __launch_bounds__(64 * WM * WN, OCC == 1 ? 1 : OCC * WM * WN / 4) voi
 
 // phase: 1 = gate/up only, 2 = down only, 3 = both
 // PH: the phases (1 gate/up, 2 down) this tile configuration serves
-template <int BM, int BN, int BK, int WM, int WN, int SA, int SB, bool ILV = false, int PH = 3, int OCC = 1>
+template <int BM, int BN, int BK, int WM, int WN, int SA, int SB, bool ILV = false, int PH = 3, int OCC = 1,
+          int FK = 32>
 int launch_grouped(int phase, const uint16_t *x, const int32_t *perm_token, const int32_t *offsets,
                    const int32_t *sel, int nsel, const int32_t *tile_start, int max_tiles,
                    const uint16_t *const *slots, int H, int I, uint16_t *h_ws, uint16_t *y, hipStream_t s) {
@@ -475,7 +478,7 @@ int launch_grouped(int phase, const uint16_t *x, const int32_t *perm_token, cons
     if constexpr ((PH & 1) != 0) if (phase & 1) {
         const size_t n1 = (size_t)max_tiles * (size_t)(I / (BN / 2));
         const unsigned g1 = (unsigned)((n1 + 7) / 8 * 8);
-        grouped_kernel<BM, BN, BK, WM, WN, SA, SB, ILV, true, OCC><<<g1, 64 * WM * WN, 0, s>>>(x, perm_token, offsets, sel, nsel, tile_start,
+        grouped_kernel<BM, BN, BK, WM, WN, SA, SB, ILV, true, OCC, FK><<<g1, 64 * WM * WN, 0, s>>>(x, perm_token, offsets, sel, nsel, tile_start,
                                                                     slots, H, I, h_ws);
         int rc = check_launch("grouped_kernel<gateup>");
         if (rc) return rc;
@@ -483,7 +486,7 @@ int launch_grouped(int phase, const uint16_t *x, const int32_t *perm_token, cons
     if constexpr ((PH & 2) != 0) if (phase & 2) {
         const size_t n2 = (size_t)max_tiles * (size_t)(H / BN);
         const unsigned g2 = (unsigned)((n2 + 7) / 8 * 8);
-        grouped_kernel<BM, BN, BK, WM, WN, SA, SB, ILV, false, OCC><<<g2, 64 * WM * WN, 0, s>>>(h_ws, nullptr, offsets, sel, nsel, tile_start,
+        grouped_kernel<BM, BN, BK, WM, WN, SA, SB, ILV, false, OCC, FK><<<g2, 64 * WM * WN, 0, s>>>(h_ws, nullptr, offsets, sel, nsel, tile_start,
                                                                      slots, H, I, y);
         return check_launch("grouped_kernel<down>");
     }
@@ -525,8 +528,16 @@ int grouped_entry(int phase, const void *x, const int32_t *perm_token, const int
         return launch_grouped<128, 256, 64, 2, 4, 3, 3>(phase, xp, perm_token, offsets, sel, nsel, tile_start, max_tiles,
                                                  sp, H, I, (uint16_t *)h_ws, (uint16_t *)y, s);
     case 256:
-        return launch_grouped<256, 256, 32, 2, 4, 4, 6>(phase, xp, perm_token, offsets, sel, nsel, tile_start, max_tiles,
-                                                 sp, H, I, (uint16_t *)h_ws, (uint16_t *)y, s);
+        // 128-byte row pieces (BK 64) halve the L2 requests of the 64-byte
+        // ones; each CU keeps about 64 requests in flight, so the bytes per
+        // request set its fill rate.  Fragments are read one MFMA K step (16)
+        // ahead, which keeps the tile within 256 VGPRs without spills, and
+        // split load roles with 2 + 3 stages fill the 160 KB of LDS
+        // (T=4096, Zipf routing: gate/up 338 -> 299 us, down 199 -> 173 us;
+        // uniform: down 190 -> 161 us; bit-identical)
+        return launch_grouped<256, 256, 64, 2, 4, 2, 3, false, 3, 1, 16>(phase, xp, perm_token, offsets, sel, nsel,
+                                                                         tile_start, max_tiles, sp, H, I,
+                                                                         (uint16_t *)h_ws, (uint16_t *)y, s);
     case 384:
         return launch_grouped<384, 128, 64, 4, 2, 2, 4, true>(phase, xp, perm_token, offsets, sel, nsel, tile_start,
                                                        max_tiles, sp, H, I, (uint16_t *)h_ws, (uint16_t *)y, s);

@@ -11,10 +11,12 @@ live as pinned host masters; the device holds a static hot set, speculative
 prefetch slots and demand staging slots, all sized so that the process's
 device memory stays within the budget:
 
-* the torch allocator is capped at budget - 1 GiB, as the reference does
-  (pdscope_compare.py:178-179), and checked at every layer call;
-* the expert slots are sized from the allocator cap minus a reserve for the
-  layer workspaces;
+* the torch allocator is capped below the budget, as the reference does
+  (pdscope_compare.py:178-179), by at least 1 GiB and at least the device
+  memory already in use outside the allocator plus a margin for its growth;
+  the cap is checked at every layer call;
+* the expert slots are sized from the allocator cap minus the bytes already
+  reserved and a reserve for the layer workspaces;
 * at the end of a run the allocator's peak plus the device memory in use
   outside the allocator must fit the budget (pdscope_compare.py:376-385);
 * the ledger must close: every submitted copy completed, no open demand,
@@ -106,18 +108,27 @@ class LayerCall:
 
 @dataclass
 class StackBudget:
-    """Device-memory budget of a stack session (bytes)."""
+    """Device-memory budget of a stack session (bytes).
+
+    The reference caps the allocator 1 GiB below the budget, leaving that
+    GiB to device memory outside the allocator (pdscope_compare.py:178-179).
+    Here that headroom is at least min_headroom and at least the memory
+    already in use outside the allocator when the session starts plus
+    external_growth (code objects loaded and graphs instantiated later);
+    the expert slots get what the allocator cap leaves after the bytes
+    already reserved and workspace_reserve for the layer workspaces."""
     device_total: int = 24 * GIB
-    allocator_headroom: int = 1 * GIB      # allocator cap = device_total - this
-    workspace_reserve: int = 1 * GIB       # allocator bytes kept out of the expert slots
+    min_headroom: int = 1 * GIB
+    external_growth: int = GIB // 2
+    workspace_reserve: int = GIB // 2
     demand_slots: int = 8
 
-    @property
-    def allocator_cap(self):
-        return self.device_total - self.allocator_headroom
-
-    def slots(self, expert_bytes):
-        return (self.allocator_cap - self.workspace_reserve) // expert_bytes
+    def plan(self, external_now, reserved_now, expert_bytes):
+        """(allocator cap, expert slots incl. demand slots) for a device whose
+        memory outside the allocator is external_now and whose allocator holds
+        reserved_now bytes."""
+        cap = self.device_total - max(self.min_headroom, external_now + self.external_growth)
+        return cap, max(0, (cap - reserved_now - self.workspace_reserve) // expert_bytes)
 
 
 @dataclass
@@ -135,21 +146,29 @@ class StackSession:
         total = torch.cuda.get_device_properties(self.device).total_memory
         if self.budget.device_total > total:
             raise ValueError("the device budget exceeds the device")
-        slots = self.budget.slots(self.expert_bytes)
+        torch.cuda.synchronize(self.device)
+        torch.cuda.empty_cache()
+        free, _ = torch.cuda.mem_get_info(self.device)
+        reserved = torch.cuda.memory_reserved(self.device)
+        self.external_at_start = max(0, total - free - reserved)
+        self.reserved_at_start = reserved
+        self.allocator_cap, slots = self.budget.plan(self.external_at_start, reserved, self.expert_bytes)
         self.speculative = slots - self.budget.demand_slots - len(m.hot)
         if self.speculative < 0:
             raise ValueError("hot set and staging slots exceed the device budget")
-        torch.cuda.synchronize(self.device)
-        torch.cuda.empty_cache()
         # the reference caps the allocator below the device budget
         # (pdscope_compare.py:178-179); restored by close()
-        torch.cuda.set_per_process_memory_fraction(self.budget.allocator_cap / total, self.device)
+        torch.cuda.set_per_process_memory_fraction(self.allocator_cap / total, self.device)
         torch.cuda.reset_peak_memory_stats(self.device)
         t0 = time.perf_counter()
-        self.runtime = PDScopeCudaRuntime(m.masters, hot_keys=m.hot, speculative_slots=self.speculative,
-                                          demand_slots=self.budget.demand_slots,
-                                          resident_graphs=self.resident_graphs, device=self.device,
-                                          diagnostics=self.diagnostics)
+        try:
+            self.runtime = PDScopeCudaRuntime(m.masters, hot_keys=m.hot, speculative_slots=self.speculative,
+                                              demand_slots=self.budget.demand_slots,
+                                              resident_graphs=self.resident_graphs, device=self.device,
+                                              diagnostics=self.diagnostics)
+        except BaseException:
+            torch.cuda.set_per_process_memory_fraction(1.0, self.device)
+            raise
         self.setup_s = time.perf_counter() - t0
 
     def close(self):
@@ -162,7 +181,7 @@ class StackSession:
         torch.cuda.set_per_process_memory_fraction(1.0, self.device)
 
     def _check_allocator(self):
-        if torch.cuda.memory_reserved(self.device) > self.budget.allocator_cap:
+        if torch.cuda.memory_reserved(self.device) > self.allocator_cap:
             raise MemoryError("GPU allocator cap exceeded")
 
     def run_pass(self, x, step, observe=None):
@@ -250,7 +269,8 @@ class StackSession:
         peak = torch.cuda.max_memory_reserved(dev)
         external = max(0, used - reserved)
         slots = len(self.model.hot) + self.speculative
-        rec = dict(device_budget_bytes=b.device_total, allocator_cap_bytes=b.allocator_cap,
+        rec = dict(device_budget_bytes=b.device_total, allocator_cap_bytes=self.allocator_cap,
+                   external_at_start_bytes=self.external_at_start, reserved_at_start_bytes=self.reserved_at_start,
                    cache_slots=slots, hot_slots=len(self.model.hot), speculative_slots=self.speculative,
                    demand_slots=b.demand_slots, expert_slot_bytes=(slots + b.demand_slots) * self.expert_bytes,
                    gpu_peak_allocated_bytes=torch.cuda.max_memory_allocated(dev), gpu_peak_reserved_bytes=peak,
