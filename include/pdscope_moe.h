@@ -89,8 +89,11 @@ int pdscope_pack(const int32_t *ids, int T, int k, int E, int32_t *counts, int32
  * device memory (code under hipGraph capture, tight serving loops, harnesses
  * that forbid hipMalloc).  Same arguments and outputs as pdscope_pack (bit
  * for bit); the multi-block path's per-chunk counts live in a library-owned
- * static device array of 512 KiB per GPU, looked up once per device on the
- * first call.  Limit: T*k <= pdscope_pack_static_max_ids() (1048576 ids);
+ * static device array of 512 KiB per GPU whose address is looked up once per
+ * device: by pdscope_pack_static_max_ids() with that device current (call it
+ * at set-up, before any capture; it returns 0 if the lookup fails), else by
+ * the first multi-block call.  Limit: T*k <= pdscope_pack_static_max_ids()
+ * (1048576 ids);
  * larger inputs return 1 (EINVAL).  Every call on one GPU shares that GPU's
  * array, so calls that overlap in time on one GPU (several streams or
  * threads) race; nothing in the array has to be cleared between calls.
@@ -102,10 +105,13 @@ int pdscope_pack_static(const int32_t *ids, int T, int k, int E, int32_t *counts
 /*
  * Tile schedule for pdscope_swiglu_grouped over a subset of experts:
  * tile_start[i] = sum_{j<i} ceil(counts[sel[j]] / block_m), i = 0..nsel.
+ * counts has E entries; a sel entry outside [0, E) counts as an expert with
+ * no rows (the same holds for the balanced schedules below and for the
+ * schedule written by pdscope_pack_schedule_balanced).
  * block_m is the row tile the grouped call will use (see
  * pdscope_grouped_block_m).
  */
-int pdscope_schedule(const int32_t *counts, const int32_t *sel, int nsel, int block_m,
+int pdscope_schedule(const int32_t *counts, int E, const int32_t *sel, int nsel, int block_m,
                      int32_t *tile_start, void *stream);
 
 /*
@@ -119,7 +125,7 @@ int pdscope_schedule(const int32_t *counts, const int32_t *sel, int nsel, int bl
  * No counterpart in the reference (its experts run one launch each).
  * Limits: nsel <= 256.
  */
-int pdscope_schedule_balanced(const int32_t *counts, const int32_t *sel, int nsel, int block_m,
+int pdscope_schedule_balanced(const int32_t *counts, int E, const int32_t *sel, int nsel, int block_m,
                               int32_t *order, int32_t *tile_start, void *stream);
 
 /*
@@ -128,8 +134,9 @@ int pdscope_schedule_balanced(const int32_t *counts, const int32_t *sel, int nse
  * launches take `order`; tile_start is its m-tile prefix for block_m and
  * tile_start2 for block_m2.  No counterpart in the reference.
  */
-int pdscope_schedule_balanced_pair(const int32_t *counts, const int32_t *sel, int nsel, int block_m, int block_m2,
-                                   int32_t *order, int32_t *tile_start, int32_t *tile_start2, void *stream);
+int pdscope_schedule_balanced_pair(const int32_t *counts, int E, const int32_t *sel, int nsel, int block_m,
+                                   int block_m2, int32_t *order, int32_t *tile_start, int32_t *tile_start2,
+                                   void *stream);
 
 /*
  * pdscope_pack followed by the balanced schedule of `sel` over the counts it
@@ -252,6 +259,17 @@ int pdscope_swiglu_decode(const void *x, const int32_t *ids, const void *w, int 
  */
 size_t pdscope_decode_workspace_bytes(void);
 int pdscope_decode_layer_supported(int H, int I, int E, int k);
+
+/*
+ * Whether pdscope_decode_layer_chained can run this shape on the current
+ * device: the checks of pdscope_decode_layer_supported, the next-layer
+ * predictor's grid condition when with_predictor is non-zero, and the
+ * co-residency of the chained variant's grid (it has its own registers and
+ * static LDS).  Replaces the graph-capture precondition of the reference's
+ * resident expert graphs (expertbench/executor.py:42-146), which only
+ * capture what can replay.
+ */
+int pdscope_decode_layer_chained_supported(int H, int I, int E, int k, int with_predictor);
 int pdscope_decode_layer(const void *x, const void *gate, const float *bias, int H, int E, int k,
                          int normalize, int merge_mode, const void *const *slots, int I, void *logits,
                          int32_t *ids, void *weights, float *probs, void *h_ws, void *out, void *workspace,
@@ -294,10 +312,12 @@ int pdscope_stage_expert(void *dst_slot, const void *pinned_src, size_t bytes, v
  * 124-129).  Copies host block [rows, row_bytes] into device scratch, then
  * for r = 0..rows-1 in order: out[tokens[r],:] += bf16(scratch[r,:]*weights[r])
  * with bf16 accumulation (one valid order of the reference's index_add_).
- * tokens int64 [rows], weights bf16 [rows], out bf16 [*, row_bytes/2].
+ * tokens int64 [rows], weights bf16 [rows], out bf16 [out_rows, row_bytes/2];
+ * a row whose token lies outside [0, out_rows) is skipped.
  */
 int pdscope_stage_merge(const void *host_block, int64_t rows, int64_t row_bytes, void *scratch,
-                        void *out, const int64_t *tokens, const void *weights, void *stream);
+                        void *out, const int64_t *tokens, const void *weights, int64_t out_rows,
+                        void *stream);
 
 /*
  * A9 native CPU-group tail, host half: replaces fill_packed and the id /

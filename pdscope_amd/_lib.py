@@ -27,9 +27,9 @@ SIGNATURES = {
     "pdscope_pack_workspace_size": ([_i32, _i32, _i32], _sz),
     "pdscope_pack_static": ([_vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp], _i32),
     "pdscope_pack_static_max_ids": ([], _sz),
-    "pdscope_schedule": ([_vp, _vp, _i32, _i32, _vp, _vp], _i32),
-    "pdscope_schedule_balanced": ([_vp, _vp, _i32, _i32, _vp, _vp, _vp], _i32),
-    "pdscope_schedule_balanced_pair": ([_vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp], _i32),
+    "pdscope_schedule": ([_vp, _i32, _vp, _i32, _i32, _vp, _vp], _i32),
+    "pdscope_schedule_balanced": ([_vp, _i32, _vp, _i32, _i32, _vp, _vp, _vp], _i32),
+    "pdscope_schedule_balanced_pair": ([_vp, _i32, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp], _i32),
     "pdscope_pack_schedule_balanced": ([_vp, _i32, _i32, _i32] + [_vp] * 6 + [_vp, _i32, _i32, _i32] + [_vp] * 4,
                                        _i32),
     "pdscope_grouped_block_m": ([_i32], _i32),
@@ -42,12 +42,13 @@ SIGNATURES = {
     "pdscope_swiglu_decode": ([_vp, _vp, _vp, _i32, _vp, _i32, _i32, _vp, _vp, _i32, _vp], _i32),
     "pdscope_decode_workspace_bytes": ([], _sz),
     "pdscope_decode_layer_supported": ([_i32, _i32, _i32, _i32], _i32),
+    "pdscope_decode_layer_chained_supported": ([_i32, _i32, _i32, _i32, _i32], _i32),
     "pdscope_decode_layer": ([_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
                               _vp, _vp], _i32),
     "pdscope_decode_layer_chained": ([_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _i32, _vp, _vp,
                                       _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp], _i32),
     "pdscope_stage_expert": ([_vp, _vp, _sz, _vp, _vp], _i32),
-    "pdscope_stage_merge": ([_vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp], _i32),
+    "pdscope_stage_merge": ([_vp, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _vp], _i32),
     "pdscope_dispatch_pack": ([_vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp], _i32),
 }
 

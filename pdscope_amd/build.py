@@ -1,10 +1,14 @@
-"""Build libpdscope_moe.so (gfx950) in-tree with hipcc.
+"""Build libpdscope_moe.so (gfx950) and the pdscope_layer_dispatch extension in-tree.
 
     python -m pdscope_amd.build          # or __graft_entry__.build()
 
 Every .hip file under pdscope_amd/csrc is compiled to an object in
 pdscope_amd/_build/ (in parallel), then linked into
-pdscope_amd/libpdscope_moe.so next to this file.
+pdscope_amd/libpdscope_moe.so next to this file.  The CPython extension
+module pdscope_layer_dispatch (csrc/layer_dispatch_module.cpp, host code only)
+is compiled with the host C++ compiler into
+pdscope_amd/pdscope_layer_dispatch<EXT_SUFFIX>; it loads the HIP library at
+import.
 """
 from __future__ import annotations
 
@@ -12,6 +16,7 @@ import os
 import shutil
 import subprocess
 import sys
+import sysconfig
 from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
@@ -65,7 +70,29 @@ def build(verbose: bool = False) -> Path:
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB} from {len(sources)} sources", file=sys.stderr)
+    mod = build_dispatch_module()
+    if verbose:
+        print(f"built {mod}", file=sys.stderr)
     return LIB
+
+
+DISPATCH_SRC = CSRC / "layer_dispatch_module.cpp"
+DISPATCH_MODULE = PKG / ("pdscope_layer_dispatch" + (sysconfig.get_config_var("EXT_SUFFIX") or ".so"))
+
+
+def build_dispatch_module() -> Path:
+    """The pdscope_layer_dispatch extension (plain CPython API, no GPU code)."""
+    cxx = shutil.which("g++") or shutil.which("c++")
+    if cxx is None:
+        raise RuntimeError("no host C++ compiler for the pdscope_layer_dispatch extension")
+    tmp = DISPATCH_MODULE.with_name(DISPATCH_MODULE.name + ".tmp")
+    cmd = [cxx, "-O2", "-std=c++17", "-shared", "-fPIC", "-fvisibility=hidden", "-Wall", "-Wextra",
+           f"-I{sysconfig.get_paths()['include']}", str(DISPATCH_SRC), "-o", str(tmp), "-ldl"]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"pdscope_layer_dispatch build failed:\n{proc.stderr[-6000:]}")
+    os.replace(tmp, DISPATCH_MODULE)
+    return DISPATCH_MODULE
 
 
 if __name__ == "__main__":

@@ -646,6 +646,17 @@ PD_API int pdscope_decode_layer_supported(int H, int I, int E, int k) {
     return n >= plan.blocks ? 1 : 0;
 }
 
+PD_API int pdscope_decode_layer_chained_supported(int H, int I, int E, int k, int with_predictor) {
+    if (!pdscope_decode_layer_supported(H, I, E, k)) return 0;
+    if (with_predictor && 2 * ((E + 3) / 4) > (H + 3) / 4) return 0;
+    DecodePlan plan;
+    std::string why;
+    if (pick_decode(H, I, k, &plan, &why) != kOk) return 0;
+    // the chained variant has its own registers and static LDS
+    const int n = resident_blocks(plan.fn_chain, plan.lds, &why);
+    return n >= plan.blocks ? 1 : 0;
+}
+
 // Shared by both entry points: checks, plan, launch.
 static int launch_decode_layer(const void *x, const void *resid, void *x_out, const void *gate, const float *bias,
                                int H, int E, int k, int normalize, int merge_mode, const void *const *slots, int I,

@@ -133,14 +133,17 @@ __global__ __launch_bounds__(256) void merge_kernel(const uint16_t *__restrict__
     }
 }
 
+// rows whose token lies outside [0, out_rows) are skipped (never written)
 __global__ __launch_bounds__(256) void stage_merge_kernel(const uint16_t *__restrict__ scratch, int64_t rows,
                                                           int H, const int64_t *__restrict__ tokens,
-                                                          const uint16_t *__restrict__ weights,
+                                                          const uint16_t *__restrict__ weights, int64_t out_rows,
                                                           uint16_t *__restrict__ out) {
     const int j = blockIdx.x * blockDim.x + threadIdx.x;
     if (j >= H) return;
     for (int64_t r = 0; r < rows; ++r) {
-        const size_t o = (size_t)tokens[r] * H + j;
+        const int64_t t = tokens[r];
+        if (t < 0 || t >= out_rows) continue;
+        const size_t o = (size_t)t * H + j;
         const float prod = bf16_round(bf2f(scratch[(size_t)r * H + j]) * bf2f(weights[r]));
         out[o] = (uint16_t)f2bf(bf2f(out[o]) + prod);
     }
@@ -183,14 +186,16 @@ PD_API int pdscope_merge_ordered(const void *y, const int32_t *row_of, const voi
 }
 
 PD_API int pdscope_stage_merge(const void *host_block, int64_t rows, int64_t row_bytes, void *scratch,
-                               void *out, const int64_t *tokens, const void *weights, void *stream) {
+                               void *out, const int64_t *tokens, const void *weights, int64_t out_rows,
+                               void *stream) {
     if (!host_block || !scratch || !out || !tokens || !weights) return fail(kEInval, "stage_merge: null pointer");
     if (rows < 1 || row_bytes < 2 || row_bytes % 2) return fail(kEInval, "invalid decode pack shape");
+    if (out_rows < 1) return fail(kEInval, "stage_merge: out needs at least one row");
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     hipError_t err = hipMemcpyAsync(scratch, host_block, (size_t)rows * (size_t)row_bytes, hipMemcpyHostToDevice, s);
     if (err != hipSuccess) return fail(kEHip, std::string("hipMemcpyAsync(stage): ") + hipGetErrorString(err));
     const int H = (int)(row_bytes / 2);
     stage_merge_kernel<<<(H + 255) / 256, 256, 0, s>>>((const uint16_t *)scratch, rows, H, tokens,
-                                                       (const uint16_t *)weights, (uint16_t *)out);
+                                                       (const uint16_t *)weights, out_rows, (uint16_t *)out);
     return check_launch("stage_merge_kernel");
 }

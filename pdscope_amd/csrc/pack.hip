@@ -49,13 +49,19 @@ __device__ int block_scan256(int v, int *s_wsum) {
 
 // The balanced order and tile prefixes, computed by threads 0..255 of the
 // calling block (every thread of the block must call it: it synchronises).
-// rows[e]: rows of expert e (global or LDS); s_rows / s_at: 256 ints of LDS
-// each (s_rows 16-byte aligned), s_wsum: 4 ints.
-__device__ void balanced_schedule(const int32_t *rows, const int32_t *__restrict__ sel, int nsel, int bm,
+// rows[e]: rows of expert e < E (global or LDS); a sel entry outside [0, E)
+// counts as an expert with no rows (no tiles: the grouped launch never
+// addresses it).  s_rows / s_at: 256 ints of LDS each (s_rows 16-byte
+// aligned), s_wsum: 4 ints.
+__device__ void balanced_schedule(const int32_t *rows, int E, const int32_t *__restrict__ sel, int nsel, int bm,
                                   int32_t *__restrict__ order, int32_t *__restrict__ tile_start, int bm2,
                                   int32_t *__restrict__ tile_start2, int *s_rows, int *s_at, int *s_wsum) {
     const int i = threadIdx.x;
-    if (i < 256) s_rows[i] = i < nsel ? rows[sel[i]] : -1;  // -1 past nsel: never ranks above a real expert
+    if (i < 256) {
+        const int e = i < nsel ? sel[i] : -1;
+        // -1 past nsel: never ranks above a real expert
+        s_rows[i] = i < nsel ? ((unsigned)e < (unsigned)E ? rows[e] : 0) : -1;
+    }
     __syncthreads();
     if (i < nsel) {
         const int c = s_rows[i];
@@ -138,8 +144,8 @@ __device__ void pack_then_schedule(const PackSchedule &ps, int E, int tot) {
     __shared__ int s_ws2[4];
     if (threadIdx.x < E) s_tot[threadIdx.x] = tot;
     __syncthreads();
-    balanced_schedule(s_tot, ps.sel, ps.nsel, ps.bm, ps.order, ps.tile_start, ps.bm2, ps.tile_start2, s_rows, s_at,
-                      s_ws2);
+    balanced_schedule(s_tot, E, ps.sel, ps.nsel, ps.bm, ps.order, ps.tile_start, ps.bm2, ps.tile_start2, s_rows,
+                      s_at, s_ws2);
 }
 
 __global__ __launch_bounds__(1024) void pack_kernel(const int32_t *__restrict__ ids, int T, int k, int E,
@@ -348,7 +354,8 @@ __global__ __launch_bounds__(1024) void pack_scatter_kernel(const int32_t *__res
     }
 }
 
-__global__ __launch_bounds__(256) void schedule_kernel(const int32_t *__restrict__ counts,
+// a sel entry outside [0, E) counts as an expert with no rows
+__global__ __launch_bounds__(256) void schedule_kernel(const int32_t *__restrict__ counts, int E,
                                                        const int32_t *__restrict__ sel, int nsel, int bm,
                                                        int32_t *__restrict__ tile_start) {
     __shared__ int s_wsum[4];
@@ -360,7 +367,8 @@ __global__ __launch_bounds__(256) void schedule_kernel(const int32_t *__restrict
     __syncthreads();
     for (int base = 0; base < nsel; base += 256) {
         const int i = base + threadIdx.x;
-        const int tiles = i < nsel ? (counts[sel[i]] + bm - 1) / bm : 0;
+        const int e = i < nsel ? sel[i] : -1;
+        const int tiles = (unsigned)e < (unsigned)E ? (counts[e] + bm - 1) / bm : 0;
         const int incl = block_scan256(tiles, s_wsum);
         if (i < nsel) tile_start[i + 1] = s_carry + incl;
         __syncthreads();
@@ -379,7 +387,7 @@ __global__ __launch_bounds__(256) void schedule_kernel(const int32_t *__restrict
 // tile_start its m-tile prefix (as schedule_kernel over `order`).  nsel <= 256.
 // With tile_start2, the same order's m-tile prefix for a second row tile bm2
 // (the order depends on the rows only, not on the tile).
-__global__ __launch_bounds__(256) void schedule_balanced_kernel(const int32_t *__restrict__ counts,
+__global__ __launch_bounds__(256) void schedule_balanced_kernel(const int32_t *__restrict__ counts, int E,
                                                                 const int32_t *__restrict__ sel, int nsel, int bm,
                                                                 int32_t *__restrict__ order,
                                                                 int32_t *__restrict__ tile_start, int bm2,
@@ -387,7 +395,7 @@ __global__ __launch_bounds__(256) void schedule_balanced_kernel(const int32_t *_
     __shared__ __align__(16) int s_rows[256];
     __shared__ int s_at[256];  // list position -> sel position
     __shared__ int s_wsum[4];
-    balanced_schedule(counts, sel, nsel, bm, order, tile_start, bm2, tile_start2, s_rows, s_at, s_wsum);
+    balanced_schedule(counts, E, sel, nsel, bm, order, tile_start, bm2, tile_start2, s_rows, s_at, s_wsum);
 }
 
 }  // namespace pd
@@ -486,7 +494,15 @@ static int pack_scratch(int32_t **out) {
     return kOk;
 }
 
-PD_API size_t pdscope_pack_static_max_ids(void) { return (size_t)kPackStaticMaxIds; }
+// The id limit of pdscope_pack_static.  Also resolves the static array's
+// address on the current device, so a caller that sizes its inputs at set-up
+// pays that lookup there, outside any stream capture; returns 0 (with the
+// error message set) if the lookup fails.
+PD_API size_t pdscope_pack_static_max_ids(void) {
+    int32_t *p = nullptr;
+    if (pack_scratch(&p) != kOk) return 0;
+    return (size_t)kPackStaticMaxIds;
+}
 
 PD_API int pdscope_pack_static(const int32_t *ids, int T, int k, int E, int32_t *counts, int32_t *offsets,
                                int32_t *perm_token, int32_t *perm_pos, int32_t *row_of, void *stream) {
@@ -505,35 +521,36 @@ PD_API int pdscope_pack_static(const int32_t *ids, int T, int k, int E, int32_t 
     return pdscope_pack(ids, T, k, E, counts, offsets, perm_token, perm_pos, row_of, hist, stream);
 }
 
-PD_API int pdscope_schedule(const int32_t *counts, const int32_t *sel, int nsel, int block_m,
+PD_API int pdscope_schedule(const int32_t *counts, int E, const int32_t *sel, int nsel, int block_m,
                             int32_t *tile_start, void *stream) {
-    if (!counts || !sel || !tile_start || nsel < 0) return fail(kEInval, "schedule: bad arguments");
+    if (!counts || !sel || !tile_start || nsel < 0 || E < 1) return fail(kEInval, "schedule: bad arguments");
     if (block_m != 32 && block_m != 64 && block_m != 128 && block_m != 256 && block_m != 384)
         return fail(kEInval, "schedule: block_m must be 32, 64, 128, 256 or 384");
-    schedule_kernel<<<1, 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(counts, sel, nsel, block_m, tile_start);
+    schedule_kernel<<<1, 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(counts, E, sel, nsel, block_m, tile_start);
     return check_launch("schedule_kernel");
 }
 
-PD_API int pdscope_schedule_balanced(const int32_t *counts, const int32_t *sel, int nsel, int block_m,
+PD_API int pdscope_schedule_balanced(const int32_t *counts, int E, const int32_t *sel, int nsel, int block_m,
                                      int32_t *order, int32_t *tile_start, void *stream) {
-    if (!counts || !sel || !order || !tile_start || nsel < 0 || nsel > 256)
+    if (!counts || !sel || !order || !tile_start || nsel < 0 || nsel > 256 || E < 1)
         return fail(kEInval, "schedule_balanced: bad arguments (nsel must be 0..256)");
     if (block_m != 32 && block_m != 64 && block_m != 128 && block_m != 256 && block_m != 384)
         return fail(kEInval, "schedule_balanced: block_m must be 32, 64, 128, 256 or 384");
-    schedule_balanced_kernel<<<1, 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(counts, sel, nsel, block_m, order,
-                                                                                   tile_start, 0, nullptr);
+    schedule_balanced_kernel<<<1, 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(counts, E, sel, nsel, block_m,
+                                                                                   order, tile_start, 0, nullptr);
     return check_launch("schedule_balanced_kernel");
 }
 
-PD_API int pdscope_schedule_balanced_pair(const int32_t *counts, const int32_t *sel, int nsel, int block_m,
+PD_API int pdscope_schedule_balanced_pair(const int32_t *counts, int E, const int32_t *sel, int nsel, int block_m,
                                           int block_m2, int32_t *order, int32_t *tile_start, int32_t *tile_start2,
                                           void *stream) {
-    if (!counts || !sel || !order || !tile_start || !tile_start2 || nsel < 0 || nsel > 256)
+    if (!counts || !sel || !order || !tile_start || !tile_start2 || nsel < 0 || nsel > 256 || E < 1)
         return fail(kEInval, "schedule_balanced_pair: bad arguments (nsel must be 0..256)");
     for (int b : {block_m, block_m2})
         if (b != 32 && b != 64 && b != 128 && b != 256 && b != 384)
             return fail(kEInval, "schedule_balanced_pair: block sizes must be 32, 64, 128, 256 or 384");
-    schedule_balanced_kernel<<<1, 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(counts, sel, nsel, block_m, order,
-                                                                                   tile_start, block_m2, tile_start2);
+    schedule_balanced_kernel<<<1, 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(counts, E, sel, nsel, block_m,
+                                                                                   order, tile_start, block_m2,
+                                                                                   tile_start2);
     return check_launch("schedule_balanced_kernel");
 }

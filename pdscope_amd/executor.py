@@ -23,6 +23,9 @@ from __future__ import annotations
 
 import contextlib
 import ctypes
+import os
+import threading
+import time
 from dataclasses import dataclass, field
 
 import torch
@@ -91,6 +94,7 @@ class PendingCompute:
     event: object
     input_ref: object
     keys: tuple = ()
+    timing_start: object = None   # start event of the launch when stages are profiled
 
 
 class _PinnedRing:
@@ -115,10 +119,35 @@ class _PinnedRing:
 
 
 class ExpertExecutor:
-    def __init__(self, cache, masters, device=0, *, pinned_source_mode="all_masters", capture_events=True,
-                 streams=None, cpu_backend=None, cache_storage=None, staging_storage=None, profile_stages=False):
+    """Expert copies, launches and CPU calls under the ledger (expertbench/executor.py:165-596).
+
+    profile_stages records per-stage times in ``stage_timings`` as the
+    reference does (executor.py:352-355, 384-385, 472-481, 518-528): the device
+    span of each expert copy (``weight_dma_gpu_span_ms``), the host time to
+    submit a grouped launch (``gpu_forward_host_submit_ms``) and its device
+    span (``gpu_forward_device_span_ms``), the host time of pinning a master
+    on first use (``source_copy_ms``) and a CPU expert call's time on the
+    worker (``cpu_forward_ms``); each key holds the latest value.
+    initialize_cpu_worker: the worker thread that runs a callable CPU backend
+    first sets torch's thread count to the control thread's (its result is
+    ``cpu_worker_init``).  cpu_staging_copy: how a master that is not already
+    one pinned block is copied into one ("torch": tensor copies, "memcpy":
+    byte copies of contiguous tensors)."""
+
+    def __init__(self, cache, masters, device=0, *, pinned_source_mode="all_masters", profile_stages=False,
+                 capture_events=True, streams=None, initialize_cpu_worker=True, cpu_backend=None,
+                 cpu_staging_copy="torch", cache_storage=None, staging_storage=None):
         if pinned_source_mode not in ("all_masters", "lazy_pinned"):
             raise ValueError("unknown pinned source mode")
+        if cpu_staging_copy not in ("torch", "memcpy"):
+            raise ValueError("unknown CPU staging copy implementation")
+        if type(initialize_cpu_worker) is not bool:
+            raise ValueError("CPU worker initialization must be explicitly boolean")
+        if type(profile_stages) is not bool:
+            raise ValueError("stage profiling must be explicitly boolean")
+        self.cpu_staging_copy, self.initialize_cpu_worker = cpu_staging_copy, initialize_cpu_worker
+        self.cpu_worker_init = None
+        self.stage_timings, self._load_starts = {}, {}
         if cpu_backend is not None and not callable(cpu_backend):
             raise ValueError("CPU backend must be an explicit callable")
         self.cache, self.masters = cache, dict(masters)
@@ -211,13 +240,21 @@ class ExpertExecutor:
         flat = w.flat
         if flat is not None and flat.is_pinned() and flat.is_contiguous():
             return flat.view(torch.uint8) if flat.dtype != torch.uint8 else flat
+        started = time.perf_counter_ns() if self.profile_stages else None
         block = torch.empty(self.expert_bytes, dtype=torch.uint8, pin_memory=True)
         off = 0
         for name in PROJECTIONS:
-            t = w.tensors[name].contiguous()
+            t = w.tensors[name]
             n = t.numel() * t.element_size()
-            block[off:off + n].copy_(t.view(torch.uint8).reshape(-1))
+            if self.cpu_staging_copy == "memcpy":
+                if not t.is_contiguous():
+                    raise ValueError("byte staging requires contiguous BF16 master tensors")
+                ctypes.memmove(block.data_ptr() + off, t.data_ptr(), n)
+            else:
+                block[off:off + n].copy_(t.contiguous().view(torch.uint8).reshape(-1))
             off += n
+        if started is not None:
+            self.stage_timings["source_copy_ms"] = (time.perf_counter_ns() - started) / 1e6
         return block
 
     def prepare_source(self, key):
@@ -233,7 +270,7 @@ class ExpertExecutor:
             raise RuntimeError("executor has been shut down; its ledger cannot be reused")
 
     def _event(self):
-        return self._free_events.pop() if self._free_events else torch.cuda.Event()
+        return self._free_events.pop() if self._free_events else torch.cuda.Event(enable_timing=self.profile_stages)
 
     def _log(self, **kw):
         if self.capture_events:
@@ -355,6 +392,10 @@ class ExpertExecutor:
             flat = self.cache_storage[slot * self.expert_bytes:(slot + 1) * self.expert_bytes]
         self.copies[ticket] = flat
         self.cache.submit(ticket)
+        if self.profile_stages:
+            start = torch.cuda.Event(enable_timing=True)
+            start.record(self.load_stream)
+            self._load_starts[ticket] = start
         ev = self._event()
         ops.stage_expert(flat, src, event=ev, stream=self.load_stream)
         self.loads[ticket] = ev
@@ -371,6 +412,9 @@ class ExpertExecutor:
             return False
         self.cache.complete_load(ticket)
         del self.loads[ticket]
+        start = self._load_starts.pop(ticket, None)
+        if start is not None:
+            self.stage_timings["weight_dma_gpu_span_ms"] = start.elapsed_time(ev)
         # kept until the copy's first consumer is launched, which waits on it
         # on the compute stream (gpu_group)
         self._landed[ticket] = ev
@@ -392,13 +436,20 @@ class ExpertExecutor:
             self._group_stream_ctx.__exit__(None, None, None)
             self._group_stream_ctx = None
 
-    def gpu_group(self, keys, launch, *, input_ref=None, wait_for=None):
+    def gpu_group(self, keys, launch, *, input_ref=None, wait_for=None, completed=None):
         """Acquire `keys`, run `launch()` (one grouped launch) on the compute stream, record one event.
 
-        With launch=None the work reading these copies is already enqueued on
-        `wait_for` (a replay issued before the reveal): the uses are accounted
-        and the event is recorded on that stream, with no compute-stream join."""
+        With launch=None the work that read these copies was enqueued on
+        `wait_for` before the ledger revealed them (a replay issued ahead of
+        the reveal): the uses are accounted and the event is recorded on that
+        stream, with no compute-stream join.  The copies were not held while
+        that work ran, so it must already have finished: `completed` is an
+        event recorded after it, and it must have completed (the caller
+        synchronised on it) or the call raises."""
         self._open()
+        if launch is None and (completed is None or not completed.query()):
+            raise RuntimeError("an already enqueued use of expert copies is accounted only after it has "
+                               "completed: pass the completed event recorded after it")
         handles = tuple(self.cache.acquire(k) for k in keys)
         for h in handles:
             if h.ticket not in self.copies or h.ticket in self.loads:
@@ -432,10 +483,17 @@ class ExpertExecutor:
             if self.consume_hook is not None:
                 for h in handles:
                     self.consume_hook(h.ticket.key, self.copies[h.ticket])
+            start = None
+            if self.profile_stages:
+                start = torch.cuda.Event(enable_timing=True)
+                start.record(self.compute_stream)
+                submit_start = time.perf_counter_ns()
             output = launch()
+            if start is not None:
+                self.stage_timings["gpu_forward_host_submit_ms"] = (time.perf_counter_ns() - submit_start) / 1e6
             ev = self._event()
             ev.record(self.compute_stream)
-        p = PendingCompute(handles, output, ev, input_ref, tuple(keys))
+        p = PendingCompute(handles, output, ev, input_ref, tuple(keys), start)
         self.computes[id(p)] = p
         self._log(event="compute_submitted", experts=len(keys))
         return p
@@ -451,6 +509,9 @@ class ExpertExecutor:
         for h in pending.handles:
             self.cache.release(h)
         del self.computes[id(pending)]
+        if pending.timing_start is not None:
+            self.stage_timings["gpu_forward_device_span_ms"] = pending.timing_start.elapsed_time(pending.event)
+            pending.timing_start = None
         self._free_events.append(pending.event)
         pending.event, pending.input_ref = None, None
         self.reclaim()
@@ -499,8 +560,23 @@ class ExpertExecutor:
         else:
             if self._cpu_pool is None:
                 from concurrent.futures import ThreadPoolExecutor
-                self._cpu_pool = ThreadPoolExecutor(max_workers=1, thread_name_prefix="pdscope-cpu")
-            future = self._cpu_pool.submit(backend, key, inputs)
+                expected = torch.get_num_threads()
+
+                def initialize():
+                    torch.set_num_threads(expected)
+                    self.cpu_worker_init = dict(expected_threads=expected, torch_threads=torch.get_num_threads(),
+                                                native_thread_id=threading.get_native_id(),
+                                                affinity=sorted(os.sched_getaffinity(0)))
+                self._cpu_pool = ThreadPoolExecutor(max_workers=1, thread_name_prefix="pdscope-cpu",
+                                                    initializer=initialize if self.initialize_cpu_worker else None)
+
+            def work():
+                started = time.perf_counter_ns()
+                out = backend(key, inputs)
+                if isinstance(out, tuple):  # (output, timing) as the reference's pool returns
+                    out = out[0]
+                return out, (time.perf_counter_ns() - started) / 1e6
+            future = self._cpu_pool.submit(work)
         pending = PendingCpu(key, future, inputs)
         self._cpu_tasks[key] = pending
         return pending
@@ -515,7 +591,9 @@ class ExpertExecutor:
             return None
         out = pending.future.result()
         if isinstance(out, tuple):  # (output, timing) as the reference's pool returns
-            out = out[0]
+            out, timing = out[0], out[1] if len(out) > 1 else None
+            if self.profile_stages and isinstance(timing, (int, float)):
+                self.stage_timings["cpu_forward_ms"] = float(timing)
         if (not isinstance(out, torch.Tensor) or out.device.type != "cpu" or out.dtype != torch.bfloat16
                 or tuple(out.shape) != tuple(pending.input_ref.shape)):
             raise ValueError("CPU backend must return completed unweighted CPU BF16 input-shaped output")

@@ -202,7 +202,7 @@ def moe_forward(x, gate, slots, ws: MoEWorkspace, *, normalize=True, bias=None, 
     shared_slot (int64 [1] device table) adds always-on shared experts
     (DeepSeek-V2); the workspace must have been built with shared_I.
     next_gate / pred_out (T == 1 on the single-launch kernel only, see
-    ops.decode_predictor_fits): the next layer's gate-fallback prediction,
+    ops.decode_chained_supported): the next layer's gate-fallback prediction,
     top-k of next_gate . x, is written to pred_out [k] int32 by the same launch.
     """
     T = x.shape[0]
@@ -225,7 +225,7 @@ def moe_forward(x, gate, slots, ws: MoEWorkspace, *, normalize=True, bias=None, 
              and ops.decode_layer_supported(ws.H, ws.I, ws.E, ws.k, x.device))
     if (next_gate is None) != (pred_out is None):
         raise ValueError("next_gate and pred_out go together")
-    if next_gate is not None and not (fused and ops.decode_predictor_fits(ws.H, ws.E)):
+    if next_gate is not None and not (fused and ops.decode_chained_supported(ws.H, ws.I, ws.E, ws.k, x.device)):
         raise ValueError("the fused next-layer prediction needs one token on the single-launch decode kernel "
                          "with E <= H/2")
     if fused:

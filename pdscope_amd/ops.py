@@ -161,17 +161,34 @@ def pack(ids, E, out: Packed | None = None, workspace=None, *, schedule=None) ->
     return out
 
 
-def pack_static_max_ids() -> int:
-    return int(_lib.load().pdscope_pack_static_max_ids())
+_static_ready = set()
+
+
+def pack_static_max_ids(device=None) -> int:
+    """The id limit of pack_static; also looks up the library's static
+    scratch on `device` (default: the current one), so a caller that sizes
+    its inputs at set-up pays that lookup outside any graph capture."""
+    device = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    if device.index is None:
+        device = torch.device(device.type, torch.cuda.current_device())
+    with torch.cuda.device(device):
+        n = int(_lib.load().pdscope_pack_static_max_ids())
+    if n == 0:
+        raise _lib.PDScopeError("pdscope_pack_static_max_ids: " + _lib.load().pdscope_last_error().decode())
+    _static_ready.add(device)
+    return n
 
 
 def pack_static(ids, E, out: Packed) -> Packed:
     """pack() through the entry point that allocates nothing (its multi-block
     scratch is a library-owned device array; calls overlapping in time on
-    one GPU race).  All outputs are caller-provided."""
+    one GPU race).  All outputs are caller-provided.  The first call on a
+    device looks the scratch up (pack_static_max_ids) unless that was done."""
     _need(ids, "ids", torch.int32, 2)
     T, k = ids.shape
     dev = ids.device
+    if dev not in _static_ready:
+        pack_static_max_ids(dev)
     for t, n, size in ((out.counts, "counts", E), (out.offsets, "offsets", E + 1), (out.perm_token, "perm_token", T * k),
                        (out.perm_pos, "perm_pos", T * k), (out.row_of, "row_of", T * k)):
         _need(t, n, torch.int32, None, dev)
@@ -193,7 +210,8 @@ def grouped_block_m(rows_hint: int, max_rows: int | None = None) -> int:
 def schedule(counts, sel, block_m, out=None, order=None, *, block_m2=None, out2=None):
     """Tile prefix over `sel` (order=None), or, with an int32 [nsel] `order`
     buffer, the balanced order of pdscope_schedule_balanced and the prefix
-    over it: the grouped launch must then take `order` as its sel.  With
+    over it: the grouped launch must then take `order` as its sel.  A sel
+    entry outside [0, counts.numel()) counts as an expert with no rows.  With
     block_m2 and out2 (balanced only), out2 receives the same order's prefix
     for a second row tile, from the same launch."""
     _need(counts, "counts", torch.int32, 1)
@@ -206,18 +224,18 @@ def schedule(counts, sel, block_m, out=None, order=None, *, block_m2=None, out2=
         _need(out2, "out2", torch.int32, 1, counts.device)
         if order.numel() < sel.numel() or out2.numel() < sel.numel() + 1:
             raise ValueError("order / out2 buffers smaller than sel")
-        _lib.call("pdscope_schedule_balanced_pair", _p(counts), _p(sel), sel.numel(), block_m, block_m2, _p(order),
-                  _p(tile_start), _p(out2), _stream(counts.device))
+        _lib.call("pdscope_schedule_balanced_pair", _p(counts), counts.numel(), _p(sel), sel.numel(), block_m,
+                  block_m2, _p(order), _p(tile_start), _p(out2), _stream(counts.device))
         return tile_start
     if order is None:
-        _lib.call("pdscope_schedule", _p(counts), _p(sel), sel.numel(), block_m, _p(tile_start),
+        _lib.call("pdscope_schedule", _p(counts), counts.numel(), _p(sel), sel.numel(), block_m, _p(tile_start),
                   _stream(counts.device))
     else:
         _need(order, "order", torch.int32, 1, counts.device)
         if order.numel() < sel.numel():
             raise ValueError("order buffer smaller than sel")
-        _lib.call("pdscope_schedule_balanced", _p(counts), _p(sel), sel.numel(), block_m, _p(order), _p(tile_start),
-                  _stream(counts.device))
+        _lib.call("pdscope_schedule_balanced", _p(counts), counts.numel(), _p(sel), sel.numel(), block_m, _p(order),
+                  _p(tile_start), _stream(counts.device))
     return tile_start
 
 
@@ -325,10 +343,24 @@ def decode_layer_supported(H, I, E, k, device) -> bool:
     return ok
 
 
-def decode_predictor_fits(H, E) -> bool:
-    """Whether the single-launch decode kernel can also compute the next
-    layer's prediction (its router and predictor blocks both fit the grid)."""
-    return 2 * ((E + 3) // 4) <= (H + 3) // 4
+_chain_ok = {}
+
+
+def decode_chained_supported(H, I, E, k, device, *, predictor=True) -> bool:
+    """Whether the chained single-launch decode kernel (residual input and/or
+    next-layer prediction) runs this shape on `device`: its grid must be
+    co-resident, which the chained variant's extra registers and LDS can
+    prevent where the plain kernel fits."""
+    device = torch.device(device)
+    if device.index is None:
+        device = torch.device(device.type, torch.cuda.current_device())
+    key = (device, H, I, E, k, bool(predictor))
+    ok = _chain_ok.get(key)
+    if ok is None:
+        with torch.cuda.device(key[0]):
+            ok = bool(_lib.load().pdscope_decode_layer_chained_supported(H, I, E, k, int(bool(predictor))))
+        _chain_ok[key] = ok
+    return ok
 
 
 def decode_layer(x, gate, slots, I, top_k, normalize, *, bias=None, out, logits, ids, weights, h_ws, probs=None,
@@ -429,6 +461,8 @@ def stage_merge(host_block_ptr, rows, row_bytes, scratch, out, tokens, weights):
     _need(weights, "weights", BF16, None, dev)
     if scratch.numel() * 2 != rows * row_bytes:
         raise RuntimeError("scratch buffer must match the packed block")
+    if out.dim() != 2 or out.shape[1] * 2 != row_bytes or tokens.numel() != rows or weights.numel() != rows:
+        raise RuntimeError("out must be [tokens, row_bytes / 2]; tokens and weights one entry per row")
     _lib.call("pdscope_stage_merge", ctypes.c_void_p(int(host_block_ptr)), int(rows), int(row_bytes), _p(scratch),
-              _p(out), _p(tokens), _p(weights), _stream(dev))
+              _p(out), _p(tokens), _p(weights), int(out.shape[0]), _stream(dev))
     return out

@@ -259,7 +259,8 @@ class PDScopeCudaRuntime:
         out = torch.empty((T, H), dtype=torch.bfloat16, device=self.device)
         predict = prefetch and next_gate is not None
         # the graph's launch also predicts the next layer where its grid allows
-        graph_pred = next_gate if (graph_path and predict and ops.decode_predictor_fits(H, E)) else None
+        graph_pred = next_gate if (graph_path and predict
+                                   and ops.decode_chained_supported(H, self.I, E, k, self.device)) else None
         pred_ids = None
         if graph_path:
             # entries the first replay saw (a copy still in flight reads as null)
@@ -426,8 +427,11 @@ class PDScopeCudaRuntime:
                         self._replay_decode_graph(layer, x, gate, normalize, k, out, ring=ring,
                                                   next_gate=graph_pred)
                 else:
-                    launch = None  # the replay on `cur` already produced `out`; account the uses it made
-                tasks.append(ex.gpu_group([key(e) for e in resident], launch, input_ref=x, wait_for=cur))
+                    # the replay on `cur` already produced `out` (the host waited
+                    # for it through _copy_done): account the uses it made
+                    launch = None
+                tasks.append(ex.gpu_group([key(e) for e in resident], launch, input_ref=x, wait_for=cur,
+                                          completed=self._copy_done))
         elif resident:
             ex.table(layer, E)
             require_copies(resident if not decode_fast else sorted(counts))

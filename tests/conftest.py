@@ -35,3 +35,27 @@ def orc():
     from oracle import oracle
     oracle.build()
     return oracle
+
+
+@pytest.fixture(scope="session")
+def dispatch_via_reference_loader(tmp_path_factory):
+    """The built pdscope_layer_dispatch extension, loaded the way the
+    reference driver loads its native module (benchmarks/pdscope_compare.py:
+    39-52): the first match of the glob
+    expertbench/native-build/layer-dispatch/pdscope_layer_dispatch*.so under
+    the tree's root, then spec_from_file_location / module_from_spec /
+    exec_module, then the submit_and_merge check.  The file is placed there
+    as a symlink to the package's build, as INTEGRATION.md describes."""
+    import importlib.util
+    from pdscope_amd import build as B
+    root = tmp_path_factory.mktemp("reference_tree")
+    where = root / "expertbench" / "native-build" / "layer-dispatch"
+    where.mkdir(parents=True)
+    (where / B.DISPATCH_MODULE.name).symlink_to(B.DISPATCH_MODULE)
+    candidates = sorted(where.glob("pdscope_layer_dispatch*.so"))
+    assert candidates, "native layer dispatch is not built"
+    spec = importlib.util.spec_from_file_location("pdscope_layer_dispatch", candidates[0])
+    module = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(module)
+    assert hasattr(module, "submit_and_merge"), "native dispatch lacks submit_and_merge"
+    return module

@@ -44,6 +44,6 @@ def test_invalid_arguments_raise_before_any_launch():
     with pytest.raises(ValueError):
         _lib.call("pdscope_route_topk", None, None, None, 1, 2048, 128, 8, 1, None, None, None, None, None, None)
     with pytest.raises(ValueError):
-        _lib.call("pdscope_schedule", None, None, 0, 48, None, None)
+        _lib.call("pdscope_schedule", None, 128, None, 0, 48, None, None)
     msg = _lib.load().pdscope_last_error().decode()
     assert "schedule" in msg

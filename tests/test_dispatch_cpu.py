@@ -1,11 +1,14 @@
-"""Host half of the native dispatch (CPU only): packing and the queue protocol."""
-import ctypes
+"""Host half of the native dispatch (CPU only): packing and the queue protocol.
 
-import numpy as np
+The pdscope_layer_dispatch extension is exercised both as the package's
+module and as the reference driver's loader finds it (glob under
+expertbench/native-build/layer-dispatch, spec_from_file_location,
+exec_module)."""
+import ctypes
+from pathlib import Path
+
 import pytest
 import torch
-
-from pdscope_amd import pdscope_layer_dispatch as nd
 
 
 class FakePool:
@@ -31,7 +34,22 @@ class RecordingLayer:
         return lambda: None
 
 
-def test_submit_group_packs_rows_ids_and_unit_coefficients():
+@pytest.fixture(params=["package", "reference_loader"])
+def nd(request, dispatch_via_reference_loader):
+    if request.param == "package":
+        from pdscope_amd import pdscope_layer_dispatch
+        return pdscope_layer_dispatch
+    return dispatch_via_reference_loader
+
+
+def test_module_is_the_native_extension(nd):
+    from pdscope_amd import build as B
+    assert Path(nd.__file__).resolve() == B.DISPATCH_MODULE.resolve()
+    assert nd.__file__.endswith(".so") and all(callable(getattr(nd, f)) for f in
+                                               ("submit_group", "finish_and_merge", "submit_and_merge"))
+
+
+def test_submit_group_packs_rows_ids_and_unit_coefficients(nd):
     rows, H = 5, 64
     row = torch.randn(H).to(torch.bfloat16)
     packed = torch.empty((rows, H), dtype=torch.bfloat16)
@@ -51,12 +69,34 @@ def test_submit_group_packs_rows_ids_and_unit_coefficients():
 
 
 @pytest.mark.parametrize("rows,row_bytes,ids", [(0, 4096, []), (2, 3, [1, 2]), (2, 4096, [1])])
-def test_submit_group_rejects_bad_shapes(rows, row_bytes, ids):
+def test_submit_group_rejects_bad_shapes(nd, rows, row_bytes, ids):
     with pytest.raises(RuntimeError):
         nd.submit_group(FakePool(), RecordingLayer(), 1, rows, row_bytes, 1, 1, 1, 1, 1, ids)
 
 
-def test_finish_and_merge_rejects_host_tensors():
+def test_finish_and_merge_rejects_host_tensors(nd):
     t = torch.zeros(4, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError):
         nd.finish_and_merge(FakePool(), 1, 1, 8, t, t, torch.zeros(1, dtype=torch.long), t)
+
+
+def test_submit_and_merge_rejects_host_tensors_before_submitting(nd):
+    pool = FakePool()
+    t = torch.zeros(4, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="CUDA device"):
+        nd.submit_and_merge(pool, RecordingLayer(), 1, 1, 8, 1, 1, t, 1, 1, 1, [3], t,
+                            torch.zeros(1, dtype=torch.long), t)
+    assert pool.queue == [] and pool.synced == 0
+
+
+def test_layer_and_pool_errors_propagate(nd):
+    class Broken:
+        def forward_task(self, *args):
+            raise KeyError("no such expert layer")
+    rows, H = 2, 64
+    row = torch.zeros(H, dtype=torch.bfloat16)
+    packed = torch.empty((rows, H), dtype=torch.bfloat16)
+    count, selected, coeff = ctypes.c_int32(0), (ctypes.c_int64 * rows)(), (ctypes.c_float * rows)()
+    with pytest.raises(KeyError):
+        nd.submit_group(FakePool(), Broken(), row.data_ptr(), rows, H * 2, packed.data_ptr(), packed.data_ptr(),
+                        ctypes.addressof(count), ctypes.addressof(selected), ctypes.addressof(coeff), [1, 2])

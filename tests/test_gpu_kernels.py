@@ -432,6 +432,46 @@ def test_pack_with_schedule_equals_pack_then_schedule(pd, T, k, E, nsel, bm, bm2
         assert torch.equal(ts2, t2)
 
 
+@pytest.mark.parametrize("T,k,E", [(40, 8, 128), (3000, 8, 64)])
+def test_schedules_count_out_of_range_sel_entries_as_empty(pd, T, k, E):
+    """A sel entry outside [0, E) (negative, E, past 256, INT32_MAX) is an
+    expert with no rows in every schedule: pdscope_schedule, the balanced
+    order and prefixes (one and two row tiles) and the schedule the pack
+    launch writes (single- and multi-block).  It gets no tiles and ranks with
+    the untouched experts, and nothing is read past `counts`."""
+    from collections import defaultdict
+    ops, layer, synthetic = pd
+    g = torch.Generator().manual_seed(T + E)
+    ids = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)]).to(torch.int32).to(DEV)
+    sel_list = [3, E + 5, 7, -1, 11, 300, 2 ** 31 - 1, E, 0, E - 1]
+    sel = torch.tensor(sel_list, dtype=torch.int32, device=DEV)
+    n = len(sel_list)
+    ref = ops.pack(ids, E)
+    torch.cuda.synchronize()
+    rows = defaultdict(int, enumerate(ref.counts.cpu().tolist()))
+    bm, bm2 = 64, 256
+    plain = ops.schedule(ref.counts, sel, bm)
+    o1 = torch.empty(n, dtype=torch.int32, device=DEV)
+    t1 = ops.schedule(ref.counts, sel, bm, order=o1)
+    o2, t2, t2b = (torch.empty(n, dtype=torch.int32, device=DEV), torch.empty(n + 1, dtype=torch.int32, device=DEV),
+                   torch.empty(n + 1, dtype=torch.int32, device=DEV))
+    ops.schedule(ref.counts, sel, bm, out=t2, order=o2, block_m2=bm2, out2=t2b)
+    o3, t3, t3b = (torch.full((n,), -7, dtype=torch.int32, device=DEV),
+                   torch.full((n + 1,), -7, dtype=torch.int32, device=DEV),
+                   torch.full((n + 1,), -7, dtype=torch.int32, device=DEV))
+    got = ops.pack(ids, E, schedule=(sel, bm, o3, t3, bm2, t3b))
+    torch.cuda.synchronize()
+    for name in ("counts", "offsets", "perm_token", "row_of"):
+        assert torch.equal(getattr(got, name), getattr(ref, name)), name
+    tiles = lambda es, b: [0] + np.cumsum([(rows[e] + b - 1) // b for e in es]).tolist()  # noqa: E731
+    assert plain.cpu().tolist() == tiles(sel_list, bm)
+    want = _snake_order(rows, sel_list)
+    for o, t in ((o1, t1), (o2, t2), (o3, t3)):
+        assert o.cpu().tolist() == want and t.cpu().tolist() == tiles(want, bm)
+    for t in (t2b, t3b):
+        assert t.cpu().tolist() == tiles(want, bm2)
+
+
 def test_decode_qwen(orc, pd, qwen, qwen_host):
     ops, layer, synthetic = pd
     ws = layer.MoEWorkspace(1, 2048, 768, 128, 8, DEV)

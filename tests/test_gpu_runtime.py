@@ -452,6 +452,81 @@ def test_executor_per_expert_hook_matches_oracle(orc):
         ex.shutdown()
 
 
+def test_executor_accounts_an_enqueued_use_only_after_it_completed():
+    """gpu_group(launch=None) accounts uses that work enqueued before the
+    reveal already made: without a completed event recorded after that work
+    it raises and acquires nothing; with one it holds the copies until its
+    own event on that stream completes, then finish_gpu releases them."""
+    from pdscope_amd.cache import DemandID, ExpertCache, ExpertKey
+    from pdscope_amd.executor import ExpertExecutor
+    H, I, E, k = 256, 128, 32, 4
+    _, masters = build(1, H, I, E, k, seed=6)
+    sizes = {key: w.nbytes for key, w in masters.items()}
+    size = next(iter(sizes.values()))
+    cache = ExpertCache(sizes, 4 * size, [size, size])
+    ex = ExpertExecutor(cache, masters, 0)
+    try:
+        key = ExpertKey(0, 5, "bf16")
+        cache.on_demand(DemandID("r", 0, 0), {key: 1})
+        assert ex.finish_load(ex.load(key), wait=True)
+        cur = torch.cuda.current_stream()
+        with pytest.raises(RuntimeError, match="completed"):
+            ex.gpu_group([key], None, wait_for=cur)
+        assert not ex.computes
+        done = torch.cuda.Event()
+        done.record(cur)
+        done.synchronize()
+        pend = ex.gpu_group([key], None, wait_for=cur, completed=done)
+        assert ex.computes and ex.finish_gpu(pend, wait=True) is None and not ex.computes
+        cache.end_demand(DemandID("r", 0, 0))
+    finally:
+        ex.shutdown()
+
+
+def test_executor_profiles_stages_and_stages_masters_by_memcpy(orc):
+    """profile_stages records the copy, launch and CPU-call spans
+    (expertbench/executor.py:352-355, 384-385, 472-481, 518-528); lazily
+    pinned masters copied byte for byte (cpu_staging_copy="memcpy") stage the
+    same bytes; a callable CPU backend runs on an initialised worker."""
+    from pdscope_amd.cache import DemandID, ExpertCache, ExpertKey
+    from pdscope_amd.executor import ExpertExecutor
+    from pdscope_amd import synthetic
+    from pdscope_amd.executor import masters_from_block
+    H, I, E, k = 256, 128, 32, 4
+    layers = [synthetic.make_layer(H, I, E, k, True, seed=11, device=DEV)]
+    masters = masters_from_block(0, layers[0].experts, E, H, I, pin=False)   # pinned on first use
+    sizes = {key: w.nbytes for key, w in masters.items()}
+    size = next(iter(sizes.values()))
+    cache = ExpertCache(sizes, 4 * size, [size, size])
+
+    def cpu_expert(key, rows):
+        return torch.zeros_like(rows)
+    ex = ExpertExecutor(cache, masters, 0, profile_stages=True, pinned_source_mode="lazy_pinned",
+                        cpu_staging_copy="memcpy", cpu_backend=cpu_expert)
+    try:
+        key, cpu_key = ExpertKey(0, 9, "bf16"), ExpertKey(0, 2, "bf16")
+        cache.on_demand(DemandID("r", 0, 0), {key: 3, cpu_key: 2})
+        t = ex.load(key)
+        assert ex.finish_load(t, wait=True)
+        st = ex.stage_timings
+        assert st["weight_dma_gpu_span_ms"] > 0 and st["source_copy_ms"] > 0
+        assert torch.equal(ex.copies[t].cpu(), masters[key].flat.view(torch.uint8))
+        x = torch.randn((3, H), device=DEV).to(torch.bfloat16)
+        y = ex.finish_gpu(ex.gpu(key, x), wait=True)
+        blk = u16(layers[0].experts[9])
+        ref = orc.expert_forward(u16(x), blk[:I * H].reshape(I, H), blk[I * H:2 * I * H].reshape(I, H),
+                                 blk[2 * I * H:].reshape(H, I))
+        assert_layer_close(orc, y, ref)
+        assert st["gpu_forward_device_span_ms"] > 0 and st["gpu_forward_host_submit_ms"] >= 0
+        rows = torch.randn((2, H)).to(torch.bfloat16)
+        out = ex.finish_cpu(ex.submit_cpu(cpu_key, rows), wait=True)
+        assert out.shape == rows.shape and st["cpu_forward_ms"] >= 0
+        assert ex.cpu_worker_init["torch_threads"] == ex.cpu_worker_init["expected_threads"]
+        cache.end_demand(DemandID("r", 0, 0))
+    finally:
+        ex.shutdown()
+
+
 def test_executor_slot_table_upload_follows_the_host_mirror():
     """upload_table copies a layer's table again only after an entry changed;
     every upload, skipped or not, leaves the device table equal to the host
@@ -526,8 +601,17 @@ class _OracleLayer:
         return run
 
 
-def test_native_dispatch_submit_and_merge(orc):
-    from pdscope_amd import pdscope_layer_dispatch as nd
+@pytest.fixture(params=["package", "reference_loader"])
+def nd(request, dispatch_via_reference_loader):
+    """The pdscope_layer_dispatch extension as the package imports it and as
+    the reference driver's loader finds it."""
+    if request.param == "package":
+        from pdscope_amd import pdscope_layer_dispatch
+        return pdscope_layer_dispatch
+    return dispatch_via_reference_loader
+
+
+def test_native_dispatch_submit_and_merge(orc, nd):
     H, I, E, k = 256, 128, 32, 4
     layers, _ = build(1, H, I, E, k, seed=8)
     experts = u16(layers[0].experts)
@@ -550,3 +634,33 @@ def test_native_dispatch_submit_and_merge(orc):
     for r in range(rows):
         ref = (ref.float() + (block[r] * weights.cpu()[r]).float()).to(torch.bfloat16)
     assert torch.equal(out.cpu()[0], ref)
+
+
+def test_native_dispatch_submit_then_finish_and_merge_with_an_out_of_range_token(orc, nd):
+    """submit_group then finish_and_merge (the split form the runtime uses);
+    a token index outside out's rows is skipped by the merge, every other
+    row is added in order with bf16 arithmetic."""
+    H, I, E, k = 256, 128, 32, 4
+    layers, _ = build(1, H, I, E, k, seed=9)
+    experts = u16(layers[0].experts)
+    rows, ids = 4, [3, 30, 8, 11]
+    row = torch.randn(H).to(torch.bfloat16)
+    packed = torch.empty((rows, H), dtype=torch.bfloat16)
+    block = torch.empty((rows, H), dtype=torch.bfloat16)
+    count, sel, coeff = ctypes.c_int32(0), (ctypes.c_int64 * rows)(), (ctypes.c_float * rows)()
+    scratch = torch.empty((rows, H), dtype=torch.bfloat16, device=DEV)
+    base = torch.randn((2, H)).to(torch.bfloat16)
+    out = base.to(DEV)
+    tokens = torch.tensor([1, 7, 0, 1], dtype=torch.long, device=DEV)   # 7 is past out's 2 rows
+    weights = torch.tensor([0.5, 4.0, -0.25, 0.125], dtype=torch.bfloat16, device=DEV)
+    pool = _Pool()
+    nd.submit_group(pool, _OracleLayer(orc, experts, H, I), row.data_ptr(), rows, H * 2, packed.data_ptr(),
+                    block.data_ptr(), ctypes.addressof(count), ctypes.addressof(sel), ctypes.addressof(coeff), ids)
+    res = nd.finish_and_merge(pool, block.data_ptr(), rows, H * 2, scratch, out, tokens, weights)
+    torch.cuda.synchronize()
+    assert res is out and list(sel) == ids
+    ref = base.clone()
+    for r, t in enumerate([1, 7, 0, 1]):
+        if t < 2:
+            ref[t] = (ref[t].float() + (block[r] * weights.cpu()[r]).float()).to(torch.bfloat16)
+    assert torch.equal(out.cpu(), ref)
