@@ -58,7 +58,8 @@ def parse():
     ap.add_argument("--workload", default="decode",
                     choices=["prefill512", "decode", "prefill4096", "prefill4096_zipf", "dsv2_mixed", "stack48",
                              "runtime_decode"])
-    ap.add_argument("--no-extra", action="store_true", help="only the main workload")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="only the main workload (for prefill4096: without the uniform-routing comparison)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0,
                     help="0: physical cores of this process's CPUs (at most 16, one GPU's share) - 1")
@@ -245,10 +246,13 @@ def run_prefill(T, steps, warmup, n_layers, device, seed0, bias=None):
             ev[2].record(stream)
         ops.merge(ws.y, packed.row_of, w, ws.out[:T])
 
-    # experts touched per layer (for algorithmic bytes) and each copy's row tile
+    # experts touched per layer (for algorithmic bytes) and each copy's row
+    # tile, from its routing and grouping alone (no grouped launch on a tile
+    # the timed steps do not use)
     touched, max_rows = [], []
     for i in range(n_layers):
-        step(i)
+        _, ids, _ = layer.route(xs[i], layers[i][0].gate, ws, bias=bias)
+        ops.pack(ids, E, out=packed, workspace=ws.pack_ws)
         torch.cuda.synchronize(device)
         counts = ws.counts.cpu()
         live = counts[counts > 0]
@@ -971,12 +975,13 @@ def main():
             bias, _ = synthetic.zipf_bias(E, 1.1, seed=20261011, device=device)
             res = run_prefill(T, steps, warmup, nl, device, 20261011 + 9000, bias=bias)
             rec = prefill_record(res)
-            uni = run_prefill(T, max(20, steps // 2), max(5, warmup // 2), nl, device, 20261011)
-            rec["uniform_routing"] = {kk: v for kk, v in prefill_record(uni).items()
-                                      if kk in ("tok_s", "kernel_ms_mean", "gateup_ms_mean", "down_ms_mean",
-                                                "gateup_mfma_frac", "mfma", "vendor_bmm", "block_m")}
-            for kk in ("first_layer", "first_x", "ws", "bias"):
-                uni.pop(kk, None)
+            if not args.no_extra:
+                uni = run_prefill(T, max(20, steps // 2), max(5, warmup // 2), nl, device, 20261011)
+                rec["uniform_routing"] = {kk: v for kk, v in prefill_record(uni).items()
+                                          if kk in ("tok_s", "kernel_ms_mean", "gateup_ms_mean", "down_ms_mean",
+                                                    "gateup_mfma_frac", "mfma", "vendor_bmm", "block_m")}
+                for kk in ("first_layer", "first_x", "ws", "bias"):
+                    uni.pop(kk, None)
         elif kind == "prefill":
             res = run_prefill(T, steps, warmup, nl, device, 20261011)
             rec = prefill_record(res)
@@ -1036,8 +1041,11 @@ def main():
     else:
         roof = dict(main["hbm"])
     roof.setdefault("kernel", main["kernel"])
-    traffic_profile = f"{args.workload}_traffic.md"
-    roof["traffic"] = traffic_from_profiles(traffic_profile)
+    # committed counter summary of the main workload's dominant launches (none for the copy-bound legs)
+    traffic_profile = {"decode": "decode_traffic.md", "prefill512": "prefill512_traffic.md",
+                       "prefill4096": "prefill4096_zipf_traffic.md",
+                       "dsv2_mixed": "dsv2_mixed_traffic.md"}.get(args.workload)
+    roof["traffic"] = traffic_from_profiles(traffic_profile) if traffic_profile else None
     roof["traffic_source"] = (f"profiles/{traffic_profile}: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of this "
                               "workload's command, committed; not measured in this run"
                               if roof["traffic"] is not None else None)

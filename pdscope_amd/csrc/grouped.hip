@@ -554,11 +554,13 @@ using namespace pd;
 // read once per expert and n-tile); 32 only for very thin experts.
 PD_API int pdscope_grouped_block_m(int rows_hint) {
     if (rows_hint <= 16) return 32;
-    if (rows_hint <= 64) return 64;
-    // up to ~124 rows a 128-row tile holds most experts whole (measured:
-    // 122 mean rows of 17 MB experts 3.6% faster than 256-row tiles, 128 mean
-    // rows of 9 MB experts 2.7% slower)
-    if (rows_hint <= 124) return 128;
+    // whole Qwen-shaped layers (pack + gate/up + down + merge), uniform
+    // routing, back to back: 24..40 mean rows run fastest on 64-row tiles,
+    // 48..96 on 128-row tiles (64 rows: 271 against 292 us), 112 and above on
+    // the 256-row tile (112: 309 against 320 us; the DeepSeek-V2-Lite mixed
+    // batch, 122 mean rows of 17 MB experts: 332 against 355 us)
+    if (rows_hint <= 44) return 64;
+    if (rows_hint <= 104) return 128;
     if (rows_hint <= 192) return 256;
     // one 384-row tile holds an expert of the typical 200..320 rows (no
     // tail tile re-reading its weights); beyond that 256x256 tiles read the

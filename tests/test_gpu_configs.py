@@ -5,7 +5,7 @@
   output against the oracle.
 * DeepSeek-V2-Lite-shaped mixed batch (48 decode tokens + 256 + 1000 prefill
   tokens in one launch, 64 routed experts top-6 without renormalisation, 2
-  shared experts as one 2816-wide MLP) on the 128-row routed tile and the
+  shared experts as one 2816-wide MLP) on the 256-row routed tile and the
   1304-row shared expert: grouping in full, and a seeded sample of tokens
   from every segment (with the segment boundaries) against the oracle.
 * A chained stack of Qwen-shaped MoE blocks through PDScopeCudaRuntime
@@ -72,7 +72,7 @@ def test_config5_dsv2_mixed_batch_1304_tokens(orc):
     ws = layer.MoEWorkspace(T, H, I, E, k, DEV, shared_I=Is)
     slots = ops.slot_table([lay.experts[e] for e in range(E)], DEV)
     shared_slot = ops.slot_table([lay.shared], DEV)
-    assert ops.grouped_block_m(T * k // E) == 128
+    assert ops.grouped_block_m(T * k // E) == 256
     out, logits, ids, w = layer.moe_forward(x, lay.gate, slots, ws, normalize=False, shared_slot=shared_slot)
     torch.cuda.synchronize()
     ik, wk, xu = ids.cpu().numpy(), u16(w), u16(x)

@@ -3,7 +3,8 @@
 48 Qwen3-30B-A3B-shaped MoE blocks (identity attention, residual and
 RMSNorm between blocks) through PDScopeCudaRuntime, exactly as the bench's
 stack workload builds them: 58 GB of pinned expert masters, a 24 GiB device
-budget (allocator capped at 23 GiB, expert slots sized within it), 8 demand
+budget (allocator capped below it by the memory already in use outside the
+allocator plus a margin, expert slots sized within the cap), 8 demand
 staging slots, gate-fallback prefetch of the next layer and decode layers
 replayed through their captured single-launch graphs.  Prefill 2048 tokens,
 then 64 decode steps.
