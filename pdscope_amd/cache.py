@@ -41,6 +41,7 @@ from collections import Counter
 from collections.abc import Mapping
 from dataclasses import dataclass, field
 from types import MappingProxyType
+from typing import NamedTuple
 from uuid import uuid4
 
 
@@ -133,14 +134,16 @@ class LoadTicket:
         return (LoadTicket, (self.owner, self.generation, self.key, self.pool, self.slot))
 
 
-@dataclass(frozen=True)
-class UseHandle:
+# The records below are built on every layer call (several per routed
+# expert): immutable named tuples, which construct in a fraction of a frozen
+# dataclass's time.
+
+class UseHandle(NamedTuple):
     ticket: LoadTicket
     serial: int
 
 
-@dataclass(frozen=True)
-class EntryView:
+class EntryView(NamedTuple):
     key: ExpertKey
     nbytes: int
     pool: str
@@ -153,8 +156,7 @@ class EntryView:
     expired: bool
 
 
-@dataclass(frozen=True)
-class DemandObservation:
+class DemandObservation(NamedTuple):
     key: ExpertKey
     tokens: int
     valid_tokens: int
@@ -317,6 +319,7 @@ class ExpertCache:
         self._counters = Counter()
         self._unprotected = _Ranking()
         self._protected_rank = _Ranking()
+        self._ranked = {}                       # key -> the ranking that holds it
         self._protected = frozenset()
         self._hint = None
 
@@ -348,6 +351,15 @@ class ExpertCache:
             return None
         return EntryView(key, c.nbytes, c.ticket.pool, c.state, c.ticket, c.phase != RESERVED, len(c.holders),
                          c.origin, c.used, c.expired)
+
+    def residency(self, key):
+        """(state, ticket) of the copy of `key` as lookup() would show them,
+        or None if it has no copy; builds no view."""
+        c = self._copies.get(key)
+        if c is None:
+            self._registered(key)
+            return None
+        return ("in_use" if c.holders else "ready" if c.phase == READY else "loading"), c.ticket
 
     def ready_in_cache(self, key):
         """Whether lookup(key) would show state 'ready' (landed, not held) in
@@ -421,14 +433,24 @@ class ExpertCache:
     def _is_protected(self, key):
         return key in self._protected or (self._hint is not None and key in self._hint.keys)
 
+    def _unrank(self, key):
+        home = self._ranked.pop(key, None)
+        if home is not None:
+            home.discard(key)
+
     def _reindex(self, key):
         """Place `key` in the ranking its copy belongs to now (or in none)."""
-        self._unprotected.discard(key)
-        self._protected_rank.discard(key)
         c = self._copies.get(key)
+        target = None
         if c is not None and self._evictable(key, c):
             target = self._protected_rank if self._is_protected(key) else self._unprotected
+        home = self._ranked.get(key)
+        if home is not None and home is not target:
+            home.discard(key)
+            del self._ranked[key]
+        if target is not None:
             target.put(key, self._rank(key))
+            self._ranked[key] = target
 
     def _choose_victims(self, size):
         """Cheapest evictable copies freeing room for `size` more bytes, or
@@ -447,8 +469,7 @@ class ExpertCache:
 
     def _drop(self, key):
         c = self._copies.pop(key)
-        self._unprotected.discard(key)
-        self._protected_rank.discard(key)
+        self._unrank(key)
         if c.ticket.pool == "cache":
             self._cache_charged -= c.nbytes
         else:
@@ -546,12 +567,13 @@ class ExpertCache:
         if valid_token_counts is not None and not isinstance(valid_token_counts, Mapping):
             raise CacheError("valid token counts must be a mapping")
         valid = dict(physical) if valid_token_counts is None else dict(valid_token_counts)
-        for key, n in valid.items():
-            if key not in physical:
-                raise CacheError("a valid count names an expert outside the demand")
-            _require_int(n, "valid tokens per expert", 1)
-            if n > physical[key]:
-                raise CacheError("valid tokens exceed routed tokens")
+        if valid_token_counts is not None:   # the physical counts were checked above
+            for key, n in valid.items():
+                if key not in physical:
+                    raise CacheError("a valid count names an expert outside the demand")
+                _require_int(n, "valid tokens per expert", 1)
+                if n > physical[key]:
+                    raise CacheError("valid tokens exceed routed tokens")
         if self._reveal is not None:
             r = self._reveal
             if r.identity == identity and r.counts == counts and r.valid == valid:
@@ -574,11 +596,10 @@ class ExpertCache:
                 self._times_demanded[o.key] += 1
                 self._last_tick[o.key] = self._tick
         self._reveal = _Reveal(identity, counts, valid, observations, set(physical))
-        # open experts cannot be evicted: they leave both rankings (what
+        # open experts cannot be evicted: they leave the rankings (what
         # _reindex does for a key that is not evictable)
         for key in physical:
-            self._unprotected.discard(key)
-            self._protected_rank.discard(key)
+            self._unrank(key)
         return observations
 
     def _observe(self, key, tokens, valid_tokens):
@@ -592,28 +613,53 @@ class ExpertCache:
                                  source)
 
     def _count_reveal(self, observations):
+        # sums per counter first, each counter then updated once; a counter
+        # is touched (and so listed in stats()) under the same conditions as
+        # when it is counted per observation
         n = self._counters
         n["physical_layer_events"] += 1
         n["demand_events"] += int(any(o.valid_tokens for o in observations))
+        tokens = padding = ready = 0
+        pad_only = demands = d_tokens = d_bytes = 0
+        hits = hit_tokens = hit_bytes = 0
+        kinds = {}
         for o in observations:
-            n["physical_expert_demands"] += 1
-            n["physical_demand_tokens"] += o.tokens
-            n["padding_token_assignments"] += o.tokens - o.valid_tokens
-            n["physical_ready_hits"] += int(o.ready_hit)
+            tokens += o.tokens
+            padding += o.tokens - o.valid_tokens
+            hit = o.hit_source is not None
+            ready += hit
             if not o.valid_tokens:
-                n["padding_only_expert_demands"] += 1
+                pad_only += 1
                 continue
-            n["expert_demands"] += 1
-            n["demand_tokens"] += o.valid_tokens
-            n["demand_bytes"] += o.nbytes
-            if o.ready_hit:
-                n["ready_hits"] += 1
-                n[f"{o.hit_source}_hits" if o.hit_source != "history" else "history_ready_hits"] += 1
-                n["ready_hit_tokens"] += o.valid_tokens
-                n["ready_hit_bytes"] += o.nbytes
-                n["cache_resident_hits" if o.pool_at_reveal == "cache" else "staging_ready_hits"] += 1
+            demands += 1
+            d_tokens += o.valid_tokens
+            d_bytes += o.nbytes
+            if hit:
+                hits += 1
+                hit_tokens += o.valid_tokens
+                hit_bytes += o.nbytes
+                for name in (f"{o.hit_source}_hits" if o.hit_source != "history" else "history_ready_hits",
+                             "cache_resident_hits" if o.pool_at_reveal == "cache" else "staging_ready_hits"):
+                    kinds[name] = kinds.get(name, 0) + 1
             else:
-                n["loading_misses" if o.state_at_reveal in ("loading", "in_use") else "absent_misses"] += 1
+                name = "loading_misses" if o.state_at_reveal in ("loading", "in_use") else "absent_misses"
+                kinds[name] = kinds.get(name, 0) + 1
+        n["physical_expert_demands"] += len(observations)
+        n["physical_demand_tokens"] += tokens
+        n["padding_token_assignments"] += padding
+        n["physical_ready_hits"] += ready
+        if pad_only:
+            n["padding_only_expert_demands"] += pad_only
+        if demands:
+            n["expert_demands"] += demands
+            n["demand_tokens"] += d_tokens
+            n["demand_bytes"] += d_bytes
+        if hits:
+            n["ready_hits"] += hits
+            n["ready_hit_tokens"] += hit_tokens
+            n["ready_hit_bytes"] += hit_bytes
+        for name, v in kinds.items():
+            n[name] += v
 
     def end_demand(self, identity):
         r = self._reveal
@@ -776,4 +822,5 @@ class ExpertCache:
         self._counters.clear()
         self._unprotected.clear()
         self._protected_rank.clear()
+        self._ranked.clear()
         self._hint = None

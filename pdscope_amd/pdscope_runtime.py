@@ -37,6 +37,7 @@ expert runs on the GPU.  There is no built-in CPU expert path.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import hashlib
 import statistics
@@ -151,6 +152,7 @@ class PDScopeCudaRuntime:
         self._graph_turn = {}
         self._dispatch_buffers = {}
         self._pinned_counts = torch.empty(2 * self.E + 64, dtype=torch.int32, pin_memory=True)
+        self._err_at = 2 * self.E + 8    # the decode error word's place in _pinned_counts
         self._copy_done = torch.cuda.Event()
         try:
             for key in hot_keys:
@@ -266,7 +268,8 @@ class PDScopeCudaRuntime:
             # entries the first replay saw (a copy still in flight reads as null)
             replay_table = list(self.executor.table(layer, E)[1])
             logits, ids, weights, gout, pred_ids = self._replay_decode_graph(layer, x, gate, normalize, k, out,
-                                                                             ring=ring, next_gate=graph_pred)
+                                                                             ring=ring, next_gate=graph_pred,
+                                                                             stream=cur)
             if self.graph_output_pool:
                 out = gout
         else:
@@ -285,15 +288,16 @@ class PDScopeCudaRuntime:
             counts_dev = ids.reshape(-1)
         host = self._pinned_counts
         n0 = counts_dev.numel()
-        host[:n0].copy_(counts_dev, non_blocking=True)
-        if pred_ids is not None:
-            host[n0:n0 + k].copy_(pred_ids, non_blocking=True)
-        elif predict:
-            host[n0:n0 + E].copy_(nws.hist, non_blocking=True)
-        err_at = 2 * E + 8
+        err_at = self._err_at
         if graph_path:
-            # the fused decode kernel's sticky error word rides along with the counts
-            host[err_at:err_at + 1].copy_(self._decode_error_word(), non_blocking=True)
+            # the replayed graph itself copied the routed ids, its prediction
+            # and the fused kernel's sticky error word into `host`
+            if pred_ids is None and predict:
+                host[n0:n0 + E].copy_(nws.hist, non_blocking=True)
+        else:
+            host[:n0].copy_(counts_dev, non_blocking=True)
+            if predict:
+                host[n0:n0 + E].copy_(nws.hist, non_blocking=True)
         self._copy_done.record(cur)
         self._copy_done.synchronize()
         if graph_path:
@@ -326,11 +330,12 @@ class PDScopeCudaRuntime:
         # experts between the CPU backend, resident copies and demand staging
         # and picks the prefetch (pdscope_runtime.py:268-279); else every
         # expert runs on the GPU, resident first, misses through staging
-        views = {e: self.cache.lookup(key(e)) for e in counts}
+        # (state, ticket) of each routed expert's copy, or None (no views built)
+        views = {e: self.cache.residency(key(e)) for e in counts}
         has_next = predict and (layer + 1) in self.layers
         if planned:
             hit_rate = observed["hits"] / observed["total"] if observed["total"] else 0.0
-            next_resident = [e for e in next_counts if self.cache.lookup(nkey(e)) is not None] if has_next else []
+            next_resident = [e for e in next_counts if self.cache.residency(nkey(e)) is not None] if has_next else []
             decision = plan_pdscope(counts, next_counts if has_next else {}, current_layer=layer, phase=phase,
                                     current_gpu_ids=[e for e in counts if views[e] is not None],
                                     next_gpu_ids=next_resident, costs=self.costs, attention_ms=attention_ms,
@@ -350,8 +355,8 @@ class PDScopeCudaRuntime:
             resident = sorted((e for e in counts if views[e] is not None), key=lambda e: (-counts[e], e))
             demand = sorted((e for e in counts if views[e] is None), key=lambda e: (-counts[e], e))
         for e in resident:
-            if views[e].state == "loading":
-                self.executor.finish_load(views[e].ticket, wait=True)
+            if views[e][0] == "loading":
+                self.executor.finish_load(views[e][1], wait=True)
                 self.pending.pop(key(e), None)
 
         ex = self.executor
@@ -486,7 +491,7 @@ class PDScopeCudaRuntime:
                         else sorted(next_counts, key=lambda e: (-next_counts[e], e)))
             for e in forecast:
                 target = nkey(e)
-                if self.cache.lookup(target) is not None:
+                if self.cache.residency(target) is not None:
                     continue
                 if len(self.transient) >= self.speculative_slots:
                     skipped.append(e)
@@ -515,7 +520,10 @@ class PDScopeCudaRuntime:
         add_in = None
         if cpu_rows or native_cpu:
             offs = packed.offsets.cpu().tolist() if T == 1 else offs
-        with torch.cuda.stream(ex.compute_stream):
+        # a graph-served layer with no CPU rows has nothing left to enqueue here
+        finish_ctx = (contextlib.nullcontext() if graph_path and not cpu_rows and not native_cpu
+                      else torch.cuda.stream(ex.compute_stream))
+        with finish_ctx:
             for e, rows in cpu_rows.items():
                 ws.y[offs[e] * H:offs[e + 1] * H].view(-1, H).copy_(rows)
             if native_cpu:
@@ -706,7 +714,8 @@ class PDScopeCudaRuntime:
     def _graph_key(layer, k, normalize, gate, ring, next_gate):
         return (layer, k, normalize, gate.data_ptr(), ring, next_gate.data_ptr() if next_gate is not None else 0)
 
-    def _replay_decode_graph(self, layer, x, gate, normalize, k, out, *, ring=0, cache=True, next_gate=None):
+    def _replay_decode_graph(self, layer, x, gate, normalize, k, out, *, ring=0, cache=True, next_gate=None,
+                             stream=None):
         """Replay the captured single-launch decode layer of `layer` over its
         current slot table (capturing it on first use, checked bit for bit
         against the eager launch).  With graph_output_pool the graph of ring
@@ -721,7 +730,8 @@ class PDScopeCudaRuntime:
         ex.table(layer, self.E)
         # the table tensor is captured by address; refresh its contents (copies
         # may have moved between calls) on the replay stream
-        slots_dev = ex.upload_table(layer, self.E, torch.cuda.current_stream(self.device))
+        cur = torch.cuda.current_stream(self.device) if stream is None else stream
+        slots_dev = ex.upload_table(layer, self.E, cur)
         if g is None:
             gws = L.MoEWorkspace(1, self.H, self.I, self.E, k, self.device)
             pred = torch.full((k,), -1, dtype=torch.int32, device=self.device) if next_gate is not None else None
@@ -730,18 +740,26 @@ class PDScopeCudaRuntime:
             xin.copy_(x)
             torch.cuda.synchronize(self.device)
             side = torch.cuda.Stream(self.device)
-            side.wait_stream(torch.cuda.current_stream(self.device))
+            side.wait_stream(cur)
             # whole layer (fused single-launch decode where the device allows)
             fwd = dict(normalize=normalize, merge=self.merge, next_gate=next_gate, pred_out=pred)
             with torch.cuda.stream(side):
                 L.moe_forward(xin, gate, slots_dev, gws, **fwd)
-            torch.cuda.current_stream(self.device).wait_stream(side)
+            cur.wait_stream(side)
             watched = lambda: [t for t in (gout, gws.logits[:1], gws.ids[:1], gws.weights[:1], pred)  # noqa: E731
                                if t is not None]
             eager = [t.clone() for t in watched()]
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
                 L.moe_forward(xin, gate, slots_dev, gws, **fwd)
+                # what forward reads back rides in the graph: the routed ids,
+                # the prediction and the sticky error word land in the pinned
+                # host buffer with every replay (no copy launches per call)
+                host = self._pinned_counts
+                host[:k].copy_(gws.ids[:1].reshape(-1), non_blocking=True)
+                if pred is not None:
+                    host[k:2 * k].copy_(pred, non_blocking=True)
+                host[self._err_at:self._err_at + 1].copy_(self._decode_error_word(), non_blocking=True)
             # a captured graph must reproduce the eager launch bit for bit
             # before it serves (the reference checks the same at capture,
             # expertbench/executor.py:95-96)
