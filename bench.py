@@ -19,7 +19,9 @@ also carries the T = 512 prefill (uniform routing), the T = 4096 prefill on
 the Zipf(1.1)-biased routing with every expert resident (the grouped SwiGLU
 the T = 4096 target names; the uniform routing beside it), the T = 4096
 Zipf-skewed layer with 32 resident experts and 8 demand staging slots
-through the runtime, and the DeepSeek-V2-Lite mixed-batch results
+through the runtime, the runtime's T = 1 layer call with every expert
+resident (its host cost around the kernel), and the DeepSeek-V2-Lite
+mixed-batch results
 ("workloads"), each with its own roofline figure, and CPU baselines: the
 AVX2 bf16 SwiGLU expert kernel under oracle/ (a stand-in for ktransformers'
 AVX2BF16_MOE, which is not available offline) timed on this host's cores on
@@ -951,10 +953,8 @@ def main():
     plan = {"prefill512": ("prefill", 512, 4), "decode": ("decode", 1, 16), "prefill4096": ("prefill", 4096, 2),
             "prefill4096_zipf": ("zipf", 4096, 2), "dsv2_mixed": ("dsv2", 1304, 4), "stack48": ("stack", 2048, 48),
             "runtime_decode": ("rtdecode", 1, 4)}
-    # the 48-layer stack pins 58 GB of host masters, and the runtime's host
-    # cost is a separate question: both run only when asked for
-    order = [args.workload] + ([] if args.no_extra else [w for w in plan
-                                                         if w not in (args.workload, "stack48", "runtime_decode")])
+    # the 48-layer stack pins 58 GB of host masters: it runs only when asked for
+    order = [args.workload] + ([] if args.no_extra else [w for w in plan if w not in (args.workload, "stack48")])
     records, raw = {}, {}
     for wl in order:
         kind, T, nl = plan[wl]
@@ -962,9 +962,9 @@ def main():
         # extra legs: enough warm-up for the weight pages of every layer copy
         # to be mapped, and steps enough for a stable mean (a few seconds each)
         steps = args.steps if main_leg else {"prefill512": 400, "decode": 500, "prefill4096": 200, "prefill4096_zipf": 20,
-                                                       "dsv2_mixed": 300}[wl]
+                                                       "dsv2_mixed": 300, "runtime_decode": 800}[wl]
         warmup = args.warmup if main_leg else {"prefill512": 100, "decode": 200, "prefill4096": 50, "prefill4096_zipf": 2,
-                                                        "dsv2_mixed": 50}[wl]
+                                                        "dsv2_mixed": 50, "runtime_decode": 80}[wl]
         if kind == "decode":
             steps = max(steps, 1)
         log(f"[bench] {wl}: T={T} layers={nl} steps={steps} warmup={warmup}")
