@@ -535,7 +535,6 @@ def run_zipf_staged(steps, warmup, n_layers, device, seed0):
         copy_gbs = copy_engine_gbs(rt, srcs, device)
     finally:
         rt.close()
-    gemm = zipf_gemm(lay0, xs[0], bias, device)
     t = statistics.mean(times)
     h2d_mean = statistics.mean(h2d)
     pcie = dict(bound="pcie_h2d", achieved=h2d_mean / t / 1e9, peak=copy_gbs, unit="GB/s",
@@ -547,47 +546,8 @@ def run_zipf_staged(steps, warmup, n_layers, device, seed0):
                 resident_experts=len(hottest), demand_slots=8, experts_touched=statistics.mean(n_touched),
                 demand_experts=statistics.mean(n_demand), h2d_bytes_per_layer=h2d_mean,
                 max_rows_per_expert=max_rows, pcie=pcie, layer_tflops=flops / t / 1e12,
-                layers_rotated=n_layers, copy_only_ms=nc * EXPERT_BYTES / copy_gbs / 1e6, grouped_gemm=gemm,
+                layers_rotated=n_layers, copy_only_ms=nc * EXPERT_BYTES / copy_gbs / 1e6,
                 first_layer=(lay0, None), first_x=xs[0], bias=bias)
-
-
-def zipf_gemm(lay, x, bias, device, reps=20):
-    """The grouped SwiGLU GEMM alone over the Zipf-skewed routing of one layer
-    with every expert in HBM: gate/up and down launches bracketed by HIP
-    events; useful flops = 2 * T * k * 3 * I * H (no tile padding)."""
-    import torch
-    from pdscope_amd import layer, ops
-    T = x.shape[0]
-    ws = layer.MoEWorkspace(T, H, I, E, K_TOP, device)
-    slots = ops.slot_table([lay.experts[e] for e in range(E)], device)
-    _, ids, _ = layer.route(x, lay.gate, ws, bias=bias)
-    _, _, _, packed = ws.views(T)
-    ops.pack(ids, E, out=packed, workspace=ws.pack_ws)
-    bm = ops.grouped_block_m((T * K_TOP) // E, int(ws.counts.max().item()))
-    max_tiles = (T * K_TOP + bm - 1) // bm + E
-    bmd = layer.down_block_m(bm, H, I)
-    ts_d = ws.tile_start_down if bmd != bm else ws.tile_start
-    ops.schedule(packed.counts, ws.sel_all, bm, out=ws.tile_start, order=ws.sel_order,
-                 **(dict(block_m2=bmd, out2=ts_d) if bmd != bm else {}))
-    max_tiles_d = (T * K_TOP + bmd - 1) // bmd + E
-    stream = torch.cuda.current_stream(device)
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(reps + 2)]
-    for r in range(reps + 2):
-        ev[r][0].record(stream)
-        ops.swiglu_grouped_gateup(x, packed.perm_token, packed.offsets, ws.sel_order, ws.tile_start, max_tiles, bm,
-                                  slots, H, I, ws.h_ws)
-        ev[r][1].record(stream)
-        ops.swiglu_grouped_down(ws.h_ws, packed.offsets, ws.sel_order, ts_d, max_tiles_d, bmd, slots, H, I, ws.y)
-        ev[r][2].record(stream)
-    torch.cuda.synchronize(device)
-    gu = statistics.mean(ev[r][0].elapsed_time(ev[r][1]) for r in range(2, reps + 2))
-    dn = statistics.mean(ev[r][1].elapsed_time(ev[r][2]) for r in range(2, reps + 2))
-    counts = ws.counts.cpu().tolist()
-    flops = 2.0 * T * K_TOP * 3 * I * H
-    achieved = flops / ((gu + dn) / 1e3) / 1e12
-    return dict(gateup_ms=gu, down_ms=dn, block_m=bm, max_rows=max(counts), experts_touched=sum(c > 0 for c in counts),
-                mfma=dict(bound="mfma", achieved=achieved, peak=BF16_PEAK_TFLOPS, unit="TFLOP/s",
-                          frac=achieved / BF16_PEAK_TFLOPS))
 
 
 def run_stack(n_layers, device, seed0, T_prefill=2048, n_decode=64, cap_gib=24, hot_per_layer=40, demand_slots=8):
