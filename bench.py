@@ -1019,10 +1019,10 @@ def main():
                 "prefill4096_zipf": "Qwen3-30B-A3B-shaped MoE layer, prefill T=4096 with a Zipf(1.1) router bias, "
                                     "32 experts resident, the rest staged through 8 demand slots",
                 "runtime_decode": "Qwen3-30B-A3B-shaped MoE layers through PDScopeCudaRuntime.forward, decode T=1, "
-                                  "all 128 experts resident, graph replay with next-layer prediction; a step is "
+                                  "all 128 experts resident, bound single-launch layer with next-layer prediction; a step is "
                                   "one layer call (host cost of the runtime included)",
                 "stack48": "48 Qwen3-30B-A3B-shaped MoE blocks (identity attention + RMSNorm), prefill 2048 then 64 "
-                           "decode steps, 24 GiB expert-slot cap, gate-fallback prefetch, decode graph replay; "
+                           "decode steps, 24 GiB expert-slot cap, gate-fallback prefetch, bound single-launch decode; "
                            "value is decode tok/s"}
     kind, T, nl = plan[args.workload]
     line = {

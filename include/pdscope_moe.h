@@ -298,6 +298,44 @@ int pdscope_decode_layer_chained(const void *x, const void *resid, void *x_out, 
                                  void *workspace, void *stream);
 
 /*
+ * A bound resident decode layer: replaces the per-expert resident graph
+ * replay of the reference (ResidentExpertGraphs.__call__,
+ * expertbench/executor.py:113-135: input copy, replay, output copy) together
+ * with the routing read-back that reveals the demand
+ * (expertbench/pdscope_runtime.py:25-26, :249).
+ *
+ * pdscope_decode_bind checks and plans every argument of
+ * pdscope_decode_layer_chained that stays put from one token to the next
+ * (resid / x_out are not bound: NULL) and keeps them in a host record
+ * (*binding, freed by pdscope_decode_unbind); the pointed-to buffers must
+ * outlive it.  ids [k] int32 is device scratch of the binding; host_ids
+ * (2k words), host_error and host_seq (1 word each) must be pinned host
+ * memory (hipHostMalloc), else the call fails.
+ *
+ * pdscope_decode_run enqueues on `stream`, on the binding's device: the
+ * fused decode kernel (inputs x, outputs out / logits / weights as in
+ * pdscope_decode_layer), then one read-back kernel that writes host_ids[0,k)
+ * = the routed ids, host_ids[k,2k) = the next-layer prediction (when bound
+ * with next_gate), *host_error = the sticky error word of the workspace,
+ * when selected != NULL selected[0,k) = the routed ids as int64 (device),
+ * and last, after a system-scope release, *host_seq = seq.  A host that
+ * reads seq there may read the other words, and the decode launch has
+ * completed (so has anything the stream ordered before it); an event
+ * recorded later on `stream` gives the same guarantee.  Two launches per
+ * token, no graph: replaying a captured graph of the same kernel costs the
+ * host several times more.  Calls that share a binding or its workspace must
+ * be ordered on one stream.
+ */
+typedef struct pdscope_decode_binding pdscope_decode_binding;
+int pdscope_decode_bind(const void *gate, const float *bias, int H, int E, int k, int normalize, int merge_mode,
+                        const void *const *slots, int I, const void *next_gate, int32_t *pred_out, int32_t *ids,
+                        float *probs, void *h_ws, void *workspace, int32_t *host_ids, int32_t *host_error,
+                        int32_t *host_seq, pdscope_decode_binding **binding);
+int pdscope_decode_run(const pdscope_decode_binding *binding, const void *x, void *out, void *logits,
+                       void *weights, int64_t *selected, int32_t seq, void *stream);
+void pdscope_decode_unbind(pdscope_decode_binding *binding);
+
+/*
  * A7 demand staging: replaces the three per-projection non_blocking copies
  * (expertbench/executor.py:341-363).  One hipMemcpyAsync of `bytes` from
  * page-locked host memory into a cache or staging slot on `stream`, then

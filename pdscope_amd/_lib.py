@@ -47,6 +47,10 @@ SIGNATURES = {
                               _vp, _vp], _i32),
     "pdscope_decode_layer_chained": ([_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _i32, _vp, _vp,
                                       _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp], _i32),
+    "pdscope_decode_bind": ([_vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                             _vp, _vp, ctypes.POINTER(_vp)], _i32),
+    "pdscope_decode_run": ([_vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp], _i32),
+    "pdscope_decode_unbind": ([_vp], None),
     "pdscope_stage_expert": ([_vp, _vp, _sz, _vp, _vp], _i32),
     "pdscope_stage_merge": ([_vp, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _vp], _i32),
     "pdscope_dispatch_pack": ([_vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp], _i32),
@@ -79,11 +83,17 @@ def call(name: str, *args) -> int:
     lib = load()
     rc = getattr(lib, name)(*args)
     if isinstance(rc, int) and rc != 0:
-        msg = lib.pdscope_last_error().decode(errors="replace")
-        if rc == 1:
-            raise ValueError(f"{name}: {msg}")
-        raise PDScopeError(f"{name} failed ({rc}): {msg}")
+        raise_for(name, rc)
     return rc
+
+
+def raise_for(name: str, rc: int):
+    """Raise for the non-zero status `rc` of entry point `name`: ValueError for
+    an invalid argument, PDScopeError for a HIP error."""
+    msg = load().pdscope_last_error().decode(errors="replace")
+    if rc == 1:
+        raise ValueError(f"{name}: {msg}")
+    raise PDScopeError(f"{name} failed ({rc}): {msg}")
 
 
 def version() -> str:

@@ -1,4 +1,4 @@
-"""Build libpdscope_moe.so (gfx950) and the pdscope_layer_dispatch extension in-tree.
+"""Build libpdscope_moe.so (gfx950) and the host extension modules in-tree.
 
     python -m pdscope_amd.build          # or __graft_entry__.build()
 
@@ -8,7 +8,8 @@ pdscope_amd/libpdscope_moe.so next to this file.  The CPython extension
 module pdscope_layer_dispatch (csrc/layer_dispatch_module.cpp, host code only)
 is compiled with the host C++ compiler into
 pdscope_amd/pdscope_layer_dispatch<EXT_SUFFIX>; it loads the HIP library at
-import.
+import.  pdscope_amd._records (csrc/records_module.cpp, host code only) is the
+C base type of the ledger's key records.
 """
 from __future__ import annotations
 
@@ -70,29 +71,42 @@ def build(verbose: bool = False) -> Path:
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB} from {len(sources)} sources", file=sys.stderr)
-    mod = build_dispatch_module()
-    if verbose:
-        print(f"built {mod}", file=sys.stderr)
+    for mod in (build_dispatch_module(), build_records_module()):
+        if verbose:
+            print(f"built {mod}", file=sys.stderr)
     return LIB
 
 
+_EXT = sysconfig.get_config_var("EXT_SUFFIX") or ".so"
 DISPATCH_SRC = CSRC / "layer_dispatch_module.cpp"
-DISPATCH_MODULE = PKG / ("pdscope_layer_dispatch" + (sysconfig.get_config_var("EXT_SUFFIX") or ".so"))
+DISPATCH_MODULE = PKG / ("pdscope_layer_dispatch" + _EXT)
+RECORDS_SRC = CSRC / "records_module.cpp"
+RECORDS_MODULE = PKG / ("_records" + _EXT)
+
+
+def _build_host_module(src: Path, out: Path, libs=()) -> Path:
+    """One CPython extension module from one C++ source (host code only)."""
+    cxx = shutil.which("g++") or shutil.which("c++")
+    if cxx is None:
+        raise RuntimeError(f"no host C++ compiler for the {out.name} extension")
+    tmp = out.with_name(out.name + ".tmp")
+    cmd = [cxx, "-O2", "-std=c++17", "-shared", "-fPIC", "-fvisibility=hidden", "-Wall", "-Wextra",
+           f"-I{sysconfig.get_paths()['include']}", str(src), "-o", str(tmp), *libs]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"{out.name} build failed:\n{proc.stderr[-6000:]}")
+    os.replace(tmp, out)
+    return out
 
 
 def build_dispatch_module() -> Path:
     """The pdscope_layer_dispatch extension (plain CPython API, no GPU code)."""
-    cxx = shutil.which("g++") or shutil.which("c++")
-    if cxx is None:
-        raise RuntimeError("no host C++ compiler for the pdscope_layer_dispatch extension")
-    tmp = DISPATCH_MODULE.with_name(DISPATCH_MODULE.name + ".tmp")
-    cmd = [cxx, "-O2", "-std=c++17", "-shared", "-fPIC", "-fvisibility=hidden", "-Wall", "-Wextra",
-           f"-I{sysconfig.get_paths()['include']}", str(DISPATCH_SRC), "-o", str(tmp), "-ldl"]
-    proc = subprocess.run(cmd, capture_output=True, text=True)
-    if proc.returncode != 0:
-        raise RuntimeError(f"pdscope_layer_dispatch build failed:\n{proc.stderr[-6000:]}")
-    os.replace(tmp, DISPATCH_MODULE)
-    return DISPATCH_MODULE
+    return _build_host_module(DISPATCH_SRC, DISPATCH_MODULE, ["-ldl"])
+
+
+def build_records_module() -> Path:
+    """pdscope_amd._records, the ledger's record base type (plain CPython API)."""
+    return _build_host_module(RECORDS_SRC, RECORDS_MODULE)
 
 
 if __name__ == "__main__":

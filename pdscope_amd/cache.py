@@ -40,9 +40,33 @@ import itertools
 from collections import Counter
 from collections.abc import Mapping
 from dataclasses import dataclass, field
+from functools import partial
 from types import MappingProxyType
 from typing import NamedTuple
 from uuid import uuid4
+
+try:
+    # hash and ==/!= of the key records in C (built by pdscope_amd.build)
+    from ._records import HashedRecord as _RecordBase
+except ImportError:     # not built: the same semantics in Python
+    class _RecordBase:
+        """Record with a cached field tuple (_t) and hash (_h): equal only to a
+        record of the same class with equal fields."""
+        __slots__ = ()
+
+        def __eq__(self, other):
+            if self is other:
+                return True
+            if other.__class__ is self.__class__:
+                return self._h == other._h and self._t == other._t
+            return NotImplemented
+
+        def __ne__(self, other):
+            eq = self.__eq__(other)
+            return eq if eq is NotImplemented else not eq
+
+        def __hash__(self):
+            return self._h
 
 
 class CacheError(ValueError):
@@ -61,7 +85,7 @@ def _require_int(value, what, low=0):
 # ---------------------------------------------------------------- public records
 
 @dataclass(frozen=True, order=True)
-class ExpertKey:
+class ExpertKey(_RecordBase):
     layer: int
     expert: int
     representation: str
@@ -72,20 +96,15 @@ class ExpertKey:
         if not isinstance(self.representation, str) or not self.representation:
             raise CacheError("an expert key names its representation")
         # the ledger hashes and compares keys on every transition: the field
-        # tuple and its hash are computed once (the record is immutable)
+        # tuple and its hash are computed once (the record is immutable) and
+        # the base answers hash() and == from them
         t = (self.layer, self.expert, self.representation)
         object.__setattr__(self, "_t", t)
         object.__setattr__(self, "_h", hash(t))
 
-    def __eq__(self, other):
-        if self is other:
-            return True
-        if other.__class__ is self.__class__:
-            return self._t == other._t
-        return NotImplemented
-
-    def __hash__(self):
-        return self._h
+    __eq__ = _RecordBase.__eq__
+    __ne__ = _RecordBase.__ne__
+    __hash__ = _RecordBase.__hash__
 
     def __reduce__(self):
         # rebuilt through __init__, so the cached hash is recomputed where the
@@ -108,7 +127,7 @@ class DemandID:
 
 
 @dataclass(frozen=True)
-class LoadTicket:
+class LoadTicket(_RecordBase):
     owner: str
     generation: int
     key: ExpertKey
@@ -116,19 +135,15 @@ class LoadTicket:
     slot: int | None     # staging slot index
 
     def __post_init__(self):
-        # tickets key the executor's copy and transfer tables: hash once
-        object.__setattr__(self, "_h", hash((self.owner, self.generation, self.key, self.pool, self.slot)))
+        # tickets key the executor's copy and transfer tables: fields and
+        # hash once, hash() and == from the base
+        t = (self.owner, self.generation, self.key, self.pool, self.slot)
+        object.__setattr__(self, "_t", t)
+        object.__setattr__(self, "_h", hash(t))
 
-    def __eq__(self, other):
-        if self is other:
-            return True
-        if other.__class__ is self.__class__:
-            return (self._h == other._h and self.generation == other.generation and self.owner == other.owner
-                    and self.key == other.key and self.pool == other.pool and self.slot == other.slot)
-        return NotImplemented
-
-    def __hash__(self):
-        return self._h
+    __eq__ = _RecordBase.__eq__
+    __ne__ = _RecordBase.__ne__
+    __hash__ = _RecordBase.__hash__
 
     def __reduce__(self):
         return (LoadTicket, (self.owner, self.generation, self.key, self.pool, self.slot))
@@ -170,6 +185,12 @@ class DemandObservation(NamedTuple):
         return self.hit_source is not None
 
 
+# the hot loops build these from a field tuple in one C call, without the
+# Python-level __new__ a NamedTuple class generates
+_new_use_handle = partial(tuple.__new__, UseHandle)
+_new_observation = partial(tuple.__new__, DemandObservation)
+
+
 @dataclass(frozen=True)
 class RetentionHint:
     source: DemandID
@@ -180,6 +201,10 @@ class RetentionHint:
 # ---------------------------------------------------------------- internals
 
 RESERVED, IN_FLIGHT, READY = "reserved", "in_flight", "ready"
+
+# counter of a ready hit by the source of the copy it hit
+_HIT_KIND = {"history": "history_ready_hits", "fresh_prefetch": "fresh_prefetch_hits",
+             "fresh_refresh": "fresh_refresh_hits"}
 
 
 @dataclass
@@ -237,24 +262,27 @@ class _Ranking:
         return len(self._rank_of)
 
     def put(self, key, rank):
-        if self._rank_of.get(key) == rank:
+        rank_of = self._rank_of
+        old = rank_of.get(key)
+        if old == rank:
             return
-        self.discard(key)
+        if old is not None:
+            self.discard(key)
         bucket = self._buckets.get(rank)
         if bucket is None:
             bucket = self._buckets[rank] = []
             bisect.insort(self._ranks, rank)
-        t = _order(key)
+        t = key._t   # _order(key), inline on this path
         bisect.insort(bucket, t)
         self._key_of[t] = key
-        self._rank_of[key] = rank
+        rank_of[key] = rank
 
     def discard(self, key):
         rank = self._rank_of.pop(key, None)
         if rank is None:
             return
         bucket = self._buckets[rank]
-        t = _order(key)
+        t = key._t
         del bucket[bisect.bisect_left(bucket, t)]
         del self._key_of[t]
         if not bucket:
@@ -439,18 +467,26 @@ class ExpertCache:
             home.discard(key)
 
     def _reindex(self, key):
-        """Place `key` in the ranking its copy belongs to now (or in none)."""
+        """Place `key` in the ranking its copy belongs to now (or in none).
+        (_evictable, _is_protected and _rank, inline: every release and
+        retention change passes here.)"""
         c = self._copies.get(key)
         target = None
-        if c is not None and self._evictable(key, c):
-            target = self._protected_rank if self._is_protected(key) else self._unprotected
-        home = self._ranked.get(key)
+        r = self._reveal
+        if (c is not None and self.policy != "static" and c.ticket.pool == "cache" and c.phase == READY
+                and not c.holders and (r is None or key not in r.open_keys)):
+            hint = self._hint
+            target = (self._protected_rank if key in self._protected or (hint is not None and key in hint.keys)
+                      else self._unprotected)
+        ranked = self._ranked
+        home = ranked.get(key)
         if home is not None and home is not target:
             home.discard(key)
-            del self._ranked[key]
+            del ranked[key]
         if target is not None:
-            target.put(key, self._rank(key))
-            self._ranked[key] = target
+            tick = self._last_tick.get(key, 0)
+            target.put(key, (self._times_demanded[key], tick) if self.policy == "LFU" else (tick,))
+            ranked[key] = target
 
     def _choose_victims(self, size):
         """Cheapest evictable copies freeing room for `size` more bytes, or
@@ -558,11 +594,14 @@ class ExpertCache:
         counts = tuple(sorted(dict(token_counts).items(), key=_order_item))
         if not counts:
             raise CacheError("an empty demand cannot be revealed")
+        registry, layer = self.expert_bytes, identity.layer
         for key, n in counts:
-            self._registered(key)
-            if key.layer != identity.layer:
+            if key not in registry:
+                self._registered(key)
+            if key.layer != layer:
                 raise CacheError("every demanded expert belongs to the revealed layer")
-            _require_int(n, "tokens per expert", 1)
+            if type(n) is not int or n < 1:
+                _require_int(n, "tokens per expert", 1)
         physical = dict(counts)
         if valid_token_counts is not None and not isinstance(valid_token_counts, Mapping):
             raise CacheError("valid token counts must be a mapping")
@@ -588,61 +627,83 @@ class ExpertCache:
             if missing:
                 raise CacheError("the initial hot set must be loaded before the first demand")
         self._drop_hint()   # a hint covers one layer ahead only
-        observations = tuple(self._observe(key, n, valid.get(key, 0)) for key, n in counts)
+        copies, valid_get = self._copies, valid.get
+        obs = []
+        for key, n in counts:   # _observe_copy, inline
+            c = copies.get(key)
+            if c is None:
+                obs.append(_new_observation((key, n, valid_get(key, 0), registry[key], "absent", None, None)))
+                continue
+            phase = c.phase
+            source = None
+            if phase == READY:
+                source = (f"fresh_{c.origin}" if c.origin in ("prefetch", "refresh") and not c.used
+                          else "history")
+            obs.append(_new_observation((key, n, valid_get(key, 0), registry[key],
+                                         "in_use" if c.holders else "ready" if phase == READY else "loading",
+                                         c.ticket.pool, source)))
+        observations = tuple(obs)
         self._tick += 1
-        self._count_reveal(observations)
-        for o in observations:
-            if o.valid_tokens:
-                self._times_demanded[o.key] += 1
-                self._last_tick[o.key] = self._tick
+        self._account_reveal(observations, self._tick)
         self._reveal = _Reveal(identity, counts, valid, observations, set(physical))
         # open experts cannot be evicted: they leave the rankings (what
         # _reindex does for a key that is not evictable)
+        ranked = self._ranked
         for key in physical:
-            self._unrank(key)
+            home = ranked.pop(key, None)
+            if home is not None:
+                home.discard(key)
         return observations
 
     def _observe(self, key, tokens, valid_tokens):
-        c = self._copies.get(key)
+        return self._observe_copy(key, tokens, valid_tokens, self._copies.get(key), self.expert_bytes[key])
+
+    @staticmethod
+    def _observe_copy(key, tokens, valid_tokens, c, nbytes):
+        """The observation of `key` at its reveal, given its copy `c` (or None)."""
+        if c is None:
+            return DemandObservation(key, tokens, valid_tokens, nbytes, "absent", None, None)
         source = None
-        if c is not None and c.phase == READY:
+        if c.phase == READY:
             fresh = c.origin in ("prefetch", "refresh") and not c.used
             source = f"fresh_{c.origin}" if fresh else "history"
-        return DemandObservation(key, tokens, valid_tokens, self.expert_bytes[key],
-                                 c.state if c is not None else "absent", c.ticket.pool if c is not None else None,
-                                 source)
+        state = "in_use" if c.holders else "ready" if c.phase == READY else "loading"
+        return DemandObservation(key, tokens, valid_tokens, nbytes, state, c.ticket.pool, source)
 
-    def _count_reveal(self, observations):
-        # sums per counter first, each counter then updated once; a counter
-        # is touched (and so listed in stats()) under the same conditions as
-        # when it is counted per observation
+    def _account_reveal(self, observations, tick):
+        """Counters, demand frequencies and last-demand ticks of one reveal.
+        Sums per counter first, each counter then updated once; a counter is
+        touched (and so listed in stats()) under the same conditions, and in
+        the same order, as when it is counted per observation."""
         n = self._counters
         n["physical_layer_events"] += 1
-        n["demand_events"] += int(any(o.valid_tokens for o in observations))
+        n["demand_events"] += int(any(o[2] for o in observations))
+        demanded, last_tick = self._times_demanded, self._last_tick
         tokens = padding = ready = 0
         pad_only = demands = d_tokens = d_bytes = 0
         hits = hit_tokens = hit_bytes = 0
         kinds = {}
-        for o in observations:
-            tokens += o.tokens
-            padding += o.tokens - o.valid_tokens
-            hit = o.hit_source is not None
+        for key, t, valid, nbytes, state, pool, source in observations:
+            tokens += t
+            padding += t - valid
+            hit = source is not None
             ready += hit
-            if not o.valid_tokens:
+            if not valid:
                 pad_only += 1
                 continue
+            demanded[key] += 1
+            last_tick[key] = tick
             demands += 1
-            d_tokens += o.valid_tokens
-            d_bytes += o.nbytes
+            d_tokens += valid
+            d_bytes += nbytes
             if hit:
                 hits += 1
-                hit_tokens += o.valid_tokens
-                hit_bytes += o.nbytes
-                for name in (f"{o.hit_source}_hits" if o.hit_source != "history" else "history_ready_hits",
-                             "cache_resident_hits" if o.pool_at_reveal == "cache" else "staging_ready_hits"):
+                hit_tokens += valid
+                hit_bytes += nbytes
+                for name in (_HIT_KIND[source], "cache_resident_hits" if pool == "cache" else "staging_ready_hits"):
                     kinds[name] = kinds.get(name, 0) + 1
             else:
-                name = "loading_misses" if o.state_at_reveal in ("loading", "in_use") else "absent_misses"
+                name = "loading_misses" if state in ("loading", "in_use") else "absent_misses"
                 kinds[name] = kinds.get(name, 0) + 1
         n["physical_expert_demands"] += len(observations)
         n["physical_demand_tokens"] += tokens
@@ -764,35 +825,60 @@ class ExpertCache:
 
     def acquire(self, key):
         """Hold a ready copy of an open expert for a computation."""
-        self._require_open(key)
-        c = self._copies.get(key)
-        if c is None or c.phase != READY:
-            raise CacheError("no ready copy to compute with (a loading copy is not a hit)")
-        handle = UseHandle(c.ticket, next(self._serials))
-        c.holders.add(handle.serial)
-        # an open expert is in no ranking (the reveal took it out and only a
-        # closed one goes back), so holding it changes no ranking
-        return handle
+        return self.acquire_many((key,))[0]
+
+    def acquire_many(self, keys):
+        """acquire() of each key in order, in one call: the same checks, the
+        same use serials (a failing key leaves the earlier ones held, as a
+        sequence of acquire() calls would)."""
+        registry, copies, serials = self.expert_bytes, self._copies, self._serials
+        r = self._reveal
+        handles = []
+        for key in keys:
+            if key not in registry:
+                self._registered(key)
+            if r is None or key not in r.open_keys:
+                raise CacheError(f"{key!r} is not an unfinished expert of the active demand")
+            c = copies.get(key)
+            if c is None or c.phase != READY:
+                raise CacheError("no ready copy to compute with (a loading copy is not a hit)")
+            handle = _new_use_handle((c.ticket, next(serials)))
+            c.holders.add(handle.serial)
+            # an open expert is in no ranking (the reveal took it out and only
+            # a closed one goes back), so holding it changes no ranking
+            handles.append(handle)
+        return tuple(handles)
 
     def release(self, handle):
         """The computation holding this copy has completed; the last release of
         an expert completes it for the open demand (a staged copy then leaves)."""
-        c = self._copy_for(handle.ticket)
-        if handle.serial not in c.holders:
-            raise CacheError("the use handle is stale, foreign or already released")
-        key = handle.ticket.key
-        c.holders.discard(handle.serial)
-        valid = key in self._reveal.valid
-        c.used = c.used or valid
-        if c.holders:
-            return
-        self._reveal.open_keys.discard(key)
-        self._counters["gpu_completed_experts"] += 1
-        self._counters["gpu_completed_valid_experts"] += int(valid)
-        if c.ticket.pool == "demand_staging":
-            self._drop(key)
-        else:
-            self._reindex(key)
+        self.release_many((handle,))
+
+    def release_many(self, handles):
+        """release() of each handle in order, in one call (same checks and
+        transitions; a failing handle leaves the earlier ones released)."""
+        r, counters, copies = self._reveal, self._counters, self._copies
+        for handle in handles:
+            ticket = handle.ticket
+            key = ticket.key
+            c = copies.get(key)   # _copy_for, inline
+            if c is None or (c.ticket is not ticket and c.ticket != ticket):
+                raise CacheError("the ticket belongs to no live copy of this ledger")
+            serial, holders = handle.serial, c.holders
+            if serial not in holders:
+                raise CacheError("the use handle is stale, foreign or already released")
+            holders.discard(serial)
+            valid = key in r.valid
+            c.used = c.used or valid
+            if holders:
+                continue
+            r.open_keys.discard(key)
+            counters["gpu_completed_experts"] += 1
+            counters["gpu_completed_valid_experts"] += int(valid)
+            if c.ticket.pool == "demand_staging":
+                self._drop(key)
+            else:
+                self._reindex(key)
 
     def finish_cpu(self, key):
         """The expert of the open demand was computed on the CPU from its master."""

@@ -158,7 +158,8 @@ class MeasureSession:
             native_completed_chunks=0,
             cache_payload_allowance_bytes=rt.cache.cache_bytes,
             source_metrics_delta={}, resident_graphs=(dict(calibration=rt.graph_cost_calibration,
-                                                           graphs=len(rt._graphs)) if rt.resident_graphs else None),
+                                                           replays=rt.bound_launches,
+                                                           bindings=len(rt._bindings)) if rt.resident_graphs else None),
             cache_pool_reserved_bytes=ex.storage()["cache_reserved_tensor_bytes"],
             demand_staging_bytes=sum(rt.cache.staging_slot_bytes),
             demand_staging_aliases="declared demand slots; one expert payload per slot",

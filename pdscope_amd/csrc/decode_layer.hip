@@ -51,6 +51,7 @@
 // and decode_down_kernel, so the result is bitwise the result of the
 // three-launch path (pdscope_route_topk + pdscope_swiglu_decode).
 #include <mutex>
+#include <new>
 #include <unordered_map>
 
 #include "common.h"
@@ -657,12 +658,12 @@ PD_API int pdscope_decode_layer_chained_supported(int H, int I, int E, int k, in
     return n >= plan.blocks ? 1 : 0;
 }
 
-// Shared by both entry points: checks, plan, launch.
-static int launch_decode_layer(const void *x, const void *resid, void *x_out, const void *gate, const float *bias,
-                               int H, int E, int k, int normalize, int merge_mode, const void *const *slots, int I,
-                               const void *next_gate, int32_t *pred_out, void *logits,
-                               int32_t *ids, void *weights, float *probs, void *h_ws, void *out, void *workspace,
-                               void *stream) {
+// Argument checks and plan shared by every entry point; the kernel variant
+// (plain, or with the residual / next-layer predictor code) goes to *fn.
+static int plan_decode_layer(const void *x, bool chain, const void *gate, int H, int E, int k, int merge_mode,
+                             const void *const *slots, int I, const void *next_gate, const int32_t *pred_out,
+                             const void *logits, const int32_t *ids, const void *weights, const void *h_ws,
+                             const void *out, const void *workspace, DecodePlan *plan, DecodeLayerFn *fn) {
     if (!x || !gate || !slots || !logits || !ids || !weights || !h_ws || !out || !workspace)
         return fail(kEInval, "decode_layer: null pointer");
     if (H < 16 || H % 16) return fail(kEInval, "decode_layer: need H % 16 == 0");
@@ -676,15 +677,27 @@ static int launch_decode_layer(const void *x, const void *resid, void *x_out, co
     if (!next_gate != !pred_out) return fail(kEInval, "decode_layer: next_gate and pred_out go together");
     if (next_gate && 2 * ((E + 3) / 4) > (H + 3) / 4)
         return fail(kEInval, "decode_layer: the next-layer predictor needs E <= H/2");
-    DecodePlan plan;
     std::string why;
-    if (pick_decode(H, I, k, &plan, &why) != kOk) return fail(kEInval, why);
-    const bool chain = resid || next_gate;
-    const DecodeLayerFn fn = chain ? plan.fn_chain : plan.fn;
-    const int resident = resident_blocks(fn, plan.lds, &why);
+    if (pick_decode(H, I, k, plan, &why) != kOk) return fail(kEInval, why);
+    *fn = chain ? plan->fn_chain : plan->fn;
+    const int resident = resident_blocks(*fn, plan->lds, &why);
     if (resident < 0) return fail(kEHip, why);
-    if (resident < plan.blocks)
+    if (resident < plan->blocks)
         return fail(kEInval, "decode_layer: the grid would not be resident at once on this device");
+    return kOk;
+}
+
+// Shared by both entry points: checks, plan, launch.
+static int launch_decode_layer(const void *x, const void *resid, void *x_out, const void *gate, const float *bias,
+                               int H, int E, int k, int normalize, int merge_mode, const void *const *slots, int I,
+                               const void *next_gate, int32_t *pred_out, void *logits,
+                               int32_t *ids, void *weights, float *probs, void *h_ws, void *out, void *workspace,
+                               void *stream) {
+    DecodePlan plan;
+    DecodeLayerFn fn = nullptr;
+    const int rc = plan_decode_layer(x, resid || next_gate, gate, H, E, k, merge_mode, slots, I, next_gate, pred_out,
+                                     logits, ids, weights, h_ws, out, workspace, &plan, &fn);
+    if (rc != kOk) return rc;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     fn<<<plan.blocks, 256, plan.lds, s>>>(
         (const uint16_t *)x, (const uint16_t *)resid, (uint16_t *)x_out, (const uint16_t *)gate, bias, H, E, k,
@@ -712,3 +725,128 @@ PD_API int pdscope_decode_layer_chained(const void *x, const void *resid, void *
     return launch_decode_layer(x, resid, x_out, gate, bias, H, E, k, normalize, merge_mode, slots, I, next_gate,
                                pred_out, logits, ids, weights, probs, h_ws, out, workspace, stream);
 }
+
+// ---------------------------------------------------------------- bound decode layer
+//
+// A resident decode layer whose gate, slot table, predictor gate and device
+// buffers stay put from one token to the next is checked and planned once
+// (pdscope_decode_bind); each token is then one call of pdscope_decode_run:
+// the fused decode kernel, then a one-wave read-back kernel that writes the
+// routed ids, the next-layer prediction and the sticky error word into pinned
+// host memory, the routed ids as int64 into the caller's device tensor, and
+// last, after a system-scope release, the call's sequence number into a
+// pinned host word: a host that sees that number there can read the other
+// words, and knows that the decode launch (ordered before the read-back on
+// the stream) has completed.  On this device a
+// direct launch costs the host about 3 us against about 23 us for replaying
+// a captured graph of the same kernel.
+
+namespace pd {
+
+__global__ __launch_bounds__(64) void decode_readback_kernel(const int32_t *__restrict__ ids,
+                                                             const int32_t *__restrict__ pred,
+                                                             const uint32_t *__restrict__ err, int k,
+                                                             int32_t *host_ids, int32_t *host_err,
+                                                             int64_t *__restrict__ selected, int32_t *host_seq,
+                                                             int32_t seq) {
+    const int j = threadIdx.x;
+    if (j < k) {
+        const int32_t e = ids[j];
+        // vector stores at system scope: the words reach host memory without
+        // waiting for a cache write-back at the end of the kernel
+        __hip_atomic_store(host_ids + j, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        if (pred) __hip_atomic_store(host_ids + k + j, pred[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        if (selected) selected[j] = (int64_t)e;
+    }
+    if (j == 0) {
+        const uint32_t w = __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(host_err, (int32_t)w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+    // every lane's words above are performed before the sequence number
+    __syncthreads();
+    if (j == 0 && host_seq) __hip_atomic_store(host_seq, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+}  // namespace pd
+
+struct pdscope_decode_binding {
+    DecodeLayerFn fn;
+    int blocks;
+    size_t lds;
+    int device;
+    const uint16_t *gate;
+    const float *bias;
+    int H, E, k, normalize, merge_mode, I;
+    const uint16_t *const *slots;
+    const uint16_t *next_gate;
+    int32_t *pred_out;
+    int32_t *ids;
+    float *probs;
+    uint16_t *h_ws;
+    uint32_t *workspace;
+    int32_t *host_ids;   // device addresses of the pinned read-back words
+    int32_t *host_err;
+    int32_t *host_seq;
+};
+
+// Device address of a word of pinned host memory (an error if it is not).
+static int pinned_device_address(void *host, int32_t **dev, const char *what) {
+    void *d = nullptr;
+    if (hipHostGetDevicePointer(&d, host, 0) != hipSuccess || !d) {
+        (void)hipGetLastError();
+        return fail(kEInval, std::string("decode_bind: ") + what + " must be pinned host memory");
+    }
+    *dev = static_cast<int32_t *>(d);
+    return kOk;
+}
+
+PD_API int pdscope_decode_bind(const void *gate, const float *bias, int H, int E, int k, int normalize,
+                               int merge_mode, const void *const *slots, int I, const void *next_gate,
+                               int32_t *pred_out, int32_t *ids, float *probs, void *h_ws, void *workspace,
+                               int32_t *host_ids, int32_t *host_error, int32_t *host_seq,
+                               pdscope_decode_binding **binding) {
+    if (!binding) return fail(kEInval, "decode_bind: null binding out-pointer");
+    *binding = nullptr;
+    if (!host_ids || !host_error || !host_seq) return fail(kEInval, "decode_bind: null read-back pointer");
+    DecodePlan plan;
+    DecodeLayerFn fn = nullptr;
+    // x, logits, weights and out arrive with each run: stand-ins pass the null checks here
+    const void *later = gate;
+    int rc = plan_decode_layer(later, next_gate != nullptr, gate, H, E, k, merge_mode, slots, I, next_gate, pred_out,
+                               later, ids, later, h_ws, later, workspace, &plan, &fn);
+    if (rc != kOk) return rc;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return fail(kEHip, "decode_bind: hipGetDevice failed");
+    int32_t *dh = nullptr, *de = nullptr, *dq = nullptr;
+    if ((rc = pinned_device_address(host_ids, &dh, "host_ids")) != kOk) return rc;
+    if ((rc = pinned_device_address(host_error, &de, "host_error")) != kOk) return rc;
+    if ((rc = pinned_device_address(host_seq, &dq, "host_seq")) != kOk) return rc;
+    auto *b = new (std::nothrow) pdscope_decode_binding;
+    if (!b) return fail(kEInval, "decode_bind: out of host memory");
+    *b = pdscope_decode_binding{fn, plan.blocks, plan.lds, dev, (const uint16_t *)gate, bias, H, E, k, normalize,
+                                merge_mode, I, (const uint16_t *const *)slots, (const uint16_t *)next_gate,
+                                pred_out, ids, probs, (uint16_t *)h_ws, (uint32_t *)workspace, dh, de, dq};
+    *binding = b;
+    return kOk;
+}
+
+PD_API int pdscope_decode_run(const pdscope_decode_binding *b, const void *x, void *out, void *logits,
+                              void *weights, int64_t *selected, int32_t seq, void *stream) {
+    if (!b) return fail(kEInval, "decode_run: null binding");
+    if (!x || !out || !logits || !weights) return fail(kEInval, "decode_run: null pointer");
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev != b->device)
+        return fail(kEInval, "decode_run: the binding belongs to another device");
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    b->fn<<<b->blocks, 256, b->lds, s>>>(
+        (const uint16_t *)x, nullptr, nullptr, b->gate, b->bias, b->H, b->E, b->k, b->normalize, b->merge_mode,
+        b->slots, b->I, b->next_gate, b->pred_out, (uint16_t *)logits, b->ids, (uint16_t *)weights, b->probs,
+        b->h_ws, (uint16_t *)out, b->workspace);
+    int rc = check_launch("decode_layer_kernel");
+    if (rc != kOk) return rc;
+    decode_readback_kernel<<<1, 64, 0, s>>>(b->ids, b->pred_out, b->workspace + kWsError, b->k, b->host_ids,
+                                            b->host_err, selected, b->host_seq, seq);
+    return check_launch("decode_readback_kernel");
+}
+
+PD_API void pdscope_decode_unbind(pdscope_decode_binding *b) { delete b; }

@@ -91,7 +91,7 @@ class PendingCpu:
 class PendingCompute:
     handles: tuple
     output: object
-    event: object
+    event: object                 # completion event; None for a use accounted after it completed
     input_ref: object
     keys: tuple = ()
     timing_start: object = None   # start event of the launch when stages are profiled
@@ -450,18 +450,19 @@ class ExpertExecutor:
         if launch is None and (completed is None or not completed.query()):
             raise RuntimeError("an already enqueued use of expert copies is accounted only after it has "
                                "completed: pass the completed event recorded after it")
-        handles = tuple(self.cache.acquire(k) for k in keys)
+        handles = self.cache.acquire_many(keys)
+        copies, loads = self.copies, self.loads
         for h in handles:
-            if h.ticket not in self.copies or h.ticket in self.loads:
+            if h.ticket not in copies or h.ticket in loads:
                 raise RuntimeError("acquired a copy whose transfer has not been confirmed")
         if launch is None:
             for h in handles:
                 ev = self._landed.pop(h.ticket, None)
                 if ev is not None:
                     self._free_events.append(ev)
-            ev = self._event()
-            ev.record(torch.cuda.current_stream(self.device) if wait_for is None else wait_for)
-            p = PendingCompute(handles, None, ev, input_ref, tuple(keys))
+            # the work completed before the call: no event of its own
+            # (finish_gpu finds it complete)
+            p = PendingCompute(handles, None, None, input_ref, tuple(keys))
             self.computes[id(p)] = p
             self._log(event="compute_submitted", experts=len(keys))
             return p
@@ -502,17 +503,19 @@ class ExpertExecutor:
         self._open()
         if self.computes.get(id(pending)) is not pending:
             raise ValueError("unknown or already completed GPU computation")
-        if wait:
-            pending.event.synchronize()
-        if not pending.event.query():
-            return None
-        for h in pending.handles:
-            self.cache.release(h)
+        ev = pending.event
+        if ev is not None:   # None: accounted after it had completed
+            if wait:
+                ev.synchronize()
+            if not ev.query():
+                return None
+        self.cache.release_many(pending.handles)
         del self.computes[id(pending)]
         if pending.timing_start is not None:
-            self.stage_timings["gpu_forward_device_span_ms"] = pending.timing_start.elapsed_time(pending.event)
+            self.stage_timings["gpu_forward_device_span_ms"] = pending.timing_start.elapsed_time(ev)
             pending.timing_start = None
-        self._free_events.append(pending.event)
+        if ev is not None:
+            self._free_events.append(ev)
         pending.event, pending.input_ref = None, None
         self.reclaim()
         self._log(event="compute_completed", experts=len(pending.handles))

@@ -418,6 +418,116 @@ def decode_layer(x, gate, slots, I, top_k, normalize, *, bias=None, out, logits,
     return out
 
 
+class DecodeBinding:
+    """One resident decode layer bound once (pdscope_decode_bind): its gate,
+    slot table (by address: refresh the contents, not the tensor), optional
+    next-layer gate and logit bias are checked and planned at construction,
+    and each token is then one C call that launches the fused decode kernel
+    and a read-back kernel.  The read-back writes the routed ids to
+    host[ids_at:ids_at+k], the next-layer prediction to
+    host[ids_at+k:ids_at+2k], the kernel's sticky error word to
+    host[error_at] and last the call's sequence number to host[seq_at]
+    (host: pinned int32 CPU tensor).  The words are readable once
+    host[seq_at] holds the call's number, which also means the decode launch
+    has completed, or once an event recorded after the call on the same
+    stream has completed.
+
+    The binding owns its device scratch (int32 ids, prediction, h) and keeps
+    every tensor it bound alive.  Calls on one device share the fused
+    kernel's workspace, so they must be ordered on one stream."""
+
+    def __init__(self, gate, slots, I, top_k, normalize, *, host, error_at, seq_at=None, ids_at=0,
+                 merge="fused", next_gate=None, bias=None):
+        dev = gate.device
+        _need(gate, "gate", BF16, 2, dev)
+        _need(slots, "slots", torch.int64, 1, dev)
+        E, H = gate.shape
+        k = int(top_k)
+        if slots.numel() < E or not slots.is_contiguous():
+            raise ValueError("DecodeBinding: slots must be a contiguous table of E entries")
+        if next_gate is not None:
+            _need(next_gate, "next_gate", BF16, 2, dev)
+            if tuple(next_gate.shape) != (E, H) or not next_gate.is_contiguous():
+                raise ValueError("DecodeBinding: next_gate must be a contiguous [E, H] tensor like gate")
+        if not gate.is_contiguous():
+            raise ValueError("DecodeBinding: gate must be contiguous")
+        if bias is not None:
+            _need(bias, "bias", torch.float32, 1, dev)
+            if bias.numel() != E:
+                raise ValueError("DecodeBinding: bias must hold E values")
+        if (not isinstance(host, torch.Tensor) or host.device.type != "cpu" or host.dtype != torch.int32
+                or not host.is_pinned() or not host.is_contiguous()):
+            raise ValueError("DecodeBinding: host must be a contiguous pinned int32 CPU tensor")
+        if seq_at is None:
+            seq_at = error_at + 1
+        if not (0 <= ids_at and ids_at + 2 * k <= host.numel() and 0 <= error_at < host.numel()
+                and 0 <= seq_at < host.numel() and seq_at != error_at
+                and not ids_at <= error_at < ids_at + 2 * k and not ids_at <= seq_at < ids_at + 2 * k):
+            raise ValueError("DecodeBinding: read-back words outside host or overlapping")
+        self.H, self.E, self.I, self.k = H, E, int(I), k
+        self.device = dev
+        self.ids = torch.zeros(k, dtype=torch.int32, device=dev)
+        self.pred = torch.full((k,), -1, dtype=torch.int32, device=dev) if next_gate is not None else None
+        self.h_ws = torch.empty(k * self.I, dtype=BF16, device=dev)
+        self.workspace = decode_workspace(dev, H)
+        self._refs = (gate, slots, next_gate, bias, host)
+        lib = _lib.load()
+        handle = ctypes.c_void_p()
+        base = host.data_ptr()
+        with torch.cuda.device(dev):
+            rc = lib.pdscope_decode_bind(_p(gate), _p(bias), H, E, k, int(bool(normalize)), merge_mode(merge),
+                                         _p(slots), self.I, _p(next_gate), _p(self.pred), _p(self.ids), None,
+                                         _p(self.h_ws), _p(self.workspace), base + 4 * ids_at, base + 4 * error_at,
+                                         base + 4 * seq_at, ctypes.byref(handle))
+        if rc != 0:
+            _lib.raise_for("pdscope_decode_bind", rc)
+        self._handle = handle.value
+        self._run = lib.pdscope_decode_run
+        self._unbind = lib.pdscope_decode_unbind
+
+    def run_ptrs(self, x, out, logits, weights, selected, seq, stream):
+        """The per-token call on raw addresses (x [H], out [H], logits [E],
+        weights [k] bf16, selected [k] int64 or 0), the int32 sequence number
+        the read-back writes last, and a raw hipStream_t, for callers that
+        checked the tensors themselves."""
+        rc = self._run(self._handle, x, out, logits, weights, selected, seq, stream)
+        if rc != 0:
+            _lib.raise_for("pdscope_decode_run", rc)
+
+    def run(self, x, out, logits, weights, selected=None, stream=None, seq=0):
+        """One token: x [1,H] bf16 in; out [1,H], logits [1,E], weights [1,k]
+        bf16 and optionally selected [1,k] int64 out, on `stream` (default:
+        the current stream of the binding's device); host[seq_at] receives
+        `seq` last."""
+        if self._handle is None:
+            raise ValueError("DecodeBinding is closed")
+        dev = self.device
+        for t, n, dt, size in ((x, "x", BF16, self.H), (out, "out", BF16, self.H), (logits, "logits", BF16, self.E),
+                               (weights, "weights", BF16, self.k)):
+            _need(t, n, dt, None, dev)
+            if t.numel() != size or not t.is_contiguous():
+                raise ValueError(f"DecodeBinding.run: {n} must be a contiguous tensor of {size} values")
+        if selected is not None:
+            _need(selected, "selected", torch.int64, None, dev)
+            if selected.numel() != self.k or not selected.is_contiguous():
+                raise ValueError("DecodeBinding.run: selected must be a contiguous tensor of k values")
+        s = torch.cuda.current_stream(dev) if stream is None else stream
+        self.run_ptrs(x.data_ptr(), out.data_ptr(), logits.data_ptr(), weights.data_ptr(),
+                      0 if selected is None else selected.data_ptr(), int(seq), s.cuda_stream)
+
+    def close(self):
+        if self._handle is not None:
+            self._unbind(self._handle)
+            self._handle = None
+            self._refs = ()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 # --------------------------------------------------------------------- A8/A9
 
 def merge(y, row_of, w, out, add_in=None, *, mode="fused"):

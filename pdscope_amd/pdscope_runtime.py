@@ -22,9 +22,14 @@ One layer call:
  5. predicted next-layer experts are prefetched into the cache pool
     (speculative_slots bound, LRU eviction, never evicting the static hot set);
  6. the merge (K5) writes the layer output in token order.
-With ``resident_graphs=True`` a decode layer whose experts are all resident
-replays a captured hipGraph of route + decode (K1 + K4); its ledger accounting
-follows the replay (nothing can evict while the control thread waits).
+With ``resident_graphs=True`` a decode layer is served by its bound
+single-launch decode (K1 + K4 in one kernel, ops.DecodeBinding: arguments
+checked and planned once per layer, then one C call per token that also
+reads the routed ids back into pinned host memory).  On this device that
+direct launch costs the host far less than replaying a captured hipGraph of
+the same kernel, which is what the reference's per-expert resident graphs
+are for.  Its ledger accounting follows the launch (nothing can evict while
+the control thread waits).
 
 Placement.  Given a cost table (``costs``, e.g. costs.FileCosts) AND a
 ``cpu_backend``, each call plans with ``plan_pdscope``
@@ -32,14 +37,17 @@ Placement.  Given a cost table (``costs``, e.g. costs.FileCosts) AND a
 runs on the backend (``cpu_backend(key, rows) -> rows`` or its ``submit``),
 overlapped with the GPU launches, and its outputs fill their rows of the
 grouped output before the merge; resident, demand and prefetch queues follow
-the plan, and the decode graph replay is not used.  Without either, every
-expert runs on the GPU.  There is no built-in CPU expert path.
+the plan, and a decode layer whose plan keeps every routed expert on the GPU
+takes the bound launch after routing.  Without either, every expert runs on
+the GPU.  There is no built-in CPU expert path.
 """
 from __future__ import annotations
 
 import contextlib
 import ctypes
 import hashlib
+import itertools
+import operator
 import statistics
 import time
 from pathlib import Path
@@ -52,6 +60,25 @@ from .adapters.qwen import Routing
 from .cache import DemandID, ExpertCache, ExpertKey
 from .executor import ExpertExecutor
 from .policy import plan_pdscope
+
+# the current stream's raw handle without building a Stream object
+_raw_current_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+# how long the host polls a bound launch's read-back word before it blocks on
+# an event instead (a decode layer takes tens of microseconds)
+_READBACK_POLL_S = 0.002
+
+
+class _HostWordEquals:
+    """Completion test of a bound launch: its read-back wrote `value` into
+    words[at] last (query() as an event's)."""
+    __slots__ = ("words", "at", "value")
+
+    def __init__(self, words, at):
+        self.words, self.at, self.value = words, at, None
+
+    def query(self):
+        return self.value is not None and self.words[self.at] == self.value
 
 
 def load_hot_profile(path, masters, slots):
@@ -148,11 +175,21 @@ class PDScopeCudaRuntime:
         self.prediction_counts = {p: dict(hits=0, total=0) for p in ("prefill", "decode")}
         self._ws = {}
         self._pws = {}
-        self._graphs = {}
+        self._bindings = {}     # bound decode launches, by (layer, k, normalize, gate, next gate)
+        self.bound_launches = 0  # tokens served through them (the reference counts its graph replays)
+        self._out_ring = {}     # graph_output_pool: two output buffers per layer
         self._graph_turn = {}
         self._dispatch_buffers = {}
-        self._pinned_counts = torch.empty(2 * self.E + 64, dtype=torch.int32, pin_memory=True)
+        self._pinned_counts = torch.zeros(2 * self.E + 64, dtype=torch.int32, pin_memory=True)
+        self._pinned_np = self._pinned_counts.numpy()   # host reads without tensor indexing
+        self._streams = {}   # raw hipStream_t -> its torch Stream object
         self._err_at = 2 * self.E + 8    # the decode error word's place in _pinned_counts
+        self._seq_at = 2 * self.E + 9    # the bound launch's sequence word
+        self._seq = 0
+        self._readback = _HostWordEquals(self._pinned_np, self._seq_at)
+        self._decode_ok = {}             # k -> (single launch fits, with the fused predictor)
+        self._out_stash = None           # (raw stream, k, outputs) of the next bound decode call
+        self._keys_full = set()          # layers whose key list holds every expert
         self._copy_done = torch.cuda.Event()
         try:
             for key in hot_keys:
@@ -214,6 +251,68 @@ class PDScopeCudaRuntime:
             self.transient.discard(key)
         self.executor.reclaim()
 
+    def _current_stream(self):
+        """The current stream of the runtime's device, one torch Stream object
+        per raw stream (built on first sight instead of once per call)."""
+        raw = _raw_current_stream(self.device.index) if _raw_current_stream is not None else None
+        s = self._streams.get(raw) if raw is not None else None
+        if s is None:
+            s = torch.cuda.current_stream(self.device)
+            if raw is not None:
+                self._streams[raw] = s
+        return s
+
+    def _layer_keys(self, layer):
+        """The key objects of `layer`'s experts 0..E-1, as a list."""
+        if layer not in self._keys_full:
+            for e in range(self.E):
+                self._key(layer, e)   # fills self._keys[layer]
+            self._keys_full.add(layer)
+        return self._keys[layer]
+
+    def _decode_support(self, k):
+        """(the single-launch decode fits k, and also with the fused next-layer predictor)."""
+        got = self._decode_ok.get(k)
+        if got is None:
+            fits = ops.decode_layer_supported(self.H, self.I, self.E, k, self.device)
+            got = (fits, fits and ops.decode_chained_supported(self.H, self.I, self.E, k, self.device))
+            self._decode_ok[k] = got
+        return got
+
+    def _new_decode_outputs(self, k):
+        """Fresh (out [1,H], logits [1,E], weights [1,k] bf16, selected [1,k]
+        int64) for one bound decode call, on the current stream."""
+        dev, bf16 = self.device, torch.bfloat16
+        return (torch.empty((1, self.H), dtype=bf16, device=dev), torch.empty((1, self.E), dtype=bf16, device=dev),
+                torch.empty((1, k), dtype=bf16, device=dev), torch.empty((1, k), dtype=torch.int64, device=dev))
+
+    def _decode_outputs(self, stream, k):
+        """The output tensors of this bound decode call: the ones allocated
+        during the previous call's wait when they were allocated on this
+        stream for this k (the caching allocator ties a block to the stream
+        it was allocated on), else fresh ones.  Each set is handed out once."""
+        st, self._out_stash = self._out_stash, None
+        if st is not None and st[0] == stream.cuda_stream and st[1] == k:
+            return st[2]
+        return self._new_decode_outputs(k)
+
+    def _await_readback(self, seq, stream):
+        """Poll the pinned sequence word until the bound launch numbered `seq`
+        wrote it (its read-back words have then landed and the launch has
+        completed); after _READBACK_POLL_S, block on an event instead."""
+        words, at = self._pinned_np, self._seq_at
+        self._readback.value = seq
+        if words[at] == seq:
+            return
+        deadline = time.perf_counter() + _READBACK_POLL_S
+        while words[at] != seq:
+            if time.perf_counter() > deadline:
+                self._copy_done.record(stream)
+                self._copy_done.synchronize()
+                if words[at] != seq:
+                    raise RuntimeError("a bound decode launch completed without its read-back words")
+                return
+
     def _layer_fully_resident(self, layer):
         ready = self.cache.ready_in_cache
         return all(ready(self._key(layer, e)) for e in range(self.E))
@@ -225,53 +324,64 @@ class PDScopeCudaRuntime:
         if (inputs.ndim != 2 or (step > 0 and inputs.shape[0] != 1) or (step == 0 and inputs.shape[0] < 2)
                 or layer not in self.layers):
             raise ValueError("invalid prefill/decode activation or layer")
-        if inputs.device != self.device or inputs.dtype != torch.bfloat16:
-            raise ValueError("inputs must be bf16 on the runtime device")
+        if inputs.device != self.device or inputs.dtype != torch.bfloat16 or inputs.shape[1] != self.H:
+            raise ValueError("inputs must be bf16 [T, H] on the runtime device")
+        if gate.shape != (self.E, self.H):
+            raise ValueError("gate must be [E, H]")
         phase = "prefill" if step == 0 else "decode"
         started = time.perf_counter()
         T, H = inputs.shape
         E, k = self.E, top_k
         x = inputs.contiguous()
         ws = self._workspace(T, k)
-        cur = torch.cuda.current_stream(self.device)
-        key = lambda e: self._key(layer, e)  # noqa: E731
+        cur = self._current_stream()
+        key = self._layer_keys(layer).__getitem__   # routed ids are range-checked below
         nkey = lambda e: self._key(layer + 1, e)  # noqa: E731
         self.poll()
         before = self.cache.stats()
-        # decode replays the captured single-launch layer over the slot table
+        # decode runs the bound single-launch layer over the slot table
         # (experts without a device copy have a null entry and contribute 0);
         # misses, at most k <= demand_slots of them, are staged in one batch
-        # and the same graph is replayed once more over the completed table
-        # (with fewer slots than k only a fully resident layer replays)
+        # and the same launch runs once more over the completed table
+        # (with fewer slots than k only a fully resident layer takes it)
         planned = self.costs is not None and self.cpu_backend is not None
-        graph_ok = (self.resident_graphs and phase == "decode" and bias is None
-                    and ops.decode_layer_supported(H, self.I, E, k, self.device)
+        fits, fits_pred = self._decode_support(k)
+        graph_ok = (self.resident_graphs and phase == "decode" and bias is None and fits
                     and (k <= self.demand_slots or self._layer_fully_resident(layer)))
-        # unplanned: the first replay also routes; planned: routing comes
-        # first, and the graph serves the layer when the plan keeps every
-        # routed expert on the GPU (decided below)
+        # unplanned: the first launch also routes; planned: routing comes
+        # first, and the bound launch serves the layer when the plan keeps
+        # every routed expert on the GPU (decided below)
         graph_path = graph_ok and not planned
-        ring = 0
+        ring_out = None
         if graph_ok and self.graph_output_pool:
             ring = self._graph_turn.get(layer, 0)
             self._graph_turn[layer] = ring ^ 1
+            ring_out = self._ring_output(layer, ring)
         replay_table, late_replays = None, 0
 
         # ---- 1-2: route (+ predictor), grouping, one D2H of the demand
-        out = torch.empty((T, H), dtype=torch.bfloat16, device=self.device)
+        if graph_ok:
+            # the bound launch writes the output and the routing straight into
+            # the tensors the call returns (allocated during the previous
+            # call's wait where it ran on this stream)
+            d_out, r_logits, r_weights, r_selected = self._decode_outputs(cur, k)
+        else:
+            d_out = torch.empty((T, H), dtype=torch.bfloat16, device=self.device)
+        out = ring_out if graph_path and ring_out is not None else d_out
         predict = prefetch and next_gate is not None
-        # the graph's launch also predicts the next layer where its grid allows
-        graph_pred = next_gate if (graph_path and predict
-                                   and ops.decode_chained_supported(H, self.I, E, k, self.device)) else None
+        # the bound launch also predicts the next layer where its grid allows
+        graph_pred = next_gate if (graph_path and predict and fits_pred) else None
         pred_ids = None
+        bound_routing = graph_path
         if graph_path:
-            # entries the first replay saw (a copy still in flight reads as null)
+            # entries the first launch saw (a copy still in flight reads as null)
             replay_table = list(self.executor.table(layer, E)[1])
-            logits, ids, weights, gout, pred_ids = self._replay_decode_graph(layer, x, gate, normalize, k, out,
-                                                                             ring=ring, next_gate=graph_pred,
-                                                                             stream=cur)
-            if self.graph_output_pool:
-                out = gout
+            binding, seq = self._bound_decode(layer, x, gate, normalize, k, out, r_logits, r_weights, r_selected,
+                                              next_gate=graph_pred, stream=cur)
+            logits, ids, weights = r_logits, r_selected, r_weights
+            pred_ids = binding.pred if graph_pred is not None else None
+            # the next call's outputs, allocated while this launch runs
+            self._out_stash = (cur.cuda_stream, k, self._new_decode_outputs(k))
         else:
             logits, ids, weights = L.route(x, gate, ws, normalize=normalize, bias=bias)
         nws = None
@@ -280,17 +390,20 @@ class PDScopeCudaRuntime:
             nws = self._pred_workspace(T, k)
             _, pred_sel, _ = L.route(x, next_gate, nws, normalize=normalize)
             ops.route_hist(pred_sel, E, out=nws.hist)
-        _, _, _, packed = ws.views(T)
-        if T > 1:
-            ops.pack(ids, E, out=packed, workspace=ws.pack_ws)
-            counts_dev = packed.counts
+        if graph_path:
+            packed, n0 = None, k   # the bound launch needs no grouping
         else:
-            counts_dev = ids.reshape(-1)
-        host = self._pinned_counts
-        n0 = counts_dev.numel()
+            _, _, _, packed = ws.views(T)
+            if T > 1:
+                ops.pack(ids, E, out=packed, workspace=ws.pack_ws)
+                counts_dev = packed.counts
+            else:
+                counts_dev = ids.reshape(-1)
+            n0 = counts_dev.numel()
+        host, hn = self._pinned_counts, self._pinned_np
         err_at = self._err_at
         if graph_path:
-            # the replayed graph itself copied the routed ids, its prediction
+            # the bound launch's read-back wrote the routed ids, its prediction
             # and the fused kernel's sticky error word into `host`
             if pred_ids is None and predict:
                 host[n0:n0 + E].copy_(nws.hist, non_blocking=True)
@@ -298,23 +411,34 @@ class PDScopeCudaRuntime:
             host[:n0].copy_(counts_dev, non_blocking=True)
             if predict:
                 host[n0:n0 + E].copy_(nws.hist, non_blocking=True)
-        self._copy_done.record(cur)
-        self._copy_done.synchronize()
-        if graph_path:
-            self._raise_if_decode_gave_up(int(host[err_at]))
-        if T > 1:
-            counts = {e: int(c) for e, c in enumerate(host[:E].tolist()) if c}
+        # the bound launch's read-back numbers its words: with nothing else to
+        # read back, the host waits for that number instead of an event
+        completed = self._copy_done
+        if graph_path and not (predict and pred_ids is None):
+            self._await_readback(seq, cur)
+            completed = self._readback
         else:
-            sel = host[:k].tolist()
+            self._copy_done.record(cur)
+            self._copy_done.synchronize()
+        if graph_path:
+            self._raise_if_decode_gave_up(int(hn[err_at]))
+        if T > 1:
+            counts = {e: c for e, c in enumerate(hn[:E].tolist()) if c}
+        else:
+            sel = hn[:k].tolist()
             if len(set(sel)) != k:
                 raise AssertionError("decode routing selected duplicate experts")
+            if min(sel) < 0 or max(sel) >= E:
+                raise AssertionError("decode routing selected an expert id outside [0, E)")
             counts = {e: 1 for e in sel}
         if pred_ids is not None:   # one token: each predicted expert once
-            next_counts = {int(e): 1 for e in host[n0:n0 + k].tolist()}
+            next_counts = {e: 1 for e in hn[n0:n0 + k].tolist()}
             if len(next_counts) != k:
                 raise AssertionError("decode prediction selected duplicate experts")
+            if min(next_counts) < 0 or max(next_counts) >= E:
+                raise AssertionError("decode prediction selected an expert id outside [0, E)")
         else:
-            next_counts = ({e: int(c) for e, c in enumerate(host[n0:n0 + E].tolist()) if c} if predict else {})
+            next_counts = ({e: c for e, c in enumerate(hn[n0:n0 + E].tolist()) if c} if predict else {})
         if sum(counts.values()) != T * k:
             raise AssertionError("lost or duplicated routed assignment")
 
@@ -331,9 +455,16 @@ class PDScopeCudaRuntime:
         # and picks the prefetch (pdscope_runtime.py:268-279); else every
         # expert runs on the GPU, resident first, misses through staging
         # (state, ticket) of each routed expert's copy, or None (no views built)
-        views = {e: self.cache.residency(key(e)) for e in counts}
         has_next = predict and (layer + 1) in self.layers
-        if planned:
+        views = None
+        if not planned and T == 1 and all(o[4] == "ready" for o in observations):
+            # every routed copy was ready at the reveal (the observations come
+            # in expert order): all resident, none loading, no demand
+            decision = None
+            cpu_list, demand = [], []
+            resident = [o[0].expert for o in observations]
+        elif planned:
+            views = {e: self.cache.residency(key(e)) for e in counts}
             hit_rate = observed["hits"] / observed["total"] if observed["total"] else 0.0
             next_resident = [e for e in next_counts if self.cache.residency(nkey(e)) is not None] if has_next else []
             decision = plan_pdscope(counts, next_counts if has_next else {}, current_layer=layer, phase=phase,
@@ -348,13 +479,16 @@ class PDScopeCudaRuntime:
             resident = list(decision["gpu_resident_queue"])
             demand = list(decision["on_demand_queue"])
             if graph_ok and not cpu_list:
-                graph_path = True  # replayed below over the (completed) slot table
+                graph_path = True  # launched below over the (completed) slot table
+                if ring_out is not None:
+                    out = ring_out
         else:
+            views = {e: self.cache.residency(key(e)) for e in counts}
             decision = None
             cpu_list = []
             resident = sorted((e for e in counts if views[e] is not None), key=lambda e: (-counts[e], e))
             demand = sorted((e for e in counts if views[e] is None), key=lambda e: (-counts[e], e))
-        for e in resident:
+        for e in (resident if views is not None else ()):
             if views[e][0] == "loading":
                 self.executor.finish_load(views[e][1], wait=True)
                 self.pending.pop(key(e), None)
@@ -422,21 +556,21 @@ class PDScopeCudaRuntime:
                 for e, r in jobs.items():
                     cpu_tasks[e] = ex.submit_cpu(key(e), r)
         if graph_path:
-            if not demand:  # with misses the demand batch below replays over the completed table
+            if not demand:  # with misses the demand batch below launches over the completed table
                 if replay_table is None or any(replay_table[e] == 0 for e in counts):
-                    # not replayed yet (planned path), or a routed copy landed
-                    # after the first replay: replay over the completed table
+                    # not launched yet (planned path), or a routed copy landed
+                    # after the first launch: launch over the completed table
                     late_replays += 1
 
                     def launch():
-                        self._replay_decode_graph(layer, x, gate, normalize, k, out, ring=ring,
-                                                  next_gate=graph_pred)
+                        self._bound_decode(layer, x, gate, normalize, k, out, r_logits, r_weights, r_selected,
+                                           next_gate=graph_pred)
                 else:
-                    # the replay on `cur` already produced `out` (the host waited
+                    # the launch on `cur` already produced `out` (the host waited
                     # for it through _copy_done): account the uses it made
                     launch = None
                 tasks.append(ex.gpu_group([key(e) for e in resident], launch, input_ref=x, wait_for=cur,
-                                          completed=self._copy_done))
+                                          completed=completed))
         elif resident:
             ex.table(layer, E)
             require_copies(resident if not decode_fast else sorted(counts))
@@ -464,8 +598,8 @@ class PDScopeCudaRuntime:
                     late_replays += 1
 
                     def launch():
-                        self._replay_decode_graph(layer, x, gate, normalize, k, out, ring=ring,
-                                                  next_gate=graph_pred)
+                        self._bound_decode(layer, x, gate, normalize, k, out, r_logits, r_weights, r_selected,
+                                           next_gate=graph_pred)
                     comp = ex.gpu_group([key(e) for e in resident + batch], launch, input_ref=x, wait_for=cur)
                 else:
                     tab = ex.upload_table(layer, E, ex.compute_stream)
@@ -512,8 +646,6 @@ class PDScopeCudaRuntime:
         # ---- finish GPU work, place the CPU experts' rows, merge in token order
         for task in tasks:
             ex.finish_gpu(task, wait=True)
-        if graph_path and self.graph_output_pool:
-            out = self._graphs[self._graph_key(layer, k, normalize, gate, ring, graph_pred)][2]
         cpu_rows = dict((e, ex.finish_cpu(p, wait=True)) for e, p in cpu_tasks.items())
         if cpu_group is not None:
             cpu_rows.update(ex.finish_cpu_group(cpu_group.values()))
@@ -554,16 +686,16 @@ class PDScopeCudaRuntime:
             if note is not None:
                 note(len(native_cpu))
         if not (graph_path and not late_replays):
-            # (a replay served before the reveal enqueued nothing on the compute stream)
+            # (a launch served before the reveal enqueued nothing on the compute stream)
             done = torch.cuda.Event()
             done.record(ex.compute_stream)
             cur.wait_event(done)
         if graph_path and late_replays:
-            # replays after the demand reveal: their error word, read once they completed
-            host[err_at:err_at + 1].copy_(self._decode_error_word(), non_blocking=True)
+            # launches after the demand reveal wrote their error word into
+            # `host` themselves: read it once they completed
             self._copy_done.record(cur)
             self._copy_done.synchronize()
-            self._raise_if_decode_gave_up(int(host[err_at]))
+            self._raise_if_decode_gave_up(int(hn[err_at]))
         self.cache.end_demand(identity)
         self._retire_current(layer, wait=True)
         self.poll()
@@ -572,10 +704,13 @@ class PDScopeCudaRuntime:
         if self.diagnostics and any(self.cache.lookup(h) is None for h in self._hot_by_layer.get(layer, ())):
             raise AssertionError("speculation evicted a charged static hot copy")
         after = self.cache.stats()
-        delta = {kk: v - before.get(kk, 0) for kk, v in after.items()}
+        delta = dict(zip(after, map(operator.sub, after.values(), map(before.get, after, itertools.repeat(0)))))
         if delta.get("cpu_completed_experts", 0) + delta.get("gpu_completed_experts", 0) != len(counts):
             raise AssertionError("lost or duplicated routed expert")
-        routing = Routing(logits.clone(), ids.long(), weights.clone())
+        # the bound launch wrote fresh tensors; the other paths' routing lives
+        # in reused workspaces
+        routing = (Routing(logits, ids, weights) if bound_routing
+                   else Routing(logits.clone(), ids.long(), weights.clone()))
         if decision is None:
             decision = dict(phase=phase, mode="gpu_all", cpu_queue=[], gpu_resident_queue=resident,
                             on_demand_queue=demand, prefetch_queue=issued, unload_queue=[],
@@ -606,17 +741,17 @@ class PDScopeCudaRuntime:
                    graph_output_pool=self.graph_output_pool,
                    pipeline="CPU queue on the backend beside the GPU launches; demand copies in staging-slot "
                             "batches before next-layer speculation",
-                   decode_path=("graph" if graph_path else "fused_gemv" if decode_fast else "grouped")
+                   decode_path=("bound_launch" if graph_path else "fused_gemv" if decode_fast else "grouped")
                    if phase == "decode" else "grouped",
                    measured_performance=False)
         return out, routing, row
 
     def _calibrate_graph_costs(self, hot_keys, reps=48, warm=16):
-        """Replay cost of the resident decode graph for the planner
+        """Cost of the bound resident decode launch for the planner
         (pdscope_runtime.py:143-175 calibrates its per-expert graphs the same
-        way): a layer graph over the first hot layer, routed by a calibration
-        gate onto k of its resident experts, is replayed `reps` times; the
-        median over the last reps-warm, divided by k, is one expert's graph
+        way): the bound launch of the first hot layer, routed by a calibration
+        gate onto k of its resident experts, runs `reps` times; the median
+        over the last reps-warm, divided by k, is one expert's resident-launch
         cost.  'measured' charges it to one-row GPU work in the cost table,
         'eager_bound' keeps the table's eager cost (the cost model of the
         reference's ResidentGraphCosts)."""
@@ -631,14 +766,18 @@ class PDScopeCudaRuntime:
         for j, e in enumerate(resident[:kk]):
             gate[e] = (x[0].float() * (0.01 * (kk - j))).to(torch.bfloat16)
         out = torch.empty_like(x)
+        logits = torch.empty((1, self.E), dtype=torch.bfloat16, device=self.device)
+        weights = torch.empty((1, kk), dtype=torch.bfloat16, device=self.device)
+        selected = torch.empty((1, kk), dtype=torch.int64, device=self.device)
         samples = []
         for i in range(reps):
             t0 = time.perf_counter()
-            self._replay_decode_graph(layer, x, gate, True, kk, out, cache=False)
+            self._bound_decode(layer, x, gate, True, kk, out, logits, weights, selected,
+                               key=("calibration", layer, kk))
             torch.cuda.synchronize(self.device)
             if i >= warm:
                 samples.append((time.perf_counter() - t0) * 1e3)
-        self._graphs.pop(("calibration", layer, kk), None)
+        self._bindings.pop(("calibration", layer, kk)).close()
         gpu_ms = statistics.median(samples) / kk
         base = self.costs.for_load(1)
         self.graph_cost_calibration = dict(samples_ms=samples, median_ms=statistics.median(samples),
@@ -646,7 +785,7 @@ class PDScopeCudaRuntime:
                                            scheduler_cost_mode=self.graph_cost_mode,
                                            scheduler_gpu_ms=base["gpu_ms"] if self.graph_cost_mode == "eager_bound"
                                            else gpu_ms,
-                                           scope="host wall time of one decode-layer graph replay over resident "
+                                           scope="host wall time of one bound decode-layer launch over resident "
                                                  "experts, per routed expert")
         self.costs = ResidentGraphCosts(self.costs, gpu_ms, self.graph_cost_mode)
 
@@ -708,73 +847,48 @@ class PDScopeCudaRuntime:
         L.grouped_ffn(x, packed, sel_dev, bm, sum((r + bm - 1) // bm for r in rows), slots_dev, ws,
                       max_tiles_down=sum((r + bmd - 1) // bmd for r in rows), perm=perm)
 
-    # ------------------------------------------------------------ resident decode graph
+    # ------------------------------------------------------------ bound resident decode
 
-    @staticmethod
-    def _graph_key(layer, k, normalize, gate, ring, next_gate):
-        return (layer, k, normalize, gate.data_ptr(), ring, next_gate.data_ptr() if next_gate is not None else 0)
+    def _ring_output(self, layer, turn):
+        """graph_output_pool: output buffer `turn` (0 or 1) of `layer`'s
+        two-deep ring (the reference's per-key output ring, executor.py:129-133)."""
+        ring = self._out_ring.get(layer)
+        if ring is None:
+            ring = self._out_ring[layer] = tuple(torch.empty((1, self.H), dtype=torch.bfloat16, device=self.device)
+                                                 for _ in range(2))
+        return ring[turn]
 
-    def _replay_decode_graph(self, layer, x, gate, normalize, k, out, *, ring=0, cache=True, next_gate=None,
-                             stream=None):
-        """Replay the captured single-launch decode layer of `layer` over its
-        current slot table (capturing it on first use, checked bit for bit
-        against the eager launch).  With graph_output_pool the graph of ring
-        entry `ring` (two per layer) writes its own output buffer, which is
-        returned as is; otherwise the output is copied into `out`.  With
-        next_gate the same launch predicts the next layer's experts.
-        Returns (logits, ids, weights, output, predicted ids or None) views of
-        the graph's buffers."""
-        gkey = self._graph_key(layer, k, normalize, gate, ring, next_gate) if cache else ("calibration", layer, k)
-        g = self._graphs.get(gkey)
-        ex = self.executor
-        ex.table(layer, self.E)
-        # the table tensor is captured by address; refresh its contents (copies
-        # may have moved between calls) on the replay stream
+    def _bound_decode(self, layer, x, gate, normalize, k, out, logits, weights, selected, *, next_gate=None,
+                      stream=None, key=None):
+        """One token of `layer` through its bound single-launch decode over the
+        layer's current slot table (bound on first use): route + SwiGLU +
+        merge write out [1,H], logits [1,E], weights [1,k] and selected [1,k]
+        int64; with next_gate the same launch predicts the next layer.  The
+        routed ids, the prediction and the fused kernel's sticky error word
+        land in the pinned read-back buffer (ids at 0, prediction at k, error
+        word at _err_at, then the launch's sequence number at _seq_at).
+        Returns (the binding, the sequence number)."""
+        if key is None:
+            key = (layer, k, normalize, gate.data_ptr(), 0 if next_gate is None else next_gate.data_ptr())
         cur = torch.cuda.current_stream(self.device) if stream is None else stream
-        slots_dev = ex.upload_table(layer, self.E, cur)
-        if g is None:
-            gws = L.MoEWorkspace(1, self.H, self.I, self.E, k, self.device)
-            pred = torch.full((k,), -1, dtype=torch.int32, device=self.device) if next_gate is not None else None
-            xin = torch.empty_like(x)
-            gout = gws.out[:1]
-            xin.copy_(x)
-            torch.cuda.synchronize(self.device)
-            side = torch.cuda.Stream(self.device)
-            side.wait_stream(cur)
-            # whole layer (fused single-launch decode where the device allows)
-            fwd = dict(normalize=normalize, merge=self.merge, next_gate=next_gate, pred_out=pred)
-            with torch.cuda.stream(side):
-                L.moe_forward(xin, gate, slots_dev, gws, **fwd)
-            cur.wait_stream(side)
-            watched = lambda: [t for t in (gout, gws.logits[:1], gws.ids[:1], gws.weights[:1], pred)  # noqa: E731
-                               if t is not None]
-            eager = [t.clone() for t in watched()]
-            graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph):
-                L.moe_forward(xin, gate, slots_dev, gws, **fwd)
-                # what forward reads back rides in the graph: the routed ids,
-                # the prediction and the sticky error word land in the pinned
-                # host buffer with every replay (no copy launches per call)
-                host = self._pinned_counts
-                host[:k].copy_(gws.ids[:1].reshape(-1), non_blocking=True)
-                if pred is not None:
-                    host[k:2 * k].copy_(pred, non_blocking=True)
-                host[self._err_at:self._err_at + 1].copy_(self._decode_error_word(), non_blocking=True)
-            # a captured graph must reproduce the eager launch bit for bit
-            # before it serves (the reference checks the same at capture,
-            # expertbench/executor.py:95-96)
-            graph.replay()
-            if not all(torch.equal(a, b) for a, b in zip(eager, watched())):
-                raise AssertionError(f"captured decode graph of layer {layer} differs from its eager launch")
-            g = (graph, xin, gout, gws, slots_dev, pred)
-            self._graphs[gkey] = g
-        graph, xin, gout, gws, _, pred = g
-        xin.copy_(x)
-        graph.replay()
-        if not self.graph_output_pool:
-            out.copy_(gout)
-        return gws.logits[:1], gws.ids[:1], gws.weights[:1], gout, pred
+        # the table is bound by address; refresh its contents (copies may have
+        # moved between calls) on the launch stream
+        slots_dev = self.executor.upload_table(layer, self.E, cur)
+        b = self._bindings.get(key)
+        if b is None:
+            b = ops.DecodeBinding(gate, slots_dev, self.I, k, normalize, host=self._pinned_counts,
+                                  error_at=self._err_at, seq_at=self._seq_at, merge=self.merge,
+                                  next_gate=next_gate)
+            self._bindings[key] = b
+        self._seq = self._seq % 0x7FFFFFFF + 1
+        b.run_ptrs(x.data_ptr(), out.data_ptr(), logits.data_ptr(), weights.data_ptr(), selected.data_ptr(),
+                   self._seq, cur.cuda_stream)
+        self.bound_launches += 1
+        return b, self._seq
 
     def close(self):
-        self._graphs.clear()
+        self._out_stash = None
+        for b in self._bindings.values():
+            b.close()
+        self._bindings.clear()
         self.executor.shutdown()

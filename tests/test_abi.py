@@ -47,3 +47,17 @@ def test_invalid_arguments_raise_before_any_launch():
         _lib.call("pdscope_schedule", None, 128, None, 0, 48, None, None)
     msg = _lib.load().pdscope_last_error().decode()
     assert "schedule" in msg
+    # the bound decode layer checks its out-pointer, read-back words and
+    # binding before touching the device
+    import ctypes
+    handle = ctypes.c_void_p()
+    with pytest.raises(ValueError, match="null binding out-pointer"):
+        _lib.call("pdscope_decode_bind", None, None, 2048, 128, 8, 1, 1, None, 768, None, None, None, None, None,
+                  None, None, None, None, None)
+    with pytest.raises(ValueError, match="null read-back pointer"):
+        _lib.call("pdscope_decode_bind", None, None, 2048, 128, 8, 1, 1, None, 768, None, None, None, None, None,
+                  None, None, None, None, ctypes.byref(handle))
+    assert handle.value is None
+    with pytest.raises(ValueError, match="null binding"):
+        _lib.call("pdscope_decode_run", None, None, None, None, None, None, 1, None)
+    _lib.load().pdscope_decode_unbind(None)   # freeing no binding is a no-op

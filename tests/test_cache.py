@@ -319,6 +319,69 @@ def test_expert_key_record_contract():
         ExpertKey(1, -1, "bf16")
 
 
+def test_key_records_hash_in_the_native_base():
+    """With the package built, ExpertKey and LoadTicket take hash() and ==
+    from the C base type pdscope_amd._records.HashedRecord."""
+    from pdscope_amd import cache
+    from pdscope_amd._records import HashedRecord
+    assert cache._RecordBase is HashedRecord
+    for cls in (cache.ExpertKey, cache.LoadTicket):
+        assert issubclass(cls, HashedRecord) and cls.__hash__ is HashedRecord.__hash__
+
+
+def test_key_records_keep_their_contract_without_the_native_base():
+    """cache.py loaded where pdscope_amd._records cannot be imported falls
+    back to a Python base with the same semantics: the record contracts
+    hold and a short ledger lifecycle runs."""
+    import dataclasses
+    import importlib.util
+    import pickle
+    import sys
+    from pathlib import Path
+
+    import pdscope_amd.cache as native
+    name = "pdscope_amd._cache_without_records"
+    saved = sys.modules.get("pdscope_amd._records")
+    sys.modules["pdscope_amd._records"] = None   # the import raises ImportError
+    try:
+        spec = importlib.util.spec_from_file_location(name, Path(native.__file__))
+        mod = importlib.util.module_from_spec(spec)
+        sys.modules[name] = mod
+        spec.loader.exec_module(mod)
+    finally:
+        if saved is None:
+            del sys.modules["pdscope_amd._records"]
+        else:
+            sys.modules["pdscope_amd._records"] = saved
+    try:
+        assert mod._RecordBase.__module__ == name
+        K = mod.ExpertKey
+        a, b, c = K(1, 2, "bf16"), K(1, 2, "bf16"), K(1, 10, "bf16")
+        assert a == b and not (a != b) and hash(a) == hash(b) and len({a, b, c}) == 2
+        assert a != c and a < c and a != (1, 2, "bf16") and not (a == (1, 2, "bf16"))
+        assert dataclasses.replace(a, expert=10) == c
+        r = pickle.loads(pickle.dumps(a))
+        assert r == a and hash(r) == hash(a)
+        t1 = mod.LoadTicket("o", 3, a, "cache", None)
+        t2 = mod.LoadTicket("o", 3, b, "cache", None)
+        assert t1 == t2 and hash(t1) == hash(t2) and dataclasses.replace(t1, slot=0) != t1
+        # a short lifecycle on the fallback records
+        keys = [K(0, e, "bf16") for e in range(4)]
+        ledger = mod.ExpertCache({k: 10 for k in keys}, 40, [10], initial_hotset=keys[:2])
+        for k in keys[:2]:
+            t = ledger.begin_load(k, origin="initial")
+            ledger.submit(t)
+            ledger.complete_load(t)
+        ident = mod.DemandID("r", 1, 0)
+        obs = ledger.on_demand(ident, {keys[0]: 2, keys[1]: 1})
+        assert [o.state_at_reveal for o in obs] == ["ready", "ready"]
+        ledger.release_many(ledger.acquire_many(keys[:2]))
+        ledger.end_demand(ident)
+        assert ledger.stats()["gpu_completed_experts"] == 2
+    finally:
+        del sys.modules[name]
+
+
 def test_load_ticket_record_contract():
     """LoadTicket equality and hash follow its fields, also across a pickle
     round trip and for distinct but equal key objects."""

@@ -171,5 +171,5 @@ def test_config4_chained_stack_through_runtime(orc):
     prefill_rows, decode_rows = rows_all[:n_layers], rows_all[n_layers:]
     assert sum(len(r["decision"]["on_demand_queue"]) for r in prefill_rows) > 0, "the slot cap forced no misses"
     assert sum(len(r["prefetch_issued"]) for r in rows_all) > 0, "the predictor prefetched nothing"
-    assert all(r["decode_path"] == "graph" for r in decode_rows)
+    assert all(r["decode_path"] == "bound_launch" for r in decode_rows)
     assert st.get("prefetch_loads_submitted", 0) > 0

@@ -327,8 +327,8 @@ def test_runtime_input_pregather_gives_the_same_bits(orc):
 
 
 def test_runtime_graph_output_pool_is_a_two_deep_ring(orc):
-    """graph_output_pool: decode layers return a view of one of two graph
-    output buffers per layer, alternating, with no copy per call; each output
+    """graph_output_pool: decode layers return one of two output buffers per
+    layer, alternating, which the bound launch writes directly; each output
     equals the eager single-launch layer until the call after next."""
     from pdscope_amd import layer, ops, synthetic
     from pdscope_amd.cache import ExpertKey
@@ -347,7 +347,7 @@ def test_runtime_graph_output_pool_is_a_two_deep_ring(orc):
             out, routing, row = rt.forward(x, layers[0].gate, layer=0, step=step)
             ref, _, _, _ = layer.moe_forward(x, layers[0].gate, slots, ws, merge=rt.merge)
             torch.cuda.synchronize()
-            assert row["decode_path"] == "graph" and row["graph_output_pool"] is True
+            assert row["decode_path"] == "bound_launch" and row["graph_output_pool"] is True
             assert torch.equal(out, ref)
             ptrs.append(out.data_ptr())
         assert ptrs[0] == ptrs[2] and ptrs[1] == ptrs[3] and ptrs[0] != ptrs[1]
@@ -356,11 +356,11 @@ def test_runtime_graph_output_pool_is_a_two_deep_ring(orc):
         rt.close()
 
 
-def test_runtime_planned_decode_replays_graphs_with_calibrated_costs(orc, tmp_path):
+def test_runtime_planned_decode_takes_the_bound_launch_with_calibrated_costs(orc, tmp_path):
     """With a cost table, a CPU backend and resident_graphs, construction
-    calibrates the graph replay (graph_cost_mode='measured' charges it to
-    one-token GPU work); a decode plan that keeps every expert on the GPU is
-    served by the layer graph."""
+    calibrates the bound resident launch (graph_cost_mode='measured' charges
+    it to one-token GPU work); a decode plan that keeps every expert on the
+    GPU is served by the layer's bound launch."""
     from pdscope_amd.cache import ExpertKey
     from pdscope_amd.costs import ResidentGraphCosts
     from pdscope_amd.pdscope_runtime import PDScopeCudaRuntime
@@ -381,7 +381,7 @@ def test_runtime_planned_decode_replays_graphs_with_calibrated_costs(orc, tmp_pa
             x = torch.randn((1, H), generator=gen, device=DEV).to(torch.bfloat16)
             out, routing, row = rt.forward(x, layers[0].gate, layer=0, step=step, top_k=k)
             torch.cuda.synchronize()
-            assert row["decision"]["cpu_queue"] == [] and row["decode_path"] == "graph"
+            assert row["decision"]["cpu_queue"] == [] and row["decode_path"] == "bound_launch"
             check_output(orc, out, routing, x, layers[0], H, I, k)
         closure(rt)
     finally:
@@ -447,7 +447,7 @@ def test_measured_requests_write_the_reference_run_files(tmp_path):
         with gzip.open(run / r["trace"]["path"], "rt") as f:
             rows = json.load(f)
         assert len(rows) == 4 * 2 and [x["step"] for x in rows] == [0, 0, 1, 1, 2, 2, 3, 3]
-        assert all(x["decode_path"] == "graph" for x in rows if x["phase"] == "decode")
+        assert all(x["decode_path"] == "bound_launch" for x in rows if x["phase"] == "decode")
         assert r["cache_stats"]["physical_demand_tokens"] == (24 + 3) * 2 * 4
     assert result["requests"][-1]["generated_ids"] == reqs[-1]["generated_ids"]
     # the three requests share the prompt and the model: the same greedy tokens

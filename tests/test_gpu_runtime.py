@@ -294,7 +294,11 @@ def test_slot_table_fill_is_ordered_before_uploads_on_other_streams():
         rt.close()
 
 
-def test_runtime_decode_graph_matches_eager(orc):
+def test_runtime_bound_decode_matches_the_single_launch_layer(orc):
+    """resident_graphs=True serves decode tokens through the layer's bound
+    launch: output and routing equal the single-launch layer bit for bit, and
+    each call returns routing tensors of its own (later calls leave them as
+    they were)."""
     from pdscope_amd import layer, ops, synthetic
     from pdscope_amd.cache import ExpertKey
     from pdscope_amd.pdscope_runtime import PDScopeCudaRuntime
@@ -304,18 +308,27 @@ def test_runtime_decode_graph_matches_eager(orc):
     rt = PDScopeCudaRuntime(masters, hot_keys=hot, speculative_slots=0, resident_graphs=True)
     slots = ops.slot_table([layers[0].experts[e] for e in range(q["E"])], DEV)
     ws = layer.MoEWorkspace(1, q["H"], q["I"], q["E"], 8, DEV)
+    kept = []
     try:
-        # step 0 is a prefill (T >= 2); decode steps replay the captured graph
+        # step 0 is a prefill (T >= 2); decode steps take the bound launch
         x0 = synthetic.make_tokens(4, q["H"], seed=94)
         rt.forward(x0, layers[0].gate, layer=0, step=0)
         for step in range(1, 5):
             x = synthetic.make_tokens(1, q["H"], seed=94 + step)
             out, routing, row = rt.forward(x, layers[0].gate, layer=0, step=step)
-            assert row["decode_path"] == "graph"
-            ref_out, _, ids, w = layer.moe_forward(x, layers[0].gate, slots, ws, merge=rt.merge)
+            assert row["decode_path"] == "bound_launch"
+            ref_out, logits, ids, w = layer.moe_forward(x, layers[0].gate, slots, ws, merge=rt.merge)
             torch.cuda.synchronize()
             assert torch.equal(out, ref_out) and torch.equal(routing.selected, ids.long())
+            assert torch.equal(routing.logits, logits) and torch.equal(routing.weights, w)
+            assert routing.selected.dtype == torch.int64 and routing.selected.shape == (1, 8)
             check_output(orc, out, routing, x, layers[0], q["H"], q["I"], 8)
+            kept.append((out, routing, ref_out.clone(), logits.clone(), ids.long(), w.clone()))
+        torch.cuda.synchronize()
+        for out, routing, ref_out, logits, ids, w in kept:
+            assert torch.equal(out, ref_out) and torch.equal(routing.selected, ids)
+            assert torch.equal(routing.logits, logits) and torch.equal(routing.weights, w)
+        assert rt.bound_launches == 4 and len(rt._bindings) == 1
         closure(rt)
     finally:
         rt.close()
@@ -337,7 +350,7 @@ def test_runtime_raises_when_the_fused_decode_error_word_is_set():
         rt.forward(synthetic.make_tokens(4, q["H"], seed=98), layers[0].gate, layer=0, step=0)
         x = synthetic.make_tokens(1, q["H"], seed=99)
         out, _, row = rt.forward(x, layers[0].gate, layer=0, step=1)
-        assert row["decode_path"] == "graph"
+        assert row["decode_path"] == "bound_launch"
         word = ops.decode_workspace(DEV, q["H"])
         word[ops.DECODE_WS_ERROR_WORD] = 1
         with pytest.raises(RuntimeError, match="bounded internal wait gave up"):
@@ -356,12 +369,12 @@ def test_runtime_raises_when_the_fused_decode_error_word_is_set():
         rt.close()
 
 
-def test_runtime_partial_resident_decode_graph(orc):
-    """Decode graph over a partly resident layer: experts without a copy read as
-    null on the first replay; misses are staged in one batch and the graph is
-    replayed over the completed table.  The output equals the single-launch
-    layer over a fully resident table bit for bit; the predictor prefetches
-    the next layer's experts on the way."""
+def test_runtime_partial_resident_bound_decode(orc):
+    """Bound decode launch over a partly resident layer: experts without a copy
+    read as null on the first launch; misses are staged in one batch and the
+    layer is launched again over the completed table.  The output equals the
+    single-launch layer over a fully resident table bit for bit; the
+    predictor prefetches the next layer's experts on the way."""
     from pdscope_amd import layer, ops, synthetic
     from pdscope_amd.cache import ExpertKey
     from pdscope_amd.pdscope_runtime import PDScopeCudaRuntime
@@ -381,7 +394,7 @@ def test_runtime_partial_resident_decode_graph(orc):
             for l in range(2):
                 out, routing, row = rt.forward(x, layers[l].gate, layer=l, step=step,
                                                next_gate=layers[1].gate if l == 0 else None)
-                assert row["decode_path"] == "graph"
+                assert row["decode_path"] == "bound_launch"
                 misses += len(row["decision"]["on_demand_queue"])
                 ref_out, _, ids, _ = layer.moe_forward(x, layers[l].gate, full[l], ws, merge=rt.merge)
                 torch.cuda.synchronize()
@@ -389,7 +402,7 @@ def test_runtime_partial_resident_decode_graph(orc):
                 assert torch.equal(out, ref_out)
                 check_output(orc, out, routing, x, layers[l], q["H"], q["I"], 8)
                 if l == 0:
-                    # the prediction the graph's launch made equals the router on the next gate
+                    # the prediction the bound launch made equals the router on the next gate
                     nids = torch.empty((1, 8), dtype=torch.int32, device=DEV)
                     ops.route_topk(x, layers[1].gate, 8, True,
                                    out=(torch.empty((1, q["E"]), dtype=torch.bfloat16, device=DEV), nids,
@@ -417,6 +430,10 @@ def test_runtime_rejects_bad_phase_shapes():
             rt.forward(x2, layers[0].gate, layer=0, step=1)
         with pytest.raises(ValueError):
             rt.forward(x2, layers[0].gate, layer=5, step=0)
+        with pytest.raises(ValueError):   # hidden size of another model
+            rt.forward(torch.zeros((2, 128), dtype=torch.bfloat16, device=DEV), layers[0].gate, layer=0, step=0)
+        with pytest.raises(ValueError):   # gate of another shape
+            rt.forward(x2, layers[0].gate[:16], layer=0, step=0)
     finally:
         rt.close()
     with pytest.raises(ValueError):

@@ -6,7 +6,7 @@ stack workload builds them: 58 GB of pinned expert masters, a 24 GiB device
 budget (allocator capped below it by the memory already in use outside the
 allocator plus a margin, expert slots sized within the cap), 8 demand
 staging slots, gate-fallback prefetch of the next layer and decode layers
-replayed through their captured single-launch graphs.  Prefill 2048 tokens,
+served by their bound single-launch decode.  Prefill 2048 tokens,
 then 64 decode steps.
 
 At every layer of the prefill and of six seeded decode steps:
@@ -89,7 +89,7 @@ def test_config4_stack48_full_size_against_the_oracle(orc):
     assert mem["gpu_peak_reserved_plus_end_external_bytes"] <= 24 << 30
     assert res["prefill"]["demand_misses"] > 0, "the budget forced no demand misses"
     assert res["prefill"]["prefetch_issued"] > 0 and res["decode"]["prefetch_issued"] > 0
-    assert res["decode"]["paths"] == ["graph"]
+    assert res["decode"]["paths"] == ["bound_launch"]
     del session, model
     gc.collect()
     torch._C._host_emptyCache()
