@@ -309,28 +309,30 @@ int pdscope_decode_layer_chained(const void *x, const void *resid, void *x_out, 
  * (resid / x_out are not bound: NULL) and keeps them in a host record
  * (*binding, freed by pdscope_decode_unbind); the pointed-to buffers must
  * outlive it.  ids [k] int32 is device scratch of the binding; host_ids
- * (2k words), host_error and host_seq (1 word each) must be pinned host
- * memory (hipHostMalloc), else the call fails.
+ * (2k words) and host_error (1 word) must be pinned host memory
+ * (hipHostMalloc), else the call fails.
  *
- * pdscope_decode_run enqueues on `stream`, on the binding's device: the
- * fused decode kernel (inputs x, outputs out / logits / weights as in
- * pdscope_decode_layer), then one read-back kernel that writes host_ids[0,k)
- * = the routed ids, host_ids[k,2k) = the next-layer prediction (when bound
- * with next_gate), *host_error = the sticky error word of the workspace,
- * when selected != NULL selected[0,k) = the routed ids as int64 (device),
- * and last, after a system-scope release, *host_seq = seq.  A host that
- * reads seq there may read the other words, and the decode launch has
- * completed (so has anything the stream ordered before it); an event
- * recorded later on `stream` gives the same guarantee.  Two launches per
- * token, no graph: replaying a captured graph of the same kernel costs the
- * host several times more.  Calls that share a binding or its workspace must
- * be ordered on one stream.
+ * pdscope_decode_run enqueues on `stream`, on the binding's device, a token
+ * numbered seq (1 .. 32767, else EINVAL): the fused decode kernel (inputs x,
+ * outputs out / logits / weights as in pdscope_decode_layer), which stores
+ * host_ids[0,k) = (seq << 16) | routed id as soon as its routing is final,
+ * before the kernel completes (and, when selected != NULL, selected[0,k) =
+ * the routed ids as int64 on the device), and host_ids[k,2k) = (seq << 16) |
+ * predicted id (when bound with next_gate); then a one-wave kernel that
+ * stores *host_error = (seq << 16) | the workspace's sticky error word.
+ * Each word is valid once it carries seq in its upper half (no fence orders
+ * them).  *host_error is stored after the decode kernel completed, so a host
+ * that reads seq there knows the launch (and anything the stream ordered
+ * before it) has completed, and finds the other words tagged too.  Two
+ * launches per token, no graph: replaying a captured graph of the same
+ * kernel costs the host several times more.  Calls that share a binding or
+ * its workspace must be ordered on one stream.
  */
 typedef struct pdscope_decode_binding pdscope_decode_binding;
 int pdscope_decode_bind(const void *gate, const float *bias, int H, int E, int k, int normalize, int merge_mode,
                         const void *const *slots, int I, const void *next_gate, int32_t *pred_out, int32_t *ids,
                         float *probs, void *h_ws, void *workspace, int32_t *host_ids, int32_t *host_error,
-                        int32_t *host_seq, pdscope_decode_binding **binding);
+                        pdscope_decode_binding **binding);
 int pdscope_decode_run(const pdscope_decode_binding *binding, const void *x, void *out, void *logits,
                        void *weights, int64_t *selected, int32_t seq, void *stream);
 void pdscope_decode_unbind(pdscope_decode_binding *binding);

@@ -48,7 +48,7 @@ SIGNATURES = {
     "pdscope_decode_layer_chained": ([_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _i32, _vp, _vp,
                                       _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp], _i32),
     "pdscope_decode_bind": ([_vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
-                             _vp, _vp, ctypes.POINTER(_vp)], _i32),
+                             _vp, ctypes.POINTER(_vp)], _i32),
     "pdscope_decode_run": ([_vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp], _i32),
     "pdscope_decode_unbind": ([_vp], None),
     "pdscope_stage_expert": ([_vp, _vp, _sz, _vp, _vp], _i32),

@@ -277,6 +277,21 @@ class _Ranking:
         self._key_of[t] = key
         rank_of[key] = rank
 
+    def put_new(self, keys, rank):
+        """put(key, rank) of each key, none of them in this ranking yet, in
+        one pass over the rank's bucket."""
+        bucket = self._buckets.get(rank)
+        if bucket is None:
+            bucket = self._buckets[rank] = []
+            bisect.insort(self._ranks, rank)
+        key_of, rank_of = self._key_of, self._rank_of
+        for key in keys:
+            t = key._t
+            key_of[t] = key
+            rank_of[key] = rank
+            bucket.append(t)
+        bucket.sort()
+
     def discard(self, key):
         rank = self._rank_of.pop(key, None)
         if rank is None:
@@ -487,6 +502,33 @@ class ExpertCache:
             tick = self._last_tick.get(key, 0)
             target.put(key, (self._times_demanded[key], tick) if self.policy == "LFU" else (tick,))
             ranked[key] = target
+
+    def _reindex_many(self, keys):
+        """_reindex of each key (distinct keys, none in a ranking yet unless
+        noted there): the keys that join a ranking at one rank go into its
+        bucket in one pass instead of one insertion each."""
+        ranked, copies, r, hint = self._ranked, self._copies, self._reveal, self._hint
+        replacing, lfu = self.policy != "static", self.policy == "LFU"
+        groups = {}
+        for key in keys:
+            if key in ranked:
+                self._reindex(key)
+                continue
+            c = copies.get(key)
+            if (c is None or not replacing or c.ticket.pool != "cache" or c.phase != READY or c.holders
+                    or (r is not None and key in r.open_keys)):
+                continue
+            target = (self._protected_rank if key in self._protected or (hint is not None and key in hint.keys)
+                      else self._unprotected)
+            tick = self._last_tick.get(key, 0)
+            rank = (self._times_demanded[key], tick) if lfu else (tick,)
+            group = groups.get((id(target), rank))
+            if group is None:
+                group = groups[(id(target), rank)] = (target, rank, [])
+            group[2].append(key)
+            ranked[key] = target
+        for target, rank, members in groups.values():
+            target.put_new(members, rank)
 
     def _choose_victims(self, size):
         """Cheapest evictable copies freeing room for `size` more bytes, or
@@ -858,27 +900,32 @@ class ExpertCache:
         """release() of each handle in order, in one call (same checks and
         transitions; a failing handle leaves the earlier ones released)."""
         r, counters, copies = self._reveal, self._counters, self._copies
-        for handle in handles:
-            ticket = handle.ticket
-            key = ticket.key
-            c = copies.get(key)   # _copy_for, inline
-            if c is None or (c.ticket is not ticket and c.ticket != ticket):
-                raise CacheError("the ticket belongs to no live copy of this ledger")
-            serial, holders = handle.serial, c.holders
-            if serial not in holders:
-                raise CacheError("the use handle is stale, foreign or already released")
-            holders.discard(serial)
-            valid = key in r.valid
-            c.used = c.used or valid
-            if holders:
-                continue
-            r.open_keys.discard(key)
-            counters["gpu_completed_experts"] += 1
-            counters["gpu_completed_valid_experts"] += int(valid)
-            if c.ticket.pool == "demand_staging":
-                self._drop(key)
-            else:
-                self._reindex(key)
+        completed = []   # cache-pool experts completed here, re-ranked together
+        try:
+            for handle in handles:
+                ticket = handle.ticket
+                key = ticket.key
+                c = copies.get(key)   # _copy_for, inline
+                if c is None or (c.ticket is not ticket and c.ticket != ticket):
+                    raise CacheError("the ticket belongs to no live copy of this ledger")
+                serial, holders = handle.serial, c.holders
+                if serial not in holders:
+                    raise CacheError("the use handle is stale, foreign or already released")
+                holders.discard(serial)
+                valid = key in r.valid
+                c.used = c.used or valid
+                if holders:
+                    continue
+                r.open_keys.discard(key)
+                counters["gpu_completed_experts"] += 1
+                counters["gpu_completed_valid_experts"] += int(valid)
+                if c.ticket.pool == "demand_staging":
+                    self._drop(key)
+                else:
+                    completed.append(key)
+        finally:
+            if completed:
+                self._reindex_many(completed)
 
     def finish_cpu(self, key):
         """The expert of the open demand was computed on the CPU from its master."""

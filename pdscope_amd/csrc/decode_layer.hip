@@ -195,7 +195,13 @@ __device__ __forceinline__ uint4 add_bf16x8(uint4 a, uint4 r) {
 //   resid    the layer input is x_eff = bf16(x + resid) (a residual stream);
 //            x_out receives x_eff (block 0) for the next layer's residual;
 //   next_gate / pred_out  the gate-fallback predictor of the next layer:
-//            top-k of next_gate . x_eff (no bias) into pred_out[k].
+//            top-k of next_gate . x_eff (no bias) into pred_out[k];
+//   host_words  pinned host words for a host that waits on this launch:
+//            [0, k) the routed ids, stored as soon as block 0 holds the final
+//            routing (well before the launch ends), [k, 2k) the prediction,
+//            each as (tag << 16) | id with a system-scope store, so a word is
+//            valid once it carries the caller's tag; selected (int64 [k],
+//            device) receives the routed ids at the same point.
 template <int NCH, int P, int DC, bool CHAIN>
 __global__ __launch_bounds__(256, 2) void decode_layer_kernel(
     const uint16_t *__restrict__ x, const uint16_t *__restrict__ resid, uint16_t *__restrict__ x_out,
@@ -203,7 +209,7 @@ __global__ __launch_bounds__(256, 2) void decode_layer_kernel(
     int merge_mode, const uint16_t *const *__restrict__ slots, int I, const uint16_t *__restrict__ next_gate,
     int32_t *__restrict__ pred_out, uint16_t *__restrict__ logits, int32_t *__restrict__ ids,
     uint16_t *__restrict__ weights, float *__restrict__ probs, uint16_t *__restrict__ h_ws,
-    uint16_t *__restrict__ out, uint32_t *ws) {
+    uint16_t *__restrict__ out, uint32_t *ws, int32_t *host_words, int64_t *__restrict__ selected, uint32_t tag) {
     extern __shared__ uint4 s_h[];       // k * I bf16
     __shared__ float s_logit[kDecodeMaxE];
     __shared__ float s_plogit[CHAIN ? kDecodeMaxE : 1];  // the next layer's predictor logits (last block)
@@ -404,6 +410,13 @@ __global__ __launch_bounds__(256, 2) void decode_layer_kernel(
             }
         }
         if (lane == 0) s_redo = exact ? 0 : 1;
+        // block 0 holds the final routing: hand it to a waiting host now
+        if (pub && host_words && lane < k) {
+            const int32_t e = exact ? s_tk.seli[lane] : s_tk2.seli[lane];
+            if (selected) selected[lane] = (int64_t)e;
+            __hip_atomic_store(host_words + lane, (int32_t)((tag << 16) | (uint32_t)e), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_SYSTEM);
+        }
     }
     if (has_resid && !add_now) {
 #pragma unroll
@@ -482,6 +495,9 @@ __global__ __launch_bounds__(256, 2) void decode_layer_kernel(
             topk_token<2>(s_plogit, nullptr, E, k, normalize, 0, pred_out, nullptr, nullptr, &s_tk2);
         else
             topk_token<4>(s_plogit, nullptr, E, k, normalize, 0, pred_out, nullptr, nullptr, &s_tk2);
+        if (host_words && lane < k)
+            __hip_atomic_store(host_words + k + lane, (int32_t)((tag << 16) | (uint32_t)s_tk2.seli[lane]),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
     __syncthreads();
     // y[s][c] = bf16(h_s . down_s[col c]), each half-wave its own slot: the
@@ -556,7 +572,7 @@ __global__ __launch_bounds__(256, 2) void decode_layer_kernel(
 typedef void (*DecodeLayerFn)(const uint16_t *, const uint16_t *, uint16_t *, const uint16_t *, const float *, int,
                               int, int, int, int, const uint16_t *const *, int, const uint16_t *,
                               int32_t *, uint16_t *, int32_t *, uint16_t *, float *, uint16_t *, uint16_t *,
-                              uint32_t *);
+                              uint32_t *, int32_t *, int64_t *, uint32_t);
 
 struct DecodePlan {
     DecodeLayerFn fn;        // plain launch
@@ -703,7 +719,7 @@ static int launch_decode_layer(const void *x, const void *resid, void *x_out, co
         (const uint16_t *)x, (const uint16_t *)resid, (uint16_t *)x_out, (const uint16_t *)gate, bias, H, E, k,
         normalize, merge_mode, (const uint16_t *const *)slots, I, (const uint16_t *)next_gate, pred_out,
         (uint16_t *)logits, ids, (uint16_t *)weights, probs, (uint16_t *)h_ws, (uint16_t *)out,
-        (uint32_t *)workspace);
+        (uint32_t *)workspace, nullptr, nullptr, 0u);
     return check_launch("decode_layer_kernel");
 }
 
@@ -730,41 +746,28 @@ PD_API int pdscope_decode_layer_chained(const void *x, const void *resid, void *
 //
 // A resident decode layer whose gate, slot table, predictor gate and device
 // buffers stay put from one token to the next is checked and planned once
-// (pdscope_decode_bind); each token is then one call of pdscope_decode_run:
-// the fused decode kernel, then a one-wave read-back kernel that writes the
-// routed ids, the next-layer prediction and the sticky error word into pinned
-// host memory, the routed ids as int64 into the caller's device tensor, and
-// last, after a system-scope release, the call's sequence number into a
-// pinned host word: a host that sees that number there can read the other
-// words, and knows that the decode launch (ordered before the read-back on
-// the stream) has completed.  On this device a
-// direct launch costs the host about 3 us against about 23 us for replaying
-// a captured graph of the same kernel.
+// (pdscope_decode_bind); each token is then one call of pdscope_decode_run,
+// numbered by the caller (seq, 1 .. 32767): the fused decode kernel, which
+// stores the routed ids and the next-layer prediction into pinned host words
+// as (seq << 16) | id as soon as it holds them, and the routed ids as int64
+// into the caller's device tensor; then a one-wave kernel that stores the
+// sticky error word as (seq << 16) | word.  Every word validates itself by
+// its tag, so no fence orders them; the error word is stored after the layer
+// kernel completed (stream order), so a host that reads seq in it knows the
+// launch has completed.  A host may act on the routed ids before that, while
+// the layer kernel still runs.  On this device a direct launch costs the
+// host about 3 us against about 23 us for replaying a captured graph of the
+// same kernel.
 
 namespace pd {
 
-__global__ __launch_bounds__(64) void decode_readback_kernel(const int32_t *__restrict__ ids,
-                                                             const int32_t *__restrict__ pred,
-                                                             const uint32_t *__restrict__ err, int k,
-                                                             int32_t *host_ids, int32_t *host_err,
-                                                             int64_t *__restrict__ selected, int32_t *host_seq,
-                                                             int32_t seq) {
-    const int j = threadIdx.x;
-    if (j < k) {
-        const int32_t e = ids[j];
-        // vector stores at system scope: the words reach host memory without
-        // waiting for a cache write-back at the end of the kernel
-        __hip_atomic_store(host_ids + j, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        if (pred) __hip_atomic_store(host_ids + k + j, pred[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        if (selected) selected[j] = (int64_t)e;
-    }
-    if (j == 0) {
+__global__ __launch_bounds__(64) void decode_error_readback_kernel(const uint32_t *__restrict__ err,
+                                                                   int32_t *host_err, uint32_t tag) {
+    if (threadIdx.x == 0) {
         const uint32_t w = __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(host_err, (int32_t)w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(host_err, (int32_t)((tag << 16) | (w & 0xffffu)), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_SYSTEM);
     }
-    // every lane's words above are performed before the sequence number
-    __syncthreads();
-    if (j == 0 && host_seq) __hip_atomic_store(host_seq, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 }  // namespace pd
@@ -786,7 +789,6 @@ struct pdscope_decode_binding {
     uint32_t *workspace;
     int32_t *host_ids;   // device addresses of the pinned read-back words
     int32_t *host_err;
-    int32_t *host_seq;
 };
 
 // Device address of a word of pinned host memory (an error if it is not).
@@ -803,11 +805,10 @@ static int pinned_device_address(void *host, int32_t **dev, const char *what) {
 PD_API int pdscope_decode_bind(const void *gate, const float *bias, int H, int E, int k, int normalize,
                                int merge_mode, const void *const *slots, int I, const void *next_gate,
                                int32_t *pred_out, int32_t *ids, float *probs, void *h_ws, void *workspace,
-                               int32_t *host_ids, int32_t *host_error, int32_t *host_seq,
-                               pdscope_decode_binding **binding) {
+                               int32_t *host_ids, int32_t *host_error, pdscope_decode_binding **binding) {
     if (!binding) return fail(kEInval, "decode_bind: null binding out-pointer");
     *binding = nullptr;
-    if (!host_ids || !host_error || !host_seq) return fail(kEInval, "decode_bind: null read-back pointer");
+    if (!host_ids || !host_error) return fail(kEInval, "decode_bind: null read-back pointer");
     DecodePlan plan;
     DecodeLayerFn fn = nullptr;
     // x, logits, weights and out arrive with each run: stand-ins pass the null checks here
@@ -817,15 +818,14 @@ PD_API int pdscope_decode_bind(const void *gate, const float *bias, int H, int E
     if (rc != kOk) return rc;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return fail(kEHip, "decode_bind: hipGetDevice failed");
-    int32_t *dh = nullptr, *de = nullptr, *dq = nullptr;
+    int32_t *dh = nullptr, *de = nullptr;
     if ((rc = pinned_device_address(host_ids, &dh, "host_ids")) != kOk) return rc;
     if ((rc = pinned_device_address(host_error, &de, "host_error")) != kOk) return rc;
-    if ((rc = pinned_device_address(host_seq, &dq, "host_seq")) != kOk) return rc;
     auto *b = new (std::nothrow) pdscope_decode_binding;
     if (!b) return fail(kEInval, "decode_bind: out of host memory");
     *b = pdscope_decode_binding{fn, plan.blocks, plan.lds, dev, (const uint16_t *)gate, bias, H, E, k, normalize,
                                 merge_mode, I, (const uint16_t *const *)slots, (const uint16_t *)next_gate,
-                                pred_out, ids, probs, (uint16_t *)h_ws, (uint32_t *)workspace, dh, de, dq};
+                                pred_out, ids, probs, (uint16_t *)h_ws, (uint32_t *)workspace, dh, de};
     *binding = b;
     return kOk;
 }
@@ -834,6 +834,7 @@ PD_API int pdscope_decode_run(const pdscope_decode_binding *b, const void *x, vo
                               void *weights, int64_t *selected, int32_t seq, void *stream) {
     if (!b) return fail(kEInval, "decode_run: null binding");
     if (!x || !out || !logits || !weights) return fail(kEInval, "decode_run: null pointer");
+    if (seq < 1 || seq > 0x7fff) return fail(kEInval, "decode_run: seq must be in 1 .. 32767");
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev != b->device)
         return fail(kEInval, "decode_run: the binding belongs to another device");
@@ -841,12 +842,11 @@ PD_API int pdscope_decode_run(const pdscope_decode_binding *b, const void *x, vo
     b->fn<<<b->blocks, 256, b->lds, s>>>(
         (const uint16_t *)x, nullptr, nullptr, b->gate, b->bias, b->H, b->E, b->k, b->normalize, b->merge_mode,
         b->slots, b->I, b->next_gate, b->pred_out, (uint16_t *)logits, b->ids, (uint16_t *)weights, b->probs,
-        b->h_ws, (uint16_t *)out, b->workspace);
+        b->h_ws, (uint16_t *)out, b->workspace, b->host_ids, selected, (uint32_t)seq);
     int rc = check_launch("decode_layer_kernel");
     if (rc != kOk) return rc;
-    decode_readback_kernel<<<1, 64, 0, s>>>(b->ids, b->pred_out, b->workspace + kWsError, b->k, b->host_ids,
-                                            b->host_err, selected, b->host_seq, seq);
-    return check_launch("decode_readback_kernel");
+    decode_error_readback_kernel<<<1, 64, 0, s>>>(b->workspace + kWsError, b->host_err, (uint32_t)seq);
+    return check_launch("decode_error_readback_kernel");
 }
 
 PD_API void pdscope_decode_unbind(pdscope_decode_binding *b) { delete b; }

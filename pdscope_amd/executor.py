@@ -310,6 +310,10 @@ class ExpertExecutor:
             host[key.expert] = addr
             self._table_version[key.layer] = self._table_version.get(key.layer, 0) + 1
 
+    def table_version(self, layer):
+        """A number that changes whenever an entry of `layer`'s slot table changes."""
+        return self._table_version.get(layer, 0)
+
     def table_entry(self, layer, e):
         host = self._host_tables.get(layer)
         return 0 if host is None or e >= len(host) else host[e]
@@ -323,7 +327,7 @@ class ExpertExecutor:
         ver = self._table_version.get(layer, 0)
         last = self._uploaded.get(layer)
         if last is not None and last[0] == ver:
-            if last[1] != stream:
+            if last[1] is not stream and last[1] != stream:
                 stream.wait_event(last[2])
             return dev
         i, buf = self._ring.take()
@@ -360,7 +364,10 @@ class ExpertExecutor:
 
     def reclaim(self):
         self._open()
-        for ticket in self.cache.take_retired():
+        retired = self.cache.take_retired()
+        if not retired:
+            return
+        for ticket in retired:
             if ticket in self.loads:
                 raise RuntimeError("the ledger retired a copy with a transfer in flight")
             flat = self.copies.pop(ticket, None)
@@ -440,12 +447,12 @@ class ExpertExecutor:
         """Acquire `keys`, run `launch()` (one grouped launch) on the compute stream, record one event.
 
         With launch=None the work that read these copies was enqueued on
-        `wait_for` before the ledger revealed them (a replay issued ahead of
-        the reveal): the uses are accounted and the event is recorded on that
-        stream, with no compute-stream join.  The copies were not held while
-        that work ran, so it must already have finished: `completed` is an
-        event recorded after it, and it must have completed (the caller
-        synchronised on it) or the call raises."""
+        `wait_for` before the ledger revealed them (a launch issued ahead of
+        the reveal): the uses are accounted with no compute-stream join and
+        no event of their own.  The copies were not held while that work ran,
+        so it must already have finished: `completed` proves it through
+        query() -- an event recorded after that work, or a host word the work
+        writes last -- and must report completion, or the call raises."""
         self._open()
         if launch is None and (completed is None or not completed.query()):
             raise RuntimeError("an already enqueued use of expert copies is accounted only after it has "
@@ -464,7 +471,8 @@ class ExpertExecutor:
             # (finish_gpu finds it complete)
             p = PendingCompute(handles, None, None, input_ref, tuple(keys))
             self.computes[id(p)] = p
-            self._log(event="compute_submitted", experts=len(keys))
+            if self.capture_events:
+                self._log(event="compute_submitted", experts=len(keys))
             return p
         span = self._group_stream_ctx is not None
         ctx = contextlib.nullcontext() if span else torch.cuda.stream(self.compute_stream)
@@ -518,7 +526,8 @@ class ExpertExecutor:
             self._free_events.append(ev)
         pending.event, pending.input_ref = None, None
         self.reclaim()
-        self._log(event="compute_completed", experts=len(pending.handles))
+        if self.capture_events:
+            self._log(event="compute_completed", experts=len(pending.handles))
         return pending.output
 
     def gpu(self, key, inputs):

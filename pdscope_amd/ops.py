@@ -422,22 +422,22 @@ class DecodeBinding:
     """One resident decode layer bound once (pdscope_decode_bind): its gate,
     slot table (by address: refresh the contents, not the tensor), optional
     next-layer gate and logit bias are checked and planned at construction,
-    and each token is then one C call that launches the fused decode kernel
-    and a read-back kernel.  The read-back writes the routed ids to
-    host[ids_at:ids_at+k], the next-layer prediction to
-    host[ids_at+k:ids_at+2k], the kernel's sticky error word to
-    host[error_at] and last the call's sequence number to host[seq_at]
-    (host: pinned int32 CPU tensor).  The words are readable once
-    host[seq_at] holds the call's number, which also means the decode launch
-    has completed, or once an event recorded after the call on the same
-    stream has completed.
+    and each token is then one C call, numbered seq (1 .. 32767), that
+    launches the fused decode kernel and a one-wave read-back kernel (host:
+    pinned int32 CPU tensor).  The decode kernel stores (seq << 16) | id of
+    the routed ids into host[ids_at:ids_at+k] as soon as its routing is final
+    (before it completes), and of the next-layer prediction into
+    host[ids_at+k:ids_at+2k]; the read-back kernel then stores (seq << 16) |
+    the kernel's sticky error word into host[error_at].  A word is valid
+    once it carries seq in its upper half; a tagged host[error_at] also
+    means that the decode launch has completed.  tagged_words() decodes.
 
     The binding owns its device scratch (int32 ids, prediction, h) and keeps
     every tensor it bound alive.  Calls on one device share the fused
     kernel's workspace, so they must be ordered on one stream."""
 
-    def __init__(self, gate, slots, I, top_k, normalize, *, host, error_at, seq_at=None, ids_at=0,
-                 merge="fused", next_gate=None, bias=None):
+    def __init__(self, gate, slots, I, top_k, normalize, *, host, error_at, ids_at=0, merge="fused",
+                 next_gate=None, bias=None):
         dev = gate.device
         _need(gate, "gate", BF16, 2, dev)
         _need(slots, "slots", torch.int64, 1, dev)
@@ -458,11 +458,8 @@ class DecodeBinding:
         if (not isinstance(host, torch.Tensor) or host.device.type != "cpu" or host.dtype != torch.int32
                 or not host.is_pinned() or not host.is_contiguous()):
             raise ValueError("DecodeBinding: host must be a contiguous pinned int32 CPU tensor")
-        if seq_at is None:
-            seq_at = error_at + 1
         if not (0 <= ids_at and ids_at + 2 * k <= host.numel() and 0 <= error_at < host.numel()
-                and 0 <= seq_at < host.numel() and seq_at != error_at
-                and not ids_at <= error_at < ids_at + 2 * k and not ids_at <= seq_at < ids_at + 2 * k):
+                and not ids_at <= error_at < ids_at + 2 * k):
             raise ValueError("DecodeBinding: read-back words outside host or overlapping")
         self.H, self.E, self.I, self.k = H, E, int(I), k
         self.device = dev
@@ -478,27 +475,39 @@ class DecodeBinding:
             rc = lib.pdscope_decode_bind(_p(gate), _p(bias), H, E, k, int(bool(normalize)), merge_mode(merge),
                                          _p(slots), self.I, _p(next_gate), _p(self.pred), _p(self.ids), None,
                                          _p(self.h_ws), _p(self.workspace), base + 4 * ids_at, base + 4 * error_at,
-                                         base + 4 * seq_at, ctypes.byref(handle))
+                                         ctypes.byref(handle))
         if rc != 0:
             _lib.raise_for("pdscope_decode_bind", rc)
         self._handle = handle.value
         self._run = lib.pdscope_decode_run
         self._unbind = lib.pdscope_decode_unbind
 
+    @staticmethod
+    def tagged_words(words, seq):
+        """The values of read-back words (a sequence of int32) if every one
+        carries seq in its upper half, else None."""
+        vals = []
+        for w in words:
+            w = int(w)
+            if w >> 16 != seq:
+                return None
+            vals.append(w & 0xFFFF)
+        return vals
+
     def run_ptrs(self, x, out, logits, weights, selected, seq, stream):
         """The per-token call on raw addresses (x [H], out [H], logits [E],
-        weights [k] bf16, selected [k] int64 or 0), the int32 sequence number
-        the read-back writes last, and a raw hipStream_t, for callers that
-        checked the tensors themselves."""
+        weights [k] bf16, selected [k] int64 or 0), its sequence number
+        (1 .. 32767, the tag of its read-back words) and a raw hipStream_t,
+        for callers that checked the tensors themselves."""
         rc = self._run(self._handle, x, out, logits, weights, selected, seq, stream)
         if rc != 0:
             _lib.raise_for("pdscope_decode_run", rc)
 
-    def run(self, x, out, logits, weights, selected=None, stream=None, seq=0):
+    def run(self, x, out, logits, weights, selected=None, stream=None, seq=1):
         """One token: x [1,H] bf16 in; out [1,H], logits [1,E], weights [1,k]
         bf16 and optionally selected [1,k] int64 out, on `stream` (default:
-        the current stream of the binding's device); host[seq_at] receives
-        `seq` last."""
+        the current stream of the binding's device); the read-back words carry
+        `seq` (1 .. 32767)."""
         if self._handle is None:
             raise ValueError("DecodeBinding is closed")
         dev = self.device

@@ -69,16 +69,17 @@ _raw_current_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 _READBACK_POLL_S = 0.002
 
 
-class _HostWordEquals:
-    """Completion test of a bound launch: its read-back wrote `value` into
-    words[at] last (query() as an event's)."""
+class _HostWordTagged:
+    """Completion test of a bound launch numbered `value`: its read-back
+    stored the error word tagged with that number into words[at] after the
+    launch completed (query() as an event's)."""
     __slots__ = ("words", "at", "value")
 
     def __init__(self, words, at):
         self.words, self.at, self.value = words, at, None
 
     def query(self):
-        return self.value is not None and self.words[self.at] == self.value
+        return self.value is not None and int(self.words[self.at]) >> 16 == self.value
 
 
 def load_hot_profile(path, masters, slots):
@@ -184,9 +185,8 @@ class PDScopeCudaRuntime:
         self._pinned_np = self._pinned_counts.numpy()   # host reads without tensor indexing
         self._streams = {}   # raw hipStream_t -> its torch Stream object
         self._err_at = 2 * self.E + 8    # the decode error word's place in _pinned_counts
-        self._seq_at = 2 * self.E + 9    # the bound launch's sequence word
-        self._seq = 0
-        self._readback = _HostWordEquals(self._pinned_np, self._seq_at)
+        self._seq = 0                    # number of the last bound launch (1 .. 32767, the read-back tag)
+        self._readback = _HostWordTagged(self._pinned_np, self._err_at)
         self._decode_ok = {}             # k -> (single launch fits, with the fused predictor)
         self._out_stash = None           # (raw stream, k, outputs) of the next bound decode call
         self._keys_full = set()          # layers whose key list holds every expert
@@ -237,6 +237,9 @@ class PDScopeCudaRuntime:
                 del self.pending[key]
 
     def _retire_current(self, layer, *, wait):
+        if not self.transient:   # no speculative copy to retire
+            self.executor.reclaim()
+            return
         unfinished = set(self.cache.unfinished_demand_keys)
         for key in list(self.transient):
             if key.layer != layer or key in unfinished:
@@ -296,22 +299,51 @@ class PDScopeCudaRuntime:
             return st[2]
         return self._new_decode_outputs(k)
 
-    def _await_readback(self, seq, stream):
-        """Poll the pinned sequence word until the bound launch numbered `seq`
-        wrote it (its read-back words have then landed and the launch has
-        completed); after _READBACK_POLL_S, block on an event instead."""
-        words, at = self._pinned_np, self._seq_at
-        self._readback.value = seq
-        if words[at] == seq:
-            return
-        deadline = time.perf_counter() + _READBACK_POLL_S
-        while words[at] != seq:
-            if time.perf_counter() > deadline:
+    def _tagged_or_raise(self, at, n, seq):
+        """Values of the n read-back words at `at` stored by the bound launch
+        numbered seq; the launch is known to have completed, so each word must
+        carry seq."""
+        vals = ops.DecodeBinding.tagged_words(self._pinned_np[at:at + n].tolist(), seq)
+        if vals is None:
+            raise RuntimeError("a bound decode launch completed without its read-back words")
+        return vals
+
+    def _await_tagged(self, at, n, seq, stream):
+        """Values of the n read-back words at `at` once each carries seq: the
+        bound launch numbered seq stores them (the routed ids before it
+        completes, the error word after).  Polls; after _READBACK_POLL_S it
+        blocks on an event recorded on `stream` instead."""
+        words, last = self._pinned_np, at + n - 1
+        deadline = None
+        while True:
+            if int(words[last]) >> 16 == seq:
+                vals = ops.DecodeBinding.tagged_words(words[at:at + n].tolist(), seq)
+                if vals is not None:
+                    return vals
+            now = time.perf_counter()
+            if deadline is None:
+                deadline = now + _READBACK_POLL_S
+            elif now > deadline:
                 self._copy_done.record(stream)
                 self._copy_done.synchronize()
-                if words[at] != seq:
-                    raise RuntimeError("a bound decode launch completed without its read-back words")
-                return
+                return self._tagged_or_raise(at, n, seq)
+
+    def _next_counts(self, predict, pred_ids, n0, k, E, seq):
+        """The next-layer forecast {expert: predicted tokens}: the fused
+        prediction's k tagged words (seq) of a bound launch, else the
+        predictor histogram copied into the read-back buffer."""
+        if not predict:
+            return {}
+        if pred_ids is None:
+            return {e: c for e, c in enumerate(self._pinned_np[n0:n0 + E].tolist()) if c}
+        # one token: each predicted expert once
+        vals = self._tagged_or_raise(n0, k, seq if seq is not None else self._seq)
+        next_counts = {e: 1 for e in vals}
+        if len(next_counts) != k:
+            raise AssertionError("decode prediction selected duplicate experts")
+        if min(next_counts) < 0 or max(next_counts) >= E:
+            raise AssertionError("decode prediction selected an expert id outside [0, E)")
+        return next_counts
 
     def _layer_fully_resident(self, layer):
         ready = self.cache.ready_in_cache
@@ -336,7 +368,8 @@ class PDScopeCudaRuntime:
         ws = self._workspace(T, k)
         cur = self._current_stream()
         key = self._layer_keys(layer).__getitem__   # routed ids are range-checked below
-        nkey = lambda e: self._key(layer + 1, e)  # noqa: E731
+        nkey = (self._layer_keys(layer + 1).__getitem__ if (layer + 1) in self.layers
+                else lambda e: self._key(layer + 1, e))  # noqa: E731
         self.poll()
         before = self.cache.stats()
         # decode runs the bound single-launch layer over the slot table
@@ -357,7 +390,7 @@ class PDScopeCudaRuntime:
             ring = self._graph_turn.get(layer, 0)
             self._graph_turn[layer] = ring ^ 1
             ring_out = self._ring_output(layer, ring)
-        replay_table, late_replays = None, 0
+        launch_table, late_replays = None, 0
 
         # ---- 1-2: route (+ predictor), grouping, one D2H of the demand
         if graph_ok:
@@ -374,8 +407,9 @@ class PDScopeCudaRuntime:
         pred_ids = None
         bound_routing = graph_path
         if graph_path:
-            # entries the first launch saw (a copy still in flight reads as null)
-            replay_table = list(self.executor.table(layer, E)[1])
+            # the table version the first launch saw (a copy still in flight
+            # reads as null; a copy that lands moves the version on)
+            launch_table = self.executor.table_version(layer)
             binding, seq = self._bound_decode(layer, x, gate, normalize, k, out, r_logits, r_weights, r_selected,
                                               next_gate=graph_pred, stream=cur)
             logits, ids, weights = r_logits, r_selected, r_weights
@@ -403,42 +437,40 @@ class PDScopeCudaRuntime:
         host, hn = self._pinned_counts, self._pinned_np
         err_at = self._err_at
         if graph_path:
-            # the bound launch's read-back wrote the routed ids, its prediction
-            # and the fused kernel's sticky error word into `host`
+            # the bound launch stores the routed ids, its prediction and the
+            # fused kernel's sticky error word into `host` itself (tagged seq)
             if pred_ids is None and predict:
                 host[n0:n0 + E].copy_(nws.hist, non_blocking=True)
         else:
             host[:n0].copy_(counts_dev, non_blocking=True)
             if predict:
                 host[n0:n0 + E].copy_(nws.hist, non_blocking=True)
-        # the bound launch's read-back numbers its words: with nothing else to
-        # read back, the host waits for that number instead of an event
+        # with nothing else to read back, the bound launch's routed ids are
+        # taken as soon as the kernel stored them, and the demand is revealed
+        # while the kernel still runs; its completion is awaited after that
+        early = graph_path and not (predict and pred_ids is None)
         completed = self._copy_done
-        if graph_path and not (predict and pred_ids is None):
-            self._await_readback(seq, cur)
-            completed = self._readback
+        decode_failed = False
+        if early:
+            sel = self._await_tagged(0, k, seq, cur)
         else:
             self._copy_done.record(cur)
             self._copy_done.synchronize()
-        if graph_path:
-            self._raise_if_decode_gave_up(int(hn[err_at]))
+            if graph_path:
+                sel = self._tagged_or_raise(0, k, seq)
+                decode_failed = self._tagged_or_raise(err_at, 1, seq)[0] != 0
+            elif T == 1:
+                sel = hn[:k].tolist()
         if T > 1:
             counts = {e: c for e, c in enumerate(hn[:E].tolist()) if c}
         else:
-            sel = hn[:k].tolist()
             if len(set(sel)) != k:
                 raise AssertionError("decode routing selected duplicate experts")
             if min(sel) < 0 or max(sel) >= E:
                 raise AssertionError("decode routing selected an expert id outside [0, E)")
             counts = {e: 1 for e in sel}
-        if pred_ids is not None:   # one token: each predicted expert once
-            next_counts = {e: 1 for e in hn[n0:n0 + k].tolist()}
-            if len(next_counts) != k:
-                raise AssertionError("decode prediction selected duplicate experts")
-            if min(next_counts) < 0 or max(next_counts) >= E:
-                raise AssertionError("decode prediction selected an expert id outside [0, E)")
-        else:
-            next_counts = ({e: c for e, c in enumerate(hn[n0:n0 + E].tolist()) if c} if predict else {})
+        if not early:
+            next_counts = self._next_counts(predict, pred_ids, n0, k, E, None)
         if sum(counts.values()) != T * k:
             raise AssertionError("lost or duplicated routed assignment")
 
@@ -449,6 +481,13 @@ class PDScopeCudaRuntime:
             self.prediction_counts[phase]["hits"] += len(set(prior) & set(counts))
             self.prediction_counts[phase]["total"] += len(prior)
         observed = dict(self.prediction_counts[phase])
+        if early:
+            # the launch has completed once its error word carries seq; a set
+            # word fails the call after the ledger has closed its demand
+            decode_failed = self._await_tagged(err_at, 1, seq, cur)[0] != 0
+            completed = self._readback
+            self._readback.value = seq
+            next_counts = self._next_counts(predict, pred_ids, n0, k, E, seq)
 
         # ---- plan: with a cost table and a CPU backend, plan_pdscope splits the
         # experts between the CPU backend, resident copies and demand staging
@@ -557,7 +596,9 @@ class PDScopeCudaRuntime:
                     cpu_tasks[e] = ex.submit_cpu(key(e), r)
         if graph_path:
             if not demand:  # with misses the demand batch below launches over the completed table
-                if replay_table is None or any(replay_table[e] == 0 for e in counts):
+                table = self.executor.table(layer, E)[1]
+                if (launch_table is None or launch_table != self.executor.table_version(layer)
+                        or any(table[e] == 0 for e in counts)):
                     # not launched yet (planned path), or a routed copy landed
                     # after the first launch: launch over the completed table
                     late_replays += 1
@@ -622,6 +663,7 @@ class PDScopeCudaRuntime:
         issued, skipped = [], []
         if has_next:
             forecast = (list(decision["prefetch_queue"]) if planned
+                        else sorted(next_counts) if pred_ids is not None   # one token: every count is 1
                         else sorted(next_counts, key=lambda e: (-next_counts[e], e)))
             for e in forecast:
                 target = nkey(e)
@@ -695,10 +737,12 @@ class PDScopeCudaRuntime:
             # `host` themselves: read it once they completed
             self._copy_done.record(cur)
             self._copy_done.synchronize()
-            self._raise_if_decode_gave_up(int(hn[err_at]))
+            decode_failed |= self._tagged_or_raise(err_at, 1, self._seq)[0] != 0
         self.cache.end_demand(identity)
         self._retire_current(layer, wait=True)
         self.poll()
+        if decode_failed:
+            self._raise_if_decode_gave_up(True)
         # the ledger never chooses a static copy as a victim; checking the
         # layer just served keeps the guard without a scan of every layer
         if self.diagnostics and any(self.cache.lookup(h) is None for h in self._hot_by_layer.get(layer, ())):
@@ -733,8 +777,8 @@ class PDScopeCudaRuntime:
                    scheduler="cross_layer" if planned else "gpu_all", predictor_prior_hit_rate=0.0,
                    selected_sha256=digest(routing.selected) if self.diagnostics else None,
                    next_selected_sha256=digest(pred_sel.long()) if self.diagnostics and predict else None,
-                   ready_at_reveal=sum(o.ready_hit for o in observations),
-                   loading_at_reveal=sum(o.state_at_reveal == "loading" for o in observations),
+                   ready_at_reveal=sum(o[6] is not None for o in observations),    # hit_source: a ready hit
+                   loading_at_reveal=sum(o[4] == "loading" for o in observations),  # state_at_reveal
                    counters=delta, ping_pong_slots=ping_pong,
                    static_retention="CPU placement keeps the charged device copy of a static hot expert",
                    merge_mode=self.merge, input_pregather=self.input_pregather, demand_slots=self.demand_slots,
@@ -866,8 +910,8 @@ class PDScopeCudaRuntime:
         int64; with next_gate the same launch predicts the next layer.  The
         routed ids, the prediction and the fused kernel's sticky error word
         land in the pinned read-back buffer (ids at 0, prediction at k, error
-        word at _err_at, then the launch's sequence number at _seq_at).
-        Returns (the binding, the sequence number)."""
+        word at _err_at, each tagged with the launch's number, the routed ids
+        before the kernel completes).  Returns (the binding, that number)."""
         if key is None:
             key = (layer, k, normalize, gate.data_ptr(), 0 if next_gate is None else next_gate.data_ptr())
         cur = torch.cuda.current_stream(self.device) if stream is None else stream
@@ -877,10 +921,9 @@ class PDScopeCudaRuntime:
         b = self._bindings.get(key)
         if b is None:
             b = ops.DecodeBinding(gate, slots_dev, self.I, k, normalize, host=self._pinned_counts,
-                                  error_at=self._err_at, seq_at=self._seq_at, merge=self.merge,
-                                  next_gate=next_gate)
+                                  error_at=self._err_at, merge=self.merge, next_gate=next_gate)
             self._bindings[key] = b
-        self._seq = self._seq % 0x7FFFFFFF + 1
+        self._seq = self._seq % 0x7FFF + 1
         b.run_ptrs(x.data_ptr(), out.data_ptr(), logits.data_ptr(), weights.data_ptr(), selected.data_ptr(),
                    self._seq, cur.cuda_stream)
         self.bound_launches += 1

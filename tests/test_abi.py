@@ -53,10 +53,10 @@ def test_invalid_arguments_raise_before_any_launch():
     handle = ctypes.c_void_p()
     with pytest.raises(ValueError, match="null binding out-pointer"):
         _lib.call("pdscope_decode_bind", None, None, 2048, 128, 8, 1, 1, None, 768, None, None, None, None, None,
-                  None, None, None, None, None)
+                  None, None, None, None)
     with pytest.raises(ValueError, match="null read-back pointer"):
         _lib.call("pdscope_decode_bind", None, None, 2048, 128, 8, 1, 1, None, 768, None, None, None, None, None,
-                  None, None, None, None, ctypes.byref(handle))
+                  None, None, None, ctypes.byref(handle))
     assert handle.value is None
     with pytest.raises(ValueError, match="null binding"):
         _lib.call("pdscope_decode_run", None, None, None, None, None, None, 1, None)

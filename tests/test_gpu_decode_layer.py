@@ -535,10 +535,10 @@ def test_bound_decode_equals_the_chained_launch_and_reads_back(pd):
     """ops.DecodeBinding (pdscope_decode_bind / _run): each token's out,
     logits, weights and int64 ids equal pdscope_decode_layer_chained with the
     same arguments bit for bit; the read-back words in pinned host memory
-    hold the routed ids, the next-layer prediction, a clear error word and
-    the call's sequence number, for several tokens in a row; a binding
-    without a next gate leaves the prediction words alone.  Bad host buffers
-    are rejected at bind time."""
+    hold the routed ids, the next-layer prediction and a clear error word,
+    each tagged with the call's number, for several tokens in a row; a
+    binding without a next gate leaves the prediction words alone.  Bad host
+    buffers and numbers are rejected."""
     import ctypes
 
     from pdscope_amd import _lib
@@ -548,10 +548,9 @@ def test_bound_decode_equals_the_chained_launch_and_reads_back(pd):
     l1 = synthetic.make_layer(**dict(synthetic.QWEN, seed=81), device=DEV)
     slots = ops.slot_table([l0.experts[e] for e in range(E)], DEV)
     host = torch.full((64,), -7, dtype=torch.int32, pin_memory=True)
-    bound = ops.DecodeBinding(l0.gate, slots, I, k, True, host=host, error_at=40, seq_at=50, merge="reference",
+    bound = ops.DecodeBinding(l0.gate, slots, I, k, True, host=host, error_at=40, merge="reference",
                               next_gate=l1.gate)
-    plain = ops.DecodeBinding(l0.gate, slots, I, k, True, host=host, ids_at=20, error_at=41, seq_at=51,
-                              merge="reference")
+    plain = ops.DecodeBinding(l0.gate, slots, I, k, True, host=host, ids_at=20, error_at=41, merge="reference")
     try:
         for seed in range(400, 404):
             x = synthetic.make_tokens(1, H, seed=seed, device=DEV)
@@ -559,10 +558,11 @@ def test_bound_decode_equals_the_chained_launch_and_reads_back(pd):
                        logits=torch.empty((1, E), dtype=torch.bfloat16, device=DEV),
                        weights=torch.empty((1, k), dtype=torch.bfloat16, device=DEV),
                        selected=torch.empty((1, k), dtype=torch.int64, device=DEV))
-            bound.run(x, got["out"], got["logits"], got["weights"], got["selected"], seq=seed)
+            tag = seed - 399
+            bound.run(x, got["out"], got["logits"], got["weights"], got["selected"], seq=tag)
             pout = torch.empty((1, H), dtype=torch.bfloat16, device=DEV)
             plain.run(x, pout, torch.empty((1, E), dtype=torch.bfloat16, device=DEV),
-                      torch.empty((1, k), dtype=torch.bfloat16, device=DEV), seq=seed + 1000)
+                      torch.empty((1, k), dtype=torch.bfloat16, device=DEV), seq=tag + 1000)
             want = dict(out=torch.empty((1, H), dtype=torch.bfloat16, device=DEV),
                         logits=torch.empty((1, E), dtype=torch.bfloat16, device=DEV),
                         ids=torch.empty((1, k), dtype=torch.int32, device=DEV),
@@ -577,13 +577,16 @@ def test_bound_decode_equals_the_chained_launch_and_reads_back(pd):
                 assert torch.equal(got[n], want[n]), (seed, n)
             assert torch.equal(pout, want["out"]), seed
             assert torch.equal(got["selected"], want["ids"].long()), seed
-            words = host.numpy()
-            assert words[:k].tolist() == want["ids"][0].tolist(), seed
-            assert words[k:2 * k].tolist() == want["pred"].tolist(), seed
-            assert words[20:20 + k].tolist() == want["ids"][0].tolist(), seed
-            assert words[20 + k:20 + 2 * k].tolist() == [-7] * k, seed   # no next gate bound
-            assert words[40] == 0 and words[41] == 0, seed
-            assert words[50] == seed and words[51] == seed + 1000, seed
+            words = host.numpy().tolist()
+            untag = ops.DecodeBinding.tagged_words
+            assert untag(words[:k], tag) == want["ids"][0].tolist(), seed
+            assert untag(words[k:2 * k], tag) == want["pred"].tolist(), seed
+            assert untag(words[20:20 + k], tag + 1000) == want["ids"][0].tolist(), seed
+            assert words[20 + k:20 + 2 * k] == [-7] * k, seed   # no next gate bound
+            assert untag(words[40:41], tag) == [0] and untag(words[41:42], tag + 1000) == [0], seed
+        for bad in (0, 0x8000):   # a number outside 1 .. 32767 is refused before any launch
+            with pytest.raises(ValueError, match="seq must be"):
+                plain.run(x, pout, got["logits"], got["weights"], seq=bad)
     finally:
         bound.close()
         plain.close()
@@ -593,8 +596,7 @@ def test_bound_decode_equals_the_chained_launch_and_reads_back(pd):
         ops.DecodeBinding(l0.gate, slots, I, k, True, host=torch.zeros(64, dtype=torch.int32), error_at=40)
     with pytest.raises(ValueError, match="overlapping"):
         ops.DecodeBinding(l0.gate, slots, I, k, True, host=host, error_at=3)
-    with pytest.raises(ValueError, match="overlapping"):
-        ops.DecodeBinding(l0.gate, slots, I, k, True, host=host, error_at=40, seq_at=40)
+
     # the C-ABI itself refuses read-back words outside pinned host memory
     plain_words = (ctypes.c_int32 * 32)()
     handle = ctypes.c_void_p()
@@ -603,7 +605,6 @@ def test_bound_decode_equals_the_chained_launch_and_reads_back(pd):
     with pytest.raises(ValueError, match="pinned host memory"):
         _lib.call("pdscope_decode_bind", l0.gate.data_ptr(), None, H, E, k, 1, 1, slots.data_ptr(), I, None, None,
                   ids.data_ptr(), None, h_ws.data_ptr(), ops.decode_workspace(DEV, H).data_ptr(),
-                  ctypes.addressof(plain_words), ctypes.addressof(plain_words) + 64,
-                  ctypes.addressof(plain_words) + 68, ctypes.byref(handle))
+                  ctypes.addressof(plain_words), ctypes.addressof(plain_words) + 64, ctypes.byref(handle))
     assert handle.value is None
     _assert_sync_clean(ops, H)

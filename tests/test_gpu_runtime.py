@@ -337,8 +337,8 @@ def test_runtime_bound_decode_matches_the_single_launch_layer(orc):
 def test_runtime_raises_when_the_fused_decode_error_word_is_set():
     """The fused decode kernel sets a sticky error word when a bounded wait
     gives up.  Forced from the host here (the word is pre-set; the kernel only
-    ever sets it), the runtime must raise on that layer call, clear the word,
-    and serve the next call normally."""
+    ever sets it), the runtime must raise on that layer call once the ledger
+    has closed its demand, clear the word, and serve the next call normally."""
     from pdscope_amd import ops, synthetic
     from pdscope_amd.cache import ExpertKey
     from pdscope_amd.pdscope_runtime import PDScopeCudaRuntime
@@ -356,6 +356,11 @@ def test_runtime_raises_when_the_fused_decode_error_word_is_set():
         with pytest.raises(RuntimeError, match="bounded internal wait gave up"):
             rt.forward(x, layers[0].gate, layer=0, step=2)
         assert int(word[ops.DECODE_WS_ERROR_WORD].item()) == 0
+        # the failed call closed its demand: the next token is served
+        out3, _, row3 = rt.forward(x, layers[0].gate, layer=0, step=3)
+        torch.cuda.synchronize()
+        assert row3["decode_path"] == "bound_launch" and torch.equal(out3, out)
+        closure(rt)
     finally:
         rt.close()
     # a fresh runtime on the same device serves normally after the cleared word
