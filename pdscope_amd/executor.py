@@ -91,10 +91,11 @@ class PendingCpu:
 class PendingCompute:
     handles: tuple
     output: object
-    event: object                 # completion event; None for a use accounted after it completed
+    event: object                 # completion event (or the caller's proof); None: accounted after it completed
     input_ref: object
     keys: tuple = ()
     timing_start: object = None   # start event of the launch when stages are profiled
+    event_owned: bool = True      # the event came from this executor's pool
 
 
 class _PinnedRing:
@@ -310,6 +311,10 @@ class ExpertExecutor:
             host[key.expert] = addr
             self._table_version[key.layer] = self._table_version.get(key.layer, 0) + 1
 
+    def table_full(self, layer, E):
+        """Whether every one of `layer`'s E experts has a ready device copy in its slot table."""
+        return 0 not in self._host_table(layer, E)
+
     def table_version(self, layer):
         """A number that changes whenever an entry of `layer`'s slot table changes."""
         return self._table_version.get(layer, 0)
@@ -443,20 +448,30 @@ class ExpertExecutor:
             self._group_stream_ctx.__exit__(None, None, None)
             self._group_stream_ctx = None
 
-    def gpu_group(self, keys, launch, *, input_ref=None, wait_for=None, completed=None):
+    def gpu_group(self, keys, launch, *, input_ref=None, wait_for=None, completed=None, running=None):
         """Acquire `keys`, run `launch()` (one grouped launch) on the compute stream, record one event.
 
         With launch=None the work that read these copies was enqueued on
         `wait_for` before the ledger revealed them (a launch issued ahead of
         the reveal): the uses are accounted with no compute-stream join and
-        no event of their own.  The copies were not held while that work ran,
-        so it must already have finished: `completed` proves it through
-        query() -- an event recorded after that work, or a host word the work
-        writes last -- and must report completion, or the call raises."""
+        no event of their own.  Either that work has finished -- `completed`
+        proves it through query() (an event recorded after the work, or a
+        host word the work writes last) and must report completion, or the
+        call raises -- or it may still run: `running` is such a proof (with
+        synchronize()) that need not report completion yet, and finish_gpu
+        waits on it.  A running use is held from this call on, so the caller
+        must make sure that nothing could evict these copies between the
+        work's launch and this call (the runtime reveals them first, with no
+        ledger call in between: an expert of the open demand is never
+        evicted)."""
         self._open()
-        if launch is None and (completed is None or not completed.query()):
-            raise RuntimeError("an already enqueued use of expert copies is accounted only after it has "
-                               "completed: pass the completed event recorded after it")
+        if launch is None:
+            if (completed is None) == (running is None):
+                raise RuntimeError("an already enqueued use of expert copies needs exactly one of completed= "
+                                   "(the work has finished) and running= (a proof to wait on)")
+            if completed is not None and not completed.query():
+                raise RuntimeError("an already enqueued use of expert copies is accounted only after it has "
+                                   "completed: pass the completed event recorded after it")
         handles = self.cache.acquire_many(keys)
         copies, loads = self.copies, self.loads
         for h in handles:
@@ -467,9 +482,9 @@ class ExpertExecutor:
                 ev = self._landed.pop(h.ticket, None)
                 if ev is not None:
                     self._free_events.append(ev)
-            # the work completed before the call: no event of its own
-            # (finish_gpu finds it complete)
-            p = PendingCompute(handles, None, None, input_ref, tuple(keys))
+            # no event of its own: finish_gpu finds the work complete, or
+            # waits on the caller's proof
+            p = PendingCompute(handles, None, running, input_ref, tuple(keys), event_owned=False)
             self.computes[id(p)] = p
             if self.capture_events:
                 self._log(event="compute_submitted", experts=len(keys))
@@ -522,7 +537,7 @@ class ExpertExecutor:
         if pending.timing_start is not None:
             self.stage_timings["gpu_forward_device_span_ms"] = pending.timing_start.elapsed_time(ev)
             pending.timing_start = None
-        if ev is not None:
+        if ev is not None and pending.event_owned:
             self._free_events.append(ev)
         pending.event, pending.input_ref = None, None
         self.reclaim()

@@ -191,6 +191,7 @@ class PDScopeCudaRuntime:
         self._out_stash = None           # (raw stream, k, outputs) of the next bound decode call
         self._keys_full = set()          # layers whose key list holds every expert
         self._copy_done = torch.cuda.Event()
+        self._layer_done = torch.cuda.Event()    # end of a prelaunched prefill layer
         try:
             for key in hot_keys:
                 self.executor.finish_load(self.executor.load(key, origin="initial"), wait=True)
@@ -385,6 +386,11 @@ class PDScopeCudaRuntime:
         # first, and the bound launch serves the layer when the plan keeps
         # every routed expert on the GPU (decided below)
         graph_path = graph_ok and not planned
+        # a prefill layer whose every expert has a ready device copy is
+        # launched whole before its counts come back, and its demand is
+        # revealed while it runs (nothing evicts between the launch and the
+        # reveal: no ledger call comes in between)
+        prelaunch = T > 1 and not planned and not self.input_pregather and self.executor.table_full(layer, E)
         ring_out = None
         if graph_ok and self.graph_output_pool:
             ring = self._graph_turn.get(layer, 0)
@@ -428,7 +434,10 @@ class PDScopeCudaRuntime:
             packed, n0 = None, k   # the bound launch needs no grouping
         else:
             _, _, _, packed = ws.views(T)
-            if T > 1:
+            if prelaunch:
+                pre_bm = self._pack_scheduled(ids, packed, ws)
+                counts_dev = packed.counts
+            elif T > 1:
                 ops.pack(ids, E, out=packed, workspace=ws.pack_ws)
                 counts_dev = packed.counts
             else:
@@ -455,6 +464,8 @@ class PDScopeCudaRuntime:
             sel = self._await_tagged(0, k, seq, cur)
         else:
             self._copy_done.record(cur)
+            if prelaunch:
+                self._launch_resident_layer(x, packed, weights, out, ws, layer, pre_bm, cur)
             self._copy_done.synchronize()
             if graph_path:
                 sel = self._tagged_or_raise(0, k, seq)
@@ -496,12 +507,13 @@ class PDScopeCudaRuntime:
         # (state, ticket) of each routed expert's copy, or None (no views built)
         has_next = predict and (layer + 1) in self.layers
         views = None
-        if not planned and T == 1 and all(o[4] == "ready" for o in observations):
+        if not planned and all(o[4] == "ready" for o in observations):
             # every routed copy was ready at the reveal (the observations come
             # in expert order): all resident, none loading, no demand
             decision = None
             cpu_list, demand = [], []
-            resident = [o[0].expert for o in observations]
+            resident = ([o[0].expert for o in observations] if T == 1
+                        else sorted(counts, key=lambda e: (-counts[e], e)))
         elif planned:
             views = {e: self.cache.residency(key(e)) for e in counts}
             hit_rate = observed["hits"] / observed["total"] if observed["total"] else 0.0
@@ -612,6 +624,11 @@ class PDScopeCudaRuntime:
                     launch = None
                 tasks.append(ex.gpu_group([key(e) for e in resident], launch, input_ref=x, wait_for=cur,
                                           completed=completed))
+        elif resident and prelaunch:
+            # the whole layer runs on `cur` since before the reveal: hold its
+            # copies from now on, while it still runs; finishing waits for it
+            tasks.append(ex.gpu_group([key(e) for e in resident], None, input_ref=x, wait_for=cur,
+                                      running=self._layer_done))
         elif resident:
             ex.table(layer, E)
             require_copies(resident if not decode_fast else sorted(counts))
@@ -661,7 +678,9 @@ class PDScopeCudaRuntime:
         # ---- retire this layer's speculation, prefetch the next layer's forecast
         self._retire_current(layer, wait=True)
         issued, skipped = [], []
-        if has_next:
+        if has_next and not planned and ex.table_full(layer + 1, E):
+            pass   # every forecast expert already has a ready copy: nothing to prefetch
+        elif has_next:
             forecast = (list(decision["prefetch_queue"]) if planned
                         else sorted(next_counts) if pred_ids is not None   # one token: every count is 1
                         else sorted(next_counts, key=lambda e: (-next_counts[e], e)))
@@ -694,8 +713,9 @@ class PDScopeCudaRuntime:
         add_in = None
         if cpu_rows or native_cpu:
             offs = packed.offsets.cpu().tolist() if T == 1 else offs
-        # a graph-served layer with no CPU rows has nothing left to enqueue here
-        finish_ctx = (contextlib.nullcontext() if graph_path and not cpu_rows and not native_cpu
+        # a graph-served or prelaunched layer with no CPU rows has nothing
+        # left to enqueue here (its merge ran with the launch)
+        finish_ctx = (contextlib.nullcontext() if (graph_path or prelaunch) and not cpu_rows and not native_cpu
                       else torch.cuda.stream(ex.compute_stream))
         with finish_ctx:
             for e, rows in cpu_rows.items():
@@ -719,7 +739,7 @@ class PDScopeCudaRuntime:
                 del handles
                 for e in native_cpu:
                     ws.y[offs[e] * H:offs[e + 1] * H].zero_()
-            if not (decode_fast or graph_path):
+            if not (decode_fast or graph_path or prelaunch):
                 ops.merge(ws.y, packed.row_of, weights, out, add_in=add_in, mode=self.merge)
         if native_cpu:
             for e in native_cpu:
@@ -727,7 +747,7 @@ class PDScopeCudaRuntime:
             note = getattr(self.cpu_backend, "note_native_dispatch", None)
             if note is not None:
                 note(len(native_cpu))
-        if not (graph_path and not late_replays):
+        if not ((graph_path and not late_replays) or prelaunch):
             # (a launch served before the reveal enqueued nothing on the compute stream)
             done = torch.cuda.Event()
             done.record(ex.compute_stream)
@@ -786,7 +806,7 @@ class PDScopeCudaRuntime:
                    pipeline="CPU queue on the backend beside the GPU launches; demand copies in staging-slot "
                             "batches before next-layer speculation",
                    decode_path=("bound_launch" if graph_path else "fused_gemv" if decode_fast else "grouped")
-                   if phase == "decode" else "grouped",
+                   if phase == "decode" else "prelaunched" if prelaunch else "grouped",
                    measured_performance=False)
         return out, routing, row
 
@@ -880,6 +900,31 @@ class PDScopeCudaRuntime:
         if self.demand_slots >= 6:
             return self.demand_slots // 2, 2
         return 1, self.demand_slots
+
+    def _pack_scheduled(self, ids, packed, ws):
+        """Grouping of a prelaunched layer with the balanced schedule of all
+        experts written by the pack launch itself; returns the row tile (from
+        the mean rows per expert, which needs no counts on the host)."""
+        T, k = ids.shape
+        bm = ops.grouped_block_m((T * k) // self.E)
+        bmd = L.down_block_m(bm, self.H, self.I)
+        sched = (ws.sel_all, bm, ws.sel_order, ws.tile_start) + ((bmd, ws.tile_start_down) if bmd != bm else ())
+        ops.pack(ids, self.E, out=packed, workspace=ws.pack_ws, schedule=sched)
+        return bm
+
+    def _launch_resident_layer(self, x, packed, weights, out, ws, layer, bm, stream):
+        """Grouped SwiGLU over every expert of a fully resident layer and the
+        merge into `out`, on `stream`, on tile counts bounded without the
+        host counts (the schedule came out of the pack launch); records
+        _layer_done after them."""
+        T, k = weights.shape
+        bmd = L.down_block_m(bm, self.H, self.I)
+        slots_dev = self.executor.upload_table(layer, self.E, stream)
+        with torch.cuda.stream(stream):
+            L.grouped_ffn(x, packed, ws.sel_all, bm, (T * k + bm - 1) // bm + self.E, slots_dev, ws,
+                          max_tiles_down=(T * k + bmd - 1) // bmd + self.E, scheduled=True)
+            ops.merge(ws.y, packed.row_of, weights, out, mode=self.merge)
+        self._layer_done.record(stream)
 
     def _grouped(self, x, packed, sel_dev, rows, slots_dev, ws, perm=None):
         """One grouped SwiGLU launch over the experts in sel_dev, whose routed

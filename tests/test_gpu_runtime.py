@@ -334,6 +334,73 @@ def test_runtime_bound_decode_matches_the_single_launch_layer(orc):
         rt.close()
 
 
+def test_runtime_prelaunches_a_fully_resident_prefill_layer(orc):
+    """A prefill layer whose every expert has a ready copy is launched whole
+    before its counts come back and its demand is revealed while it runs
+    (decode_path 'prelaunched'): output and routing equal the resident layer
+    (layer.moe_forward) bit for bit, the oracle holds, the ledger closes,
+    and the prediction for the next layer is the router's.  A layer missing
+    one copy takes the grouped path instead."""
+    from pdscope_amd import layer, ops, synthetic
+    from pdscope_amd.cache import ExpertKey
+    from pdscope_amd.pdscope_runtime import PDScopeCudaRuntime
+    H, I, E, k = 256, 128, 32, 4
+    layers, masters = build(2, H, I, E, k, seed=83)
+    hot = [ExpertKey(l, e, "bf16") for l in range(2) for e in range(E)]
+    rt = PDScopeCudaRuntime(masters, hot_keys=hot, speculative_slots=0)
+    slots = [ops.slot_table([layers[l].experts[e] for e in range(E)], DEV) for l in range(2)]
+    ws = layer.MoEWorkspace(96, H, I, E, k, DEV)
+    try:
+        for i, T in enumerate((96, 17)):
+            x = synthetic.make_tokens(T, H, seed=84 + i)
+            for l in range(2):
+                out, routing, row = rt.forward(x, layers[l].gate, layer=l, step=0, request=f"p{i}", top_k=k,
+                                               next_gate=layers[1].gate if l == 0 else None)
+                assert row["decode_path"] == "prelaunched"
+                ref, _, ids, _ = layer.moe_forward(x, layers[l].gate, slots[l], ws, merge=rt.merge)
+                torch.cuda.synchronize()
+                assert torch.equal(out, ref) and torch.equal(routing.selected, ids.long()), (T, l)
+                check_output(orc, out, routing, x, layers[l], H, I, k)
+                if l == 0:
+                    _, nids, _ = layer.route(x, layers[1].gate, layer.MoEWorkspace(96, H, I, E, k, DEV))
+                    torch.cuda.synchronize()
+                    want = {}
+                    for e in nids.reshape(-1).tolist():
+                        want[e] = want.get(e, 0) + 1
+                    assert row["next_prediction_counts"] == want
+        closure(rt)
+    finally:
+        rt.close()
+    # the Qwen shape at T=512, bitwise against the resident layer
+    q = synthetic.QWEN
+    qlayers, qmasters = build(1, q["H"], q["I"], q["E"], q["k"], seed=85)
+    rt = PDScopeCudaRuntime(qmasters, hot_keys=[ExpertKey(0, e, "bf16") for e in range(q["E"])],
+                            speculative_slots=0)
+    try:
+        x = synthetic.make_tokens(512, q["H"], seed=86)
+        out, routing, row = rt.forward(x, qlayers[0].gate, layer=0, step=0)
+        qws = layer.MoEWorkspace(512, q["H"], q["I"], q["E"], q["k"], DEV)
+        qslots = ops.slot_table([qlayers[0].experts[e] for e in range(q["E"])], DEV)
+        ref, _, ids, _ = layer.moe_forward(x, qlayers[0].gate, qslots, qws, merge=rt.merge)
+        torch.cuda.synchronize()
+        assert row["decode_path"] == "prelaunched"
+        assert torch.equal(out, ref) and torch.equal(routing.selected, ids.long())
+        closure(rt)
+    finally:
+        rt.close()
+    # one expert without a copy: the grouped path after the reveal
+    rt = PDScopeCudaRuntime(masters, hot_keys=hot[:E - 1], speculative_slots=0, demand_slots=2)
+    try:
+        x = synthetic.make_tokens(96, H, seed=87)
+        out, routing, row = rt.forward(x, layers[0].gate, layer=0, step=0, top_k=k)
+        torch.cuda.synchronize()
+        assert row["decode_path"] == "grouped"
+        check_output(orc, out, routing, x, layers[0], H, I, k)
+        closure(rt)
+    finally:
+        rt.close()
+
+
 def test_runtime_raises_when_the_fused_decode_error_word_is_set():
     """The fused decode kernel sets a sticky error word when a bounded wait
     gives up.  Forced from the host here (the word is pre-set; the kernel only
@@ -501,6 +568,54 @@ def test_executor_accounts_an_enqueued_use_only_after_it_completed():
         pend = ex.gpu_group([key], None, wait_for=cur, completed=done)
         assert ex.computes and ex.finish_gpu(pend, wait=True) is None and not ex.computes
         cache.end_demand(DemandID("r", 0, 0))
+    finally:
+        ex.shutdown()
+
+
+def test_executor_holds_a_running_use_until_its_proof_completes():
+    """gpu_group(launch=None, running=proof) holds the copies of work that
+    may still run: finish_gpu(wait=False) leaves them held while the proof
+    reports the work running, finish_gpu(wait=True) waits through the
+    proof's synchronize() and then releases them; a call names exactly one
+    of completed= and running=, and the proof never joins the executor's
+    event pool."""
+    from pdscope_amd.cache import DemandID, ExpertCache, ExpertKey
+    from pdscope_amd.executor import ExpertExecutor
+    H, I, E, k = 256, 128, 32, 4
+    _, masters = build(1, H, I, E, k, seed=7)
+    sizes = {key: w.nbytes for key, w in masters.items()}
+    size = next(iter(sizes.values()))
+    cache = ExpertCache(sizes, 4 * size, [size, size])
+    ex = ExpertExecutor(cache, masters, 0)
+
+    class Proof:   # a completion proof the test flips by hand
+        def __init__(self):
+            self.done, self.waited = False, 0
+
+        def query(self):
+            return self.done
+
+        def synchronize(self):
+            self.waited += 1
+            self.done = True
+
+    try:
+        key = ExpertKey(0, 3, "bf16")
+        ident = DemandID("r", 0, 0)
+        cache.on_demand(ident, {key: 1})
+        assert ex.finish_load(ex.load(key), wait=True)
+        cur = torch.cuda.current_stream()
+        proof = Proof()
+        with pytest.raises(RuntimeError, match="exactly one"):
+            ex.gpu_group([key], None, wait_for=cur, completed=proof, running=proof)
+        assert not ex.computes
+        pend = ex.gpu_group([key], None, wait_for=cur, running=proof)
+        assert cache.lookup(key).state == "in_use"
+        assert ex.finish_gpu(pend) is None and ex.computes and cache.lookup(key).state == "in_use"
+        assert ex.finish_gpu(pend, wait=True) is None and not ex.computes
+        assert proof.waited == 1 and cache.lookup(key).state == "ready"
+        assert all(e is not proof for e in ex._free_events)
+        cache.end_demand(ident)
     finally:
         ex.shutdown()
 
