@@ -2,7 +2,8 @@
 """MoE-layer benchmark on one MI355X: Qwen3-30B-A3B-shaped layers, seeded random weights.
 
     python bench.py [--steps K] [--warmup W]
-                    [--workload prefill512|decode|prefill4096|prefill4096_zipf|dsv2_mixed|stack48|runtime_decode]
+                    [--workload prefill512|decode|prefill4096|prefill4096_zipf|dsv2_mixed|stack48|runtime_decode|
+                                runtime_prefill512]
 
 Inputs and weights are resident in HBM when timing starts.  A prefill step
 is one MoE layer forward over one batch of synthetic tokens: route (K1) ->
@@ -19,8 +20,8 @@ also carries the T = 512 prefill (uniform routing), the T = 4096 prefill on
 the Zipf(1.1)-biased routing with every expert resident (the grouped SwiGLU
 the T = 4096 target names; the uniform routing beside it), the T = 4096
 Zipf-skewed layer with 32 resident experts and 8 demand staging slots
-through the runtime, the runtime's T = 1 layer call with every expert
-resident (its host cost around the kernel), and the DeepSeek-V2-Lite
+through the runtime, the runtime's T = 1 and T = 512 layer calls with every
+expert resident (their host cost around the kernels), and the DeepSeek-V2-Lite
 mixed-batch results
 ("workloads"), each with its own roofline figure, and CPU baselines: the
 AVX2 bf16 SwiGLU expert kernel under oracle/ (a stand-in for ktransformers'
@@ -59,7 +60,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--workload", default="decode",
                     choices=["prefill512", "decode", "prefill4096", "prefill4096_zipf", "dsv2_mixed", "stack48",
-                             "runtime_decode"])
+                             "runtime_decode", "runtime_prefill512"])
     ap.add_argument("--no-extra", action="store_true",
                     help="only the main workload (for prefill4096: without the uniform-routing comparison)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -583,13 +584,16 @@ def run_stack(n_layers, device, seed0, T_prefill=2048, n_decode=64, cap_gib=24, 
                 setup_s=setup_s, tokens_prefill=T_prefill, decode_steps=n_decode, pcie=pcie, steps_run=n_decode)
 
 
-def run_runtime_decode(steps, warmup, n_layers, device, seed0):
-    """Decode through the drop-in runtime with every expert resident: one
-    token per PDScopeCudaRuntime.forward call, each layer replaying its
-    captured single-launch graph (with the next layer's prediction), the
-    routing read back for the ledger's reveal, acquire / release of the
-    routed experts and the trace row.  A step is one layer call, timed by
-    wall clock: the host cost of the runtime around the layer kernel."""
+def run_runtime_decode(steps, warmup, n_layers, device, seed0, T=1):
+    """Layer calls through the drop-in runtime with every expert resident.
+    T=1 (decode): one token per PDScopeCudaRuntime.forward call, each layer
+    served by its bound single-launch kernel (with the next layer's
+    prediction), the routing read back for the ledger's reveal, acquire /
+    release of the routed experts and the trace row.  T>1 (prefill, step 0
+    of a new request per pass): the whole resident layer launched before the
+    counts come back, the demand revealed while it runs.  A step is one
+    layer call, timed by wall clock: the host cost of the runtime around the
+    layer's kernels."""
     import torch
     from pdscope_amd import synthetic
     from pdscope_amd.cache import ExpertKey
@@ -605,11 +609,13 @@ def run_runtime_decode(steps, warmup, n_layers, device, seed0):
     torch.cuda.empty_cache()
     rt = PDScopeCudaRuntime(masters, hot_keys=hot, speculative_slots=0, demand_slots=8, resident_graphs=True,
                             device=device, diagnostics=False)
-    x = synthetic.make_tokens(1, H, seed=seed0 + 40999, device=device)
+    x = synthetic.make_tokens(T, H, seed=seed0 + 40999, device=device)
     try:
         def pass_(step):
             for l in range(n_layers):
-                rt.forward(x, gates[l], layer=l, step=step, request="runtime_decode", top_k=K_TOP,
+                # decode steps continue one request; a prefill is step 0 of a request of its own
+                rt.forward(x, gates[l], layer=l, step=step if T == 1 else 0,
+                           request="runtime_decode" if T == 1 else f"runtime_prefill_{step}", top_k=K_TOP,
                            next_gate=gates[l + 1] if l + 1 < n_layers else None)
         n_warm = max(1, -(-warmup // n_layers))
         n_timed = max(1, steps // n_layers)
@@ -625,10 +631,12 @@ def run_runtime_decode(steps, warmup, n_layers, device, seed0):
         rt.close()
     calls = n_timed * n_layers
     t = wall / calls
-    layer_bytes = K_TOP * EXPERT_BYTES + ROUTER_BYTES + 2 * H * 2
+    touched = min(E, T * K_TOP)
+    layer_bytes = touched * EXPERT_BYTES + ROUTER_BYTES + 2 * T * H * 2
     hbm = dict(bound="hbm", achieved=layer_bytes / t / 1e9, peak=HBM_PEAK_GBS, unit="GB/s")
     hbm["frac"] = hbm["achieved"] / hbm["peak"]
-    return dict(tok_s=1.0 / t, ms_per_step=t * 1e3, kernel="PDScopeCudaRuntime.forward, T=1, all experts resident",
+    return dict(tok_s=T / t, ms_per_step=t * 1e3,
+                kernel=f"PDScopeCudaRuntime.forward, T={T}, all experts resident",
                 kernel_ms_mean=t * 1e3, host_us_per_layer_call=t * 1e6, layers_rotated=n_layers, hbm=hbm,
                 steps_run=calls)
 
@@ -912,7 +920,7 @@ def main():
 
     plan = {"prefill512": ("prefill", 512, 4), "decode": ("decode", 1, 16), "prefill4096": ("prefill", 4096, 2),
             "prefill4096_zipf": ("zipf", 4096, 2), "dsv2_mixed": ("dsv2", 1304, 4), "stack48": ("stack", 2048, 48),
-            "runtime_decode": ("rtdecode", 1, 4)}
+            "runtime_decode": ("rtdecode", 1, 4), "runtime_prefill512": ("rtdecode", 512, 4)}
     # the 48-layer stack pins 58 GB of host masters: it runs only when asked for
     order = [args.workload] + ([] if args.no_extra else [w for w in plan if w not in (args.workload, "stack48")])
     records, raw = {}, {}
@@ -922,9 +930,11 @@ def main():
         # extra legs: enough warm-up for the weight pages of every layer copy
         # to be mapped, and steps enough for a stable mean (a few seconds each)
         steps = args.steps if main_leg else {"prefill512": 400, "decode": 500, "prefill4096": 200, "prefill4096_zipf": 20,
-                                                       "dsv2_mixed": 300, "runtime_decode": 800}[wl]
+                                                       "dsv2_mixed": 300, "runtime_decode": 800,
+                                                       "runtime_prefill512": 200}[wl]
         warmup = args.warmup if main_leg else {"prefill512": 100, "decode": 200, "prefill4096": 50, "prefill4096_zipf": 2,
-                                                        "dsv2_mixed": 50, "runtime_decode": 80}[wl]
+                                                        "dsv2_mixed": 50, "runtime_decode": 80,
+                                                        "runtime_prefill512": 20}[wl]
         if kind == "decode":
             steps = max(steps, 1)
         log(f"[bench] {wl}: T={T} layers={nl} steps={steps} warmup={warmup}")
@@ -955,7 +965,7 @@ def main():
             res = run_stack(nl, device, 20261011)
             rec = dict(res)
         elif kind == "rtdecode":
-            res = run_runtime_decode(steps, warmup, nl, device, 20261011)
+            res = run_runtime_decode(steps, warmup, nl, device, 20261011, T=T)
             rec = dict(res)
         else:
             res = run_decode(steps, warmup, nl, device, 20261011)
@@ -1018,6 +1028,9 @@ def main():
                                "T=4096 layer's routing), all 128 experts resident: the grouped SwiGLU",
                 "prefill4096_zipf": "Qwen3-30B-A3B-shaped MoE layer, prefill T=4096 with a Zipf(1.1) router bias, "
                                     "32 experts resident, the rest staged through 8 demand slots",
+                "runtime_prefill512": "Qwen3-30B-A3B-shaped MoE layers through PDScopeCudaRuntime.forward, prefill "
+                                      "T=512, all 128 experts resident (launched before the counts come back); a step "
+                                      "is one layer call (host cost of the runtime included)",
                 "runtime_decode": "Qwen3-30B-A3B-shaped MoE layers through PDScopeCudaRuntime.forward, decode T=1, "
                                   "all 128 experts resident, bound single-launch layer with next-layer prediction; a step is "
                                   "one layer call (host cost of the runtime included)",
