@@ -67,11 +67,12 @@ class FileCosts:
 
 
 class ResidentGraphCosts:
-    """A cost table seen by a runtime whose resident decode experts replay a
-    captured graph.  mode 'eager_bound' leaves every cost as measured eagerly
-    (the default: misses and speculative copies still run eagerly);
-    'measured' charges one-token GPU work at the calibrated replay cost and
-    keeps the staged path's total (copy + compute) unchanged."""
+    """A cost table seen by a runtime whose resident decode experts run a
+    cheaper resident launch (the reference's captured graphs; here the bound
+    single-launch layer).  mode 'eager_bound' leaves every cost as measured
+    eagerly (the default: misses and speculative copies still run eagerly);
+    'measured' charges one-token GPU work at the calibrated resident-launch
+    cost and keeps the staged path's total (copy + compute) unchanged."""
 
     MODES = ("eager_bound", "measured")
 
@@ -79,7 +80,7 @@ class ResidentGraphCosts:
         if mode not in self.MODES:
             raise ValueError(f"resident graph cost mode must be one of {self.MODES}")
         if not graph_gpu_ms > 0:
-            raise ValueError("a calibrated graph replay must take positive time")
+            raise ValueError("a calibrated resident launch must take positive time")
         self.base, self.graph_gpu_ms, self.mode = base, float(graph_gpu_ms), mode
         self.sources = list(getattr(base, "sources", []))
 
