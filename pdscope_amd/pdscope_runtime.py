@@ -43,6 +43,7 @@ the GPU.  There is no built-in CPU expert path.
 """
 from __future__ import annotations
 
+import collections
 import contextlib
 import ctypes
 import hashlib
@@ -67,6 +68,11 @@ _raw_current_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 # how long the host polls a bound launch's read-back word before it blocks on
 # an event instead (a decode layer takes tens of microseconds)
 _READBACK_POLL_S = 0.002
+
+# bound decode layers kept at once: every layer of a deep stack with a few
+# gate / predictor variants each; a caller that passes new gate tensors call
+# after call evicts the least recently used binding instead of growing
+_MAX_BINDINGS = 512
 
 
 class _HostWordTagged:
@@ -176,7 +182,9 @@ class PDScopeCudaRuntime:
         self.prediction_counts = {p: dict(hits=0, total=0) for p in ("prefill", "decode")}
         self._ws = {}
         self._pws = {}
-        self._bindings = {}     # bound decode launches, by (layer, k, normalize, gate, next gate)
+        # bound decode launches, by (layer, k, normalize, gate, next gate),
+        # least recently used first (a binding keeps its tensors alive)
+        self._bindings = collections.OrderedDict()
         self.bound_launches = 0  # tokens served through them (the reference counts its graph replays)
         self._out_ring = {}     # graph_output_pool: two output buffers per layer
         self._graph_turn = {}
@@ -964,7 +972,11 @@ class PDScopeCudaRuntime:
         # moved between calls) on the launch stream
         slots_dev = self.executor.upload_table(layer, self.E, cur)
         b = self._bindings.get(key)
-        if b is None:
+        if b is not None:
+            self._bindings.move_to_end(key)
+        else:
+            if len(self._bindings) >= _MAX_BINDINGS:
+                self._bindings.popitem(last=False)[1].close()
             b = ops.DecodeBinding(gate, slots_dev, self.I, k, normalize, host=self._pinned_counts,
                                   error_at=self._err_at, merge=self.merge, next_gate=next_gate)
             self._bindings[key] = b
