@@ -375,7 +375,7 @@ class ExpertExecutor:
         for ticket in retired:
             if ticket in self.loads:
                 raise RuntimeError("the ledger retired a copy with a transfer in flight")
-            flat = self.copies.pop(ticket, None)
+            self.copies.pop(ticket, None)
             ev = self._landed.pop(ticket, None)
             if ev is not None:
                 self._free_events.append(ev)

@@ -262,7 +262,7 @@ class StackSession:
         """Peak allocator bytes plus the device bytes in use outside the
         allocator must fit the budget (pdscope_compare.py:376-385).  On a
         one-GPU box the device's used bytes are this process's."""
-        dev, rt, b = self.device, self.runtime, self.budget
+        dev, b = self.device, self.budget
         free, total = torch.cuda.mem_get_info(dev)
         used = total - free
         reserved = torch.cuda.memory_reserved(dev)

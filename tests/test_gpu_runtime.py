@@ -212,7 +212,7 @@ def test_runtime_t4096_sampled_tokens(orc, case):
     from pdscope_amd import synthetic
     from pdscope_amd.cache import ExpertKey
     from pdscope_amd.pdscope_runtime import PDScopeCudaRuntime
-    from tests.gpu_helpers import MAX_REL, MEAN_ABS, err_metrics, ulp_diff_bf16
+    from tests.gpu_helpers import MAX_REL, MEAN_ABS, err_metrics
     q = synthetic.QWEN
     H, I, E, k, T = q["H"], q["I"], q["E"], q["k"], 4096
     layers, masters = build(1, H, I, E, k, seed=97)
