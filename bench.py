@@ -736,7 +736,7 @@ def host_cores():
 def cpu_threads(requested):
     """Worker threads of the CPU baseline: one per physical core of the
     process's CPUs, within one GPU's share of the box, minus one for the
-    control thread (README.md:142; docs/REPRODUCE.md:38-41 of the reference)."""
+    control thread (the reference's README.md:142 and docs/REPRODUCE.md:38-41)."""
     if requested > 0:
         return requested
     hc = host_cores()

@@ -44,7 +44,8 @@ def dispatch_via_reference_loader(tmp_path_factory):
     expertbench/native-build/layer-dispatch/pdscope_layer_dispatch*.so under
     the tree's root, then spec_from_file_location / module_from_spec /
     exec_module, then the submit_and_merge check.  The file is placed there
-    as a symlink to the package's build, as INTEGRATION.md describes."""
+    as a symlink to the package's build, which is how a user of the
+    reference installs it."""
     import importlib.util
     from pdscope_amd import build as B
     root = tmp_path_factory.mktemp("reference_tree")
