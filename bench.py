@@ -713,7 +713,7 @@ def run_dsv2_mixed(steps, warmup, n_layers, device, seed0):
 
 # ----------------------------------------------------------------------------- CPU baseline
 
-CPU_SHARE = 16   # host CPUs one GPU's work may occupy on the GPU box
+CPU_SHARE = 16   # host CPUs one GPU's work may occupy (a 128-CPU host with 8 GPUs)
 
 
 def host_cores():
@@ -735,7 +735,7 @@ def host_cores():
 
 def cpu_threads(requested):
     """Worker threads of the CPU baseline: one per physical core of the
-    process's CPUs, within one GPU's share of the box, minus one for the
+    process's CPUs, within one GPU's share of the host, minus one for the
     control thread (the reference's README.md:142 and docs/REPRODUCE.md:38-41)."""
     if requested > 0:
         return requested

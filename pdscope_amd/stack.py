@@ -260,8 +260,9 @@ class StackSession:
 
     def check_memory(self):
         """Peak allocator bytes plus the device bytes in use outside the
-        allocator must fit the budget (pdscope_compare.py:376-385).  On a
-        one-GPU box the device's used bytes are this process's."""
+        allocator must fit the budget (pdscope_compare.py:376-385).  The
+        device's used bytes are taken as this process's (one process per
+        device)."""
         dev, b = self.device, self.budget
         free, total = torch.cuda.mem_get_info(dev)
         used = total - free
