@@ -713,7 +713,7 @@ def run_dsv2_mixed(steps, warmup, n_layers, device, seed0):
 
 # ----------------------------------------------------------------------------- CPU baseline
 
-CPU_SHARE = 16   # host CPUs one GPU's work may occupy (a 128-CPU host with 8 GPUs)
+CPU_SHARE = 16   # host CPUs that one GPU's work may occupy
 
 
 def host_cores():
