@@ -334,6 +334,46 @@ def test_runtime_bound_decode_matches_the_single_launch_layer(orc):
         rt.close()
 
 
+def test_runtime_bound_decode_across_the_launch_number_wrap(orc):
+    """The bound launches are numbered 1 .. 32767 and the number wraps to 1:
+    calls on both sides of the wrap (routed ids, prediction and error word
+    all read back by their tags) still equal the single-launch layer and
+    predict what the router picks for the next layer."""
+    from pdscope_amd import layer, ops, synthetic
+    from pdscope_amd.cache import ExpertKey
+    from pdscope_amd.pdscope_runtime import PDScopeCudaRuntime
+    q = synthetic.QWEN
+    H, I, E, k = q["H"], q["I"], q["E"], q["k"]
+    layers, masters = build(2, H, I, E, k, seed=193)
+    hot = [ExpertKey(l, e, "bf16") for l in range(2) for e in range(E)]
+    rt = PDScopeCudaRuntime(masters, hot_keys=hot, speculative_slots=0, resident_graphs=True)
+    slots = ops.slot_table([layers[0].experts[e] for e in range(E)], DEV)
+    ws = layer.MoEWorkspace(1, H, I, E, k, DEV)
+    ws_pred = layer.MoEWorkspace(1, H, I, E, k, DEV)
+    try:
+        rt.forward(synthetic.make_tokens(4, H, seed=194), layers[0].gate, layer=0, step=0)
+        rt._seq = 0x7FFF - 2
+        seen = []
+        for step in range(1, 6):
+            x = synthetic.make_tokens(1, H, seed=194 + step)
+            out, routing, row = rt.forward(x, layers[0].gate, layer=0, step=step, next_gate=layers[1].gate)
+            seen.append(rt._seq)
+            assert row["decode_path"] == "bound_launch"
+            ref_out, logits, ids, w = layer.moe_forward(x, layers[0].gate, slots, ws, merge=rt.merge)
+            _, _, pred, _ = layer.moe_forward(x, layers[1].gate, slots, ws_pred, merge=rt.merge)
+            torch.cuda.synchronize()
+            assert torch.equal(out, ref_out) and torch.equal(routing.selected, ids.long())
+            assert torch.equal(routing.logits, logits) and torch.equal(routing.weights, w)
+            got = rt._pinned_np[k:2 * k].tolist()
+            assert sorted(v & 0xFFFF for v in got) == sorted(pred.view(-1).tolist())
+            assert all(v >> 16 == rt._seq for v in got)
+            check_output(orc, out, routing, x, layers[0], H, I, k)
+        assert seen == [0x7FFE, 0x7FFF, 1, 2, 3]
+        closure(rt)
+    finally:
+        rt.close()
+
+
 def test_runtime_prelaunches_a_fully_resident_prefill_layer(orc):
     """A prefill layer whose every expert has a ready copy is launched whole
     before its counts come back and its demand is revealed while it runs
