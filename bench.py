@@ -264,13 +264,19 @@ def run_prefill(T, steps, warmup, n_layers, device, seed0, bias=None):
         tiles[i] = ops.grouped_block_m(int(live.sum()) // int(live.numel()), int(live.max()))
     for i in range(warmup):
         step(i)
-    events = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(3)) for _ in range(steps)]
+    # the measured pass (no events: an event between launches costs the
+    # stream a few microseconds), then a pass with events around the two
+    # grouped launches of every step for their times
     torch.cuda.synchronize(device)
     t0 = time.perf_counter()
     for i in range(steps):
-        step(i, events[i])
+        step(i)
     torch.cuda.synchronize(device)
     wall = time.perf_counter() - t0
+    events = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(3)) for _ in range(steps)]
+    for i in range(steps):
+        step(i, events[i])
+    torch.cuda.synchronize(device)
     gateup_ms = [a.elapsed_time(b) for a, b, _ in events]
     down_ms = [b.elapsed_time(c) for _, b, c in events]
     grouped_ms = [g + d for g, d in zip(gateup_ms, down_ms)]
@@ -319,10 +325,12 @@ def run_decode(steps, warmup, n_layers, device, seed0):
     """All layer copies captured in ONE hipGraph (as a decode step over a stack
     of resident layers replays them).  A step is one replay: one token through
     the n_layers layers.  Exactly `steps` replays are timed after `warmup`
-    untimed ones, with a HIP event on the replay stream after each; the layer
-    time is the events' total over steps * n_layers launches, and both the
-    throughput and the roofline come from it.  The same is done for the
-    three-launch path (route + decode GEMV + down/merge) for reference."""
+    untimed ones between a HIP event on the replay stream before the first and
+    one after the last; the layer time is their span over steps * n_layers
+    launches, and both the throughput and the roofline come from it (the
+    spread over replays comes from a second pass with an event after each).
+    The same is done for the three-launch path (route + decode GEMV +
+    down/merge) for reference."""
     import torch
     from pdscope_amd import layer, ops, synthetic
     layers = build_layers(n_layers, device, seed0)
@@ -358,19 +366,27 @@ def run_decode(steps, warmup, n_layers, device, seed0):
                 raise AssertionError("decode graph replay differs from eager execution")
         for _ in range(nwarm):
             g.replay()
-        # exactly nsteps replays between two synchronisations; an event on the
-        # replay stream after each one
-        events = [torch.cuda.Event(enable_timing=True) for _ in range(nsteps + 1)]
+        # the measured pass: exactly nsteps replays between two
+        # synchronisations, a HIP event before the first and after the last
+        # (an event between replays costs the stream a few microseconds)
+        first, last = (torch.cuda.Event(enable_timing=True) for _ in range(2))
         torch.cuda.synchronize(device)
         t0 = time.perf_counter()
+        first.record(stream)
+        for r in range(nsteps):
+            g.replay()
+        last.record(stream)
+        torch.cuda.synchronize(device)
+        wall = time.perf_counter() - t0
+        # the spread over replays, from a second pass with an event after each
+        events = [torch.cuda.Event(enable_timing=True) for _ in range(nsteps + 1)]
         events[0].record(stream)
         for r in range(nsteps):
             g.replay()
             events[r + 1].record(stream)
         torch.cuda.synchronize(device)
-        wall = time.perf_counter() - t0
         replay_ms = [events[r].elapsed_time(events[r + 1]) for r in range(nsteps)]
-        return wall, replay_ms, events[0].elapsed_time(events[nsteps])
+        return wall, replay_ms, first.elapsed_time(last)
 
     fused = ops.decode_layer_supported(H, I, E, K_TOP, device)
     g = capture(True)
@@ -441,15 +457,17 @@ def run_decode_chain(layers, device, seed0, reps):
     hits = sum(len(set(bufs[l]["pred"].tolist()) & set(bufs[l + 1]["ids"][0].tolist())) for l in range(n - 1))
     for _ in range(5):
         g.replay()
-    events = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+    # timed as the plain decode step: HIP events before the first replay and
+    # after the last
+    first, last = (torch.cuda.Event(enable_timing=True) for _ in range(2))
     torch.cuda.synchronize(device)
-    events[0].record(stream)
+    first.record(stream)
     for k in range(reps):
         g.replay()
-        events[k + 1].record(stream)
+    last.record(stream)
     torch.cuda.synchronize(device)
-    layer_ms = [events[k].elapsed_time(events[k + 1]) / n for k in range(reps)]
-    return dict(layer_ms_median=statistics.median(layer_ms), predictor_hits=hits, predictor_total=K_TOP * (n - 1),
+    return dict(layer_ms_mean=first.elapsed_time(last) / (reps * n), predictor_hits=hits,
+                predictor_total=K_TOP * (n - 1),
                 what="residual sum + next-layer gate-fallback prediction fused into each layer's launch")
 
 
@@ -687,25 +705,36 @@ def run_dsv2_mixed(steps, warmup, n_layers, device, seed0):
         touched.append(int((ws.counts > 0).sum().item()))
     for i in range(warmup):
         step(i)
-    events = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    # the measured pass, HIP events before the first step and after the last
+    # (an event between steps costs the stream a few microseconds); then the
+    # spread over steps from a pass with an event after each
+    first, last = (torch.cuda.Event(enable_timing=True) for _ in range(2))
     torch.cuda.synchronize(device)
     t0 = time.perf_counter()
+    first.record(stream)
+    for i in range(steps):
+        step(i)
+    last.record(stream)
+    torch.cuda.synchronize(device)
+    wall = time.perf_counter() - t0
+    mean_ms = first.elapsed_time(last) / steps
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
     events[0].record(stream)
     for i in range(steps):
         step(i)
         events[i + 1].record(stream)
     torch.cuda.synchronize(device)
-    wall = time.perf_counter() - t0
     layer_ms = [events[i].elapsed_time(events[i + 1]) for i in range(steps)]
     mean_touched = sum(touched[i % n_layers] for i in range(steps)) / steps
     expert = 3 * Id * Hd * 2
     layer_bytes = mean_touched * expert + 3 * Is * Hd * 2 + Ed * Hd * 2 + 2 * T * Hd * 2
     layer_flops = 2.0 * T * kd * 3 * Id * Hd + 2.0 * T * 3 * Is * Hd + 2.0 * T * Ed * Hd
-    t = statistics.mean(layer_ms) / 1e3
+    t = mean_ms / 1e3
     hbm = dict(bound="hbm", achieved=layer_bytes / t / 1e9, peak=HBM_PEAK_GBS, unit="GB/s")
     hbm["frac"] = hbm["achieved"] / hbm["peak"]
-    return dict(tok_s=T * steps / wall, ms_per_step=wall / steps * 1e3, kernel="whole layer (events per step)",
-                kernel_ms_mean=statistics.mean(layer_ms), kernel_ms_median=statistics.median(layer_ms),
+    return dict(tok_s=T * steps / wall, ms_per_step=wall / steps * 1e3,
+                kernel="whole layer (events around the measured steps)",
+                kernel_ms_mean=mean_ms, kernel_ms_median=statistics.median(layer_ms),
                 experts_touched=mean_touched, tokens=T, layers_rotated=n_layers, hbm=hbm,
                 layer_tflops=layer_flops / t / 1e12, layer_bytes=layer_bytes,
                 shape=dict(hidden=Hd, experts=Ed, intermediate=Id, top_k=kd, shared_intermediate=Is))
