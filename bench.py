@@ -968,8 +968,8 @@ def main():
             steps = max(steps, 1)
         log(f"[bench] {wl}: T={T} layers={nl} steps={steps} warmup={warmup}")
         if kind == "prefill" and T == 4096:
-            # config 3's layers, tokens and Zipf(1.1) router bias with every
-            # expert resident: the grouped SwiGLU the T=4096 target names;
+            # the staged T=4096 layer's weights, tokens and Zipf(1.1) router bias with every
+            # expert resident: the grouped SwiGLU whose MFMA fraction the record reports;
             # the uniform routing of the same shape is recorded beside it
             bias, _ = synthetic.zipf_bias(E, 1.1, seed=20261011, device=device)
             res = run_prefill(T, steps, warmup, nl, device, 20261011 + 9000, bias=bias)

@@ -12,7 +12,7 @@
   (identity attention, residual and RMSNorm between blocks), with masters in
   pinned host memory, an HBM slot cap that forces demand misses through the
   8 staging slots, gate-fallback prefetch of the next layer and decode steps
-  replayed through the per-layer hipGraph: every layer of the prefill and of
+  served by each layer's bound single-launch decode: every layer of the prefill and of
   each decode step against the oracle given the runtime's routing.
 
 Routing is checked bit-exact against the oracle given the kernel's logits;
@@ -35,7 +35,7 @@ def _close(orc, got_u16, ref_u16, what):
     return m
 
 
-def test_config2_t512_uniform_every_token(orc):
+def test_prefill_t512_uniform_every_token(orc):
     from pdscope_amd import layer, ops, synthetic
     H, I, E, k, T = 2048, 768, 128, 8, 512
     lay = synthetic.make_layer(**synthetic.QWEN, device=DEV)
@@ -61,7 +61,7 @@ def test_config2_t512_uniform_every_token(orc):
     assert (d <= 1).all()
 
 
-def test_config5_dsv2_mixed_batch_1304_tokens(orc):
+def test_dsv2_mixed_batch_1304_tokens(orc):
     from pdscope_amd import layer, ops, synthetic
     cfg = dict(synthetic.DSV2)
     H, I, E, k, Is = cfg["H"], cfg["I"], cfg["E"], cfg["k"], cfg["shared_I"]
@@ -116,7 +116,7 @@ def _rms_residual(out, x, eps=1e-6):
     return (h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + eps)).to(torch.bfloat16)
 
 
-def test_config4_chained_stack_through_runtime(orc):
+def test_chained_stack_through_runtime(orc):
     from pdscope_amd import layer as LY
     from pdscope_amd import synthetic
     from pdscope_amd.cache import ExpertKey

@@ -35,7 +35,7 @@ def _host_bf16(t):
     return t.view(torch.int16).numpy().view(np.uint16)
 
 
-def test_config4_stack48_full_size_against_the_oracle(orc):
+def test_stack48_full_size_against_the_oracle(orc):
     from pdscope_amd import stack
     dev = torch.device("cuda", 0)
     print("stack48: building 48 layers and pinning 58 GB of masters", flush=True)
