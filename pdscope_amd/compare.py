@@ -260,7 +260,7 @@ def main(argv=None):
     ap.add_argument("--hot-per-layer", type=int, default=40)
     ap.add_argument("--speculative-slots", type=int, default=16)
     ap.add_argument("--demand-slots", type=int, default=8)
-    ap.add_argument("--graphs", action="store_true", help="resident decode graphs")
+    ap.add_argument("--graphs", action="store_true", help="resident_graphs: decode layers through their bound single launch")
     ap.add_argument("--merge", choices=["reference", "fused"], default="reference")
     ap.add_argument("--input-pregather", action="store_true")
     ap.add_argument("--graph-output-pool", action="store_true")

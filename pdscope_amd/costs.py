@@ -13,9 +13,9 @@ on its own, so a table may bend); outside the measured domain the table
 refuses to extrapolate.  ``costs/mi355x_cost_table.json`` is the table
 measured on MI355X by ``bench.py --calibrate-costs``.
 
-``ResidentGraphCosts`` wraps a table for a runtime that replays captured
-decode graphs of resident experts (the cost modes of
-expertbench/pdscope_runtime.py:40-59).
+``ResidentGraphCosts`` wraps a table for a runtime that serves resident
+decode layers through a cheaper resident launch (the reference's captured
+graphs; the cost modes of expertbench/pdscope_runtime.py:40-59).
 """
 from __future__ import annotations
 

@@ -721,7 +721,7 @@ class PDScopeCudaRuntime:
         add_in = None
         if cpu_rows or native_cpu:
             offs = packed.offsets.cpu().tolist() if T == 1 else offs
-        # a graph-served or prelaunched layer with no CPU rows has nothing
+        # a layer served by its bound launch or prelaunched, with no CPU rows, has nothing
         # left to enqueue here (its merge ran with the launch)
         finish_ctx = (contextlib.nullcontext() if (graph_path or prelaunch) and not cpu_rows and not native_cpu
                       else torch.cuda.stream(ex.compute_stream))

@@ -114,7 +114,7 @@ class StackBudget:
     GiB to device memory outside the allocator (pdscope_compare.py:178-179).
     Here that headroom is at least min_headroom and at least the memory
     already in use outside the allocator when the session starts plus
-    external_growth (code objects loaded and graphs instantiated later);
+    external_growth (code objects and runtime buffers loaded later);
     the expert slots get what the allocator cap leaves after the bytes
     already reserved and workspace_reserve for the layer workspaces."""
     device_total: int = 24 * GIB
