@@ -48,8 +48,10 @@ def logits_within_accumulation_error(kern, orc_exact, x_u16, gate_u16, bf16_to_f
     return ok, int((d > 0).sum())
 
 
-def oracle_layer_given_routing(orc, x_u16, ids, w_u16, experts_u16, H, I):
-    """Oracle expert path + merge for a given routing (ids int [T,k], weights bf16 bits)."""
+def oracle_layer_given_routing(orc, x_u16, ids, w_u16, experts_u16, H, I, merge="fused"):
+    """Oracle expert path + merge for a given routing (ids int [T,k], weights bf16 bits).
+    merge "fused" is the exactly rounded weighted sum, "reference" the
+    reference's bf16 index_add_ in ascending expert id."""
     E = experts_u16.shape[0]
     p = orc.pack(np.ascontiguousarray(ids, dtype=np.int32), E)
     xg = x_u16[p["perm_token"]]
@@ -60,7 +62,10 @@ def oracle_layer_given_routing(orc, x_u16, ids, w_u16, experts_u16, H, I):
         blk = experts_u16[e]
         y[a:b] = orc.expert_forward(xg[a:b], blk[:IH].reshape(I, H), blk[IH:2 * IH].reshape(I, H),
                                     blk[2 * IH:].reshape(H, I))
-    return orc.merge(y, p["row_of"], w_u16), y, p
+    if merge not in ("fused", "reference"):
+        raise ValueError(merge)
+    mrg = orc.merge if merge == "fused" else orc.merge_ordered
+    return mrg(y, p["row_of"], w_u16), y, p
 
 
 def oracle_tokens_given_routing(orc, x_u16, ids, w_u16, tokens, block_of, H, I, add_in=None, merge="fused"):

@@ -147,7 +147,8 @@ def test_chained_stack_through_runtime(orc):
             ids = routing.selected.cpu().numpy()
             oi, ow = orc.route_from_logits(u16(routing.logits), k, True)
             assert np.array_equal(ids, oi) and np.array_equal(u16(routing.weights), ow), f"layer {l} routing"
-            ref, _, _ = oracle_layer_given_routing(orc, u16(x), ids, u16(routing.weights), experts_host[l], H, I)
+            ref, _, _ = oracle_layer_given_routing(orc, u16(x), ids, u16(routing.weights), experts_host[l], H, I,
+                                                   merge=rt.merge)
             _close(orc, u16(out), ref, f"layer {l}")
 
         for step in range(decode_steps + 1):

@@ -75,7 +75,7 @@ def test_runtime_places_experts_on_the_cpu_backend(orc, tmp_path):
                 out, routing, row = rt.forward(x, layers[l].gate, layer=l, step=step,
                                                next_gate=layers[1].gate if l == 0 else None, top_k=k)
                 torch.cuda.synchronize()
-                check_output(orc, out, routing, x, layers[l], H, I, k)
+                check_output(orc, out, routing, x, layers[l], H, I, k, merge=rt.merge)
                 d = row["decision"]
                 assert row["scheduler"] == "cross_layer" and d["mode"] in (
                     "prefill", "a_load", "b_prefetch", "c_unload", "d_cross_layer")
@@ -109,7 +109,7 @@ def test_runtime_with_expensive_cpu_keeps_the_load_on_the_gpu(orc, tmp_path):
         x = torch.randn((32, H), generator=torch.Generator(device=DEV).manual_seed(6), device=DEV).to(torch.bfloat16)
         out, routing, row = rt.forward(x, layers[0].gate, layer=0, step=0, top_k=k)
         torch.cuda.synchronize()
-        check_output(orc, out, routing, x, layers[0], H, I, k)
+        check_output(orc, out, routing, x, layers[0], H, I, k, merge=rt.merge)
         d, counts = row["decision"], row["token_counts"]
         assert len(d["cpu_queue"]) <= 1 and backend.calls == len(d["cpu_queue"])
         if d["cpu_queue"]:
@@ -152,7 +152,8 @@ def test_checkpoint_masters_in_pinned_pool_drive_the_runtime(orc, tmp_path):
             assert np.array_equal(ids, oi) and np.array_equal(u16(routing.weights), ow)
             blocks = np.stack([u16(masters[ExpertKey(l, e, "bf16")].flat.view(torch.bfloat16)) for e in range(CE)])
             from tests.gpu_helpers import assert_layer_close, oracle_layer_given_routing
-            ref, _, _ = oracle_layer_given_routing(orc, u16(x), ids, u16(routing.weights), blocks, CH, CI)
+            ref, _, _ = oracle_layer_given_routing(orc, u16(x), ids, u16(routing.weights), blocks, CH, CI,
+                                                   merge=rt.merge)
             assert_layer_close(orc, out, ref)
         closure(rt)
     finally:
@@ -323,7 +324,7 @@ def test_runtime_input_pregather_gives_the_same_bits(orc):
         finally:
             rt.close()
     assert torch.equal(outs[0], outs[1])
-    check_output(orc, outs[1], routing, x, layers[0], H, I, k)
+    check_output(orc, outs[1], routing, x, layers[0], H, I, k, merge=rt.merge)
 
 
 def test_runtime_graph_output_pool_is_a_two_deep_ring(orc):
@@ -382,7 +383,7 @@ def test_runtime_planned_decode_takes_the_bound_launch_with_calibrated_costs(orc
             out, routing, row = rt.forward(x, layers[0].gate, layer=0, step=step, top_k=k)
             torch.cuda.synchronize()
             assert row["decision"]["cpu_queue"] == [] and row["decode_path"] == "bound_launch"
-            check_output(orc, out, routing, x, layers[0], H, I, k)
+            check_output(orc, out, routing, x, layers[0], H, I, k, merge=rt.merge)
         closure(rt)
     finally:
         rt.close()
@@ -408,7 +409,7 @@ def test_runtime_reference_merge_is_the_bf16_expert_order_sum(orc):
         y = u16(ws.y[:64 * k * H]).reshape(64 * k, H)
         p = orc.pack(routing.selected.cpu().numpy().astype(np.int32), E)
         assert np.array_equal(u16(out), orc.merge_ordered(y, p["row_of"], u16(routing.weights)))
-        check_output(orc, out, routing, x, layers[0], H, I, k)
+        check_output(orc, out, routing, x, layers[0], H, I, k, merge=rt.merge)
     finally:
         rt.close()
 

@@ -27,11 +27,19 @@ def build(n_layers, H, I, E, k, seed=77):
     return layers, masters
 
 
-def check_output(orc, out, routing, x, layer_obj, H, I, k, normalize=True, row=None):
+def check_output(orc, out, routing, x, layer_obj, H, I, k, normalize=True, row=None, merge=None):
+    """Routing bit-exact against the oracle given the logits, and the output
+    within tolerance of the oracle layer with the runtime's merge (taken from
+    the trace row when `merge` is not given)."""
+    if merge is None and row is not None:
+        merge = row["merge_mode"]
+    if merge is None:
+        raise ValueError("check_output needs the runtime's merge mode (merge= or row=)")
     ids = routing.selected.cpu().numpy()
     oi, ow = orc.route_from_logits(u16(routing.logits), k, normalize)
     assert np.array_equal(ids, oi) and np.array_equal(u16(routing.weights), ow)
-    ref, _, _ = oracle_layer_given_routing(orc, u16(x), ids, u16(routing.weights), u16(layer_obj.experts), H, I)
+    ref, _, _ = oracle_layer_given_routing(orc, u16(x), ids, u16(routing.weights), u16(layer_obj.experts), H, I,
+                                           merge=merge)
     try:
         assert_layer_close(orc, out, ref)
     except AssertionError as err:
@@ -133,7 +141,7 @@ def test_runtime_prefill_then_decode_with_staging_and_prefetch(orc):
                 out, routing, row = rt.forward(x, layers[l].gate, layer=l, step=step, next_gate=
                                                layers[l + 1].gate if l + 1 < 2 else None, top_k=k)
                 torch.cuda.synchronize()
-                check_output(orc, out, routing, x, layers[l], H, I, k)
+                check_output(orc, out, routing, x, layers[l], H, I, k, merge=rt.merge)
                 assert set(row["decision"]["gpu_resident_queue"]) | set(row["decision"]["on_demand_queue"]) == \
                     set(row["token_counts"])
                 x = torch.nn.functional.layer_norm((out.float() + x.float()), (H,)).to(torch.bfloat16)
@@ -322,7 +330,7 @@ def test_runtime_bound_decode_matches_the_single_launch_layer(orc):
             assert torch.equal(out, ref_out) and torch.equal(routing.selected, ids.long())
             assert torch.equal(routing.logits, logits) and torch.equal(routing.weights, w)
             assert routing.selected.dtype == torch.int64 and routing.selected.shape == (1, 8)
-            check_output(orc, out, routing, x, layers[0], q["H"], q["I"], 8)
+            check_output(orc, out, routing, x, layers[0], q["H"], q["I"], 8, merge=rt.merge)
             kept.append((out, routing, ref_out.clone(), logits.clone(), ids.long(), w.clone()))
         torch.cuda.synchronize()
         for out, routing, ref_out, logits, ids, w in kept:
@@ -367,7 +375,7 @@ def test_runtime_bound_decode_across_the_launch_number_wrap(orc):
             got = rt._pinned_np[k:2 * k].tolist()
             assert sorted(v & 0xFFFF for v in got) == sorted(pred.view(-1).tolist())
             assert all(v >> 16 == rt._seq for v in got)
-            check_output(orc, out, routing, x, layers[0], H, I, k)
+            check_output(orc, out, routing, x, layers[0], H, I, k, merge=rt.merge)
         assert seen == [0x7FFE, 0x7FFF, 1, 2, 3]
         closure(rt)
     finally:
@@ -400,7 +408,7 @@ def test_runtime_prelaunches_a_fully_resident_prefill_layer(orc):
                 ref, _, ids, _ = layer.moe_forward(x, layers[l].gate, slots[l], ws, merge=rt.merge)
                 torch.cuda.synchronize()
                 assert torch.equal(out, ref) and torch.equal(routing.selected, ids.long()), (T, l)
-                check_output(orc, out, routing, x, layers[l], H, I, k)
+                check_output(orc, out, routing, x, layers[l], H, I, k, merge=rt.merge)
                 if l == 0:
                     _, nids, _ = layer.route(x, layers[1].gate, layer.MoEWorkspace(96, H, I, E, k, DEV))
                     torch.cuda.synchronize()
@@ -435,7 +443,7 @@ def test_runtime_prelaunches_a_fully_resident_prefill_layer(orc):
         out, routing, row = rt.forward(x, layers[0].gate, layer=0, step=0, top_k=k)
         torch.cuda.synchronize()
         assert row["decode_path"] == "grouped"
-        check_output(orc, out, routing, x, layers[0], H, I, k)
+        check_output(orc, out, routing, x, layers[0], H, I, k, merge=rt.merge)
         closure(rt)
     finally:
         rt.close()
@@ -512,7 +520,7 @@ def test_runtime_partial_resident_bound_decode(orc):
                 torch.cuda.synchronize()
                 assert torch.equal(routing.selected, ids.long())
                 assert torch.equal(out, ref_out)
-                check_output(orc, out, routing, x, layers[l], q["H"], q["I"], 8)
+                check_output(orc, out, routing, x, layers[l], q["H"], q["I"], 8, merge=rt.merge)
                 if l == 0:
                     # the prediction the bound launch made equals the router on the next gate
                     nids = torch.empty((1, 8), dtype=torch.int32, device=DEV)
